@@ -1,0 +1,169 @@
+/*
+ * engine_hip.h -- C-ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * Drop-in replacement for Titan's engine-cuda paged-KV / paged-attention /
+ * flash-attention launchers (NVRTC + cuLaunchKernel) with offline-compiled
+ * gfx950 code objects loaded by hipModuleLoad and launched by
+ * hipModuleLaunchKernel.  Each entry point names the reference interface it
+ * replaces (paths relative to the reference root).
+ *
+ * Conventions (engine-cuda/src/{paged_kv,paged_attention}.rs):
+ *   - the caller owns every device buffer and passes (pointer, size in bytes);
+ *     sizes are validated exactly as the reference validates DeviceBuffer
+ *     sizes and a short buffer yields EH_INVALID_SIZE with expected/actual;
+ *   - launches are asynchronous on the caller's stream (hipStream_t, 0 = null
+ *     stream), never synchronise the host and never allocate device memory;
+ *   - an optional device `pos_ptr` (uint32) overrides the host position so a
+ *     captured graph can be replayed as the position advances;
+ *   - n_tokens == 0 is success;
+ *   - the failing call's detail is kept per thread (eh_last_error).
+ */
+#ifndef TITAN_ENGINE_HIP_H
+#define TITAN_ENGINE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct eh_context eh_context;
+typedef void* eh_stream; /* hipStream_t */
+
+/* One code per CudaError / KvCacheError variant
+ * (engine-cuda/src/error.rs:6-50, engine-kvcache/src/error.rs:4-16). */
+typedef enum eh_status {
+    EH_OK = 0,
+    EH_INVALID_SIZE = 1,   /* CudaError::InvalidSize{expected, actual} */
+    EH_KERNEL_LOAD = 2,    /* CudaError::KernelLoad(site, code) */
+    EH_KERNEL_LAUNCH = 3,  /* CudaError::KernelLaunch(site, code) */
+    EH_ALLOC_FAILED = 4,   /* CudaError::AllocFailed */
+    EH_STREAM_FAILED = 5,  /* CudaError::StreamFailed */
+    EH_MEMCPY_FAILED = 6,  /* CudaError::MemcpyFailed */
+    EH_EVENT_FAILED = 7,   /* CudaError::EventFailed */
+    EH_GRAPH_FAILED = 8,   /* CudaError::GraphFailed */
+    EH_DRIVER = 9,         /* CudaError::Driver (device selection etc.) */
+    EH_POOL_EXHAUSTED = 20,/* KvCacheError::PoolExhausted{blocks_used, blocks_total} */
+    EH_INVALID_ARGS = 21,  /* KvCacheError::InvalidArgs(msg) */
+    EH_UNSUPPORTED = 30    /* shape outside the compiled kernel set (no reference counterpart) */
+} eh_status;
+
+/* KvDataType (engine-cuda/src/paged_kv.rs:36-52) plus BF16 (extension). */
+typedef enum eh_kv_dtype { EH_KV_F32 = 0, EH_KV_F16 = 1, EH_KV_FP8 = 2, EH_KV_BF16 = 3 } eh_kv_dtype;
+
+/* PagedKvLayout (engine-cuda/src/paged_kv.rs:55-102), 64-bit fields. */
+typedef struct eh_kv_layout {
+    uint64_t n_blocks;
+    uint64_t block_tokens;
+    uint64_t row_len;    /* n_kv_heads * head_dim elements */
+    uint32_t data_type;  /* eh_kv_dtype */
+    uint32_t reserved;
+} eh_kv_layout;
+
+/* ---- context: PagedKvGpu::new / PagedAttention::new / FlashAttention2::new
+ *      (paged_kv.rs:122-196, paged_attention.rs:58-134, flash_attention.rs:44-93).
+ * Loads the gfx950 code objects from code_object_dir (NULL = the directory
+ * of this library) and allocates the split-K scratch once. */
+eh_status eh_create(int device, const char* code_object_dir, eh_context** out);
+/* Drop for all three (paged_kv.rs:478-491): unloads modules, frees scratch. */
+void eh_destroy(eh_context* ctx);
+/* Detail of this thread's last failure: expected/actual for InvalidSize and
+ * PoolExhausted (blocks_used/blocks_total), the site string, the HIP code. */
+eh_status eh_last_error(uint64_t* expected, uint64_t* actual, const char** site, int* hip_code);
+const char* eh_status_name(eh_status s);
+/* PagedKvLayout::{element_bytes, bytes_total} (paged_kv.rs:45-51, 94-96). */
+uint64_t eh_kv_element_bytes(uint32_t data_type);
+uint64_t eh_kv_layout_bytes_total(const eh_kv_layout* layout);
+
+/* ---- PagedKvGpu::append_kv / append_kv_with_pos_ptr (paged_kv.rs:200-327).
+ * keys/values: [n_tokens, row_len] in the pool's element type. */
+eh_status eh_append_kv(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                       void* pool, uint64_t pool_bytes, const void* keys, uint64_t keys_bytes,
+                       const void* values, uint64_t values_bytes, const uint32_t* block_table,
+                       uint64_t bt_bytes, uint64_t start_token, uint64_t n_tokens,
+                       const uint32_t* pos_ptr);
+
+/* ---- PagedKvGpu::read_keys / read_values (paged_kv.rs:331-470). */
+eh_status eh_gather_kv(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                       const void* pool, uint64_t pool_bytes, const uint32_t* block_table,
+                       uint64_t bt_bytes, void* out, uint64_t out_bytes, uint64_t start_token,
+                       uint64_t n_tokens, int is_value);
+
+/* ---- Batched append (extension of paged_kv.rs:200 for B sequences):
+ * token i of the ragged batch belongs to sequence b with
+ * cu_seqlens[b] <= i < cu_seqlens[b+1] and lands at logical position
+ * start_pos[b] + i - cu_seqlens[b] through block_tables + b*bt_stride.
+ * cu_seqlens [batch+1], start_pos [batch] and block_tables are device arrays. */
+eh_status eh_append_kv_batched(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                               void* pool, uint64_t pool_bytes, const void* keys,
+                               uint64_t keys_bytes, const void* values, uint64_t values_bytes,
+                               const uint32_t* block_tables, uint64_t bt_bytes, uint32_t bt_stride,
+                               const uint32_t* cu_seqlens, const uint32_t* start_pos,
+                               uint32_t batch, uint64_t total_tokens);
+
+/* ---- Page copies dst_ids[k] <- src_ids[k] (device arrays): copy-on-write
+ * of a shared tail page (the copy_block_gpu step sketched for
+ * CowBlockTable::perform_tail_cow, engine-kvcache/src/cow.rs:73-81) and
+ * gather-compaction of surviving pages.  Pairs with src == dst are skipped;
+ * destinations must not also be sources. */
+eh_status eh_copy_pages(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                        void* pool, uint64_t pool_bytes, const uint32_t* src_ids,
+                        const uint32_t* dst_ids, uint32_t n_pairs);
+
+/* ---- Block-table rewrite after compaction: e = remap[e] for e < n_remap. */
+eh_status eh_remap_block_tables(eh_context* ctx, eh_stream stream, uint32_t* block_tables,
+                                uint64_t n_entries, const uint32_t* remap, uint32_t n_remap);
+
+/* ---- Page reference counts (Arc::strong_count of SharedBlock, cow.rs:56-61,
+ * counted over device block tables): counts[p] = number of entries j <
+ * n_used[b] of rows b equal to p.  counts [n_blocks] is overwritten. */
+eh_status eh_page_refcounts(eh_context* ctx, eh_stream stream, const uint32_t* block_tables,
+                            uint32_t bt_stride, const uint32_t* n_used, uint32_t batch,
+                            uint32_t* counts, uint32_t n_blocks);
+
+/* ---- PagedAttention::launch / launch_with_pos_ptr (paged_attention.rs:143-345):
+ * single-pass decode for one sequence; q/out [n_head, head_dim] f32, pool in
+ * kv_dtype.  Validation follows paged_attention.rs:193-257. */
+eh_status eh_paged_attention(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                             const float* q, uint64_t q_bytes, const void* pool,
+                             uint64_t pool_bytes, const uint32_t* block_table, uint64_t bt_bytes,
+                             float* out, uint64_t out_bytes, uint64_t n_head, uint64_t n_head_kv,
+                             uint64_t head_dim, uint64_t block_tokens, uint64_t seq_tokens,
+                             uint64_t query_pos, int causal, const uint32_t* pos_ptr);
+
+/* ---- PagedAttention::launch_flash_decoding (paged_attention.rs:352-490):
+ * split-K decode using the context's scratch.  Unlike the reference, every
+ * token is attended (no 32-split cap) and the split count follows the
+ * device-side position when pos_ptr is given (grid sized from the block
+ * table's capacity).  Calls sharing one context must not overlap in time. */
+eh_status eh_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                            const float* q, uint64_t q_bytes, const void* pool,
+                            uint64_t pool_bytes, const uint32_t* block_table, uint64_t bt_bytes,
+                            float* out, uint64_t out_bytes, uint64_t n_head, uint64_t n_head_kv,
+                            uint64_t head_dim, uint64_t block_tokens, uint64_t seq_tokens,
+                            uint64_t query_pos, int causal, const uint32_t* pos_ptr);
+
+/* ---- Batched decode (extension: B sequences in one launch).
+ * eh_decode_plan picks tokens_per_split (0 = automatic) and the split
+ * bound for contexts up to max_ctx, and the workspace size the call needs. */
+eh_status eh_decode_plan(uint32_t batch, uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
+                         uint32_t max_ctx, uint32_t tokens_per_split_hint,
+                         uint32_t* tokens_per_split, uint32_t* max_splits,
+                         uint64_t* workspace_bytes);
+/* q/out [batch, n_head, head_dim] f32; block_tables [batch, bt_stride] u32;
+ * ctx_lens [batch] u32 = tokens each query attends (its own position + 1).
+ * workspace/tokens_per_split/max_splits from eh_decode_plan. */
+eh_status eh_paged_decode_batched(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                                  const float* q, uint64_t q_bytes, const void* pool,
+                                  uint64_t pool_bytes, const uint32_t* block_tables,
+                                  uint64_t bt_bytes, uint32_t bt_stride, const uint32_t* ctx_lens,
+                                  uint32_t batch, float* out, uint64_t out_bytes, uint32_t n_head,
+                                  uint32_t n_head_kv, uint32_t head_dim, uint32_t block_tokens,
+                                  uint32_t tokens_per_split, uint32_t max_splits, void* workspace,
+                                  uint64_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

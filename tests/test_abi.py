@@ -1,0 +1,165 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared symbol,
+the code objects hold every kernel the launcher names, host-only entry points
+behave, and the host bookkeeping equals the oracle's PagedKvCache bit for bit.
+No GPU compute is called."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import orc
+from titan_amd import _lib
+from titan_amd.errors import KvCacheError, check
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in ("engine_hip.h", "kv_host.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        names |= set(re.findall(r"\b(eh_\w+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    missing = [n for n in sorted(declared_symbols()) if not hasattr(L, n)]
+    assert not missing, missing
+    assert declared_symbols() == set(_lib.EXPORTED)
+
+
+def test_code_objects_contain_launched_kernels():
+    kv = open(os.path.join(_lib.LIB_DIR, "paged_kv.hsaco"), "rb").read()
+    for ch in (16, 8, 4, 2):
+        for k in ("eh_append_kv_c", "eh_gather_kv_c", "eh_copy_pages_c"):
+            assert f"{k}{ch}".encode() in kv
+    for k in ("eh_remap_block_tables", "eh_page_refcounts", "eh_fill_u32"):
+        assert k.encode() in kv
+    dec = open(os.path.join(_lib.LIB_DIR, "paged_decode.hsaco"), "rb").read()
+    assert b"eh_decode_merge" in dec
+    for dt in ("f32", "f16", "bf16"):
+        for hd in (4, 8, 16, 32, 64, 128, 256):
+            for g in (1, 2, 4, 6, 7, 8):
+                assert f"eh_decode_split_{dt}_hd{hd}_g{g}".encode() in dec
+
+
+def test_status_names_and_layout_bytes():
+    L = _lib.load()
+    assert L.eh_status_name(1) == b"InvalidSize" and L.eh_status_name(20) == b"PoolExhausted"
+    lay = _lib.eh_kv_layout(10, 16, 256, 1, 0)
+    assert L.eh_kv_layout_bytes_total(C.byref(lay)) == 10 * 16 * 2 * 256 * 2
+    assert [L.eh_kv_element_bytes(d) for d in range(4)] == [4, 2, 1, 2]
+
+
+def test_null_context_is_rejected_before_any_hip_call():
+    L = _lib.load()
+    lay = _lib.eh_kv_layout(1, 1, 1, 0, 0)
+    st = L.eh_append_kv(None, None, C.byref(lay), None, 0, None, 0, None, 0, None, 0, 0, 0, None)
+    assert st == 21
+
+
+def test_decode_plan():
+    L = _lib.load()
+    tps, ms, ws = C.c_uint32(), C.c_uint32(), C.c_uint64()
+    assert L.eh_decode_plan(32, 12, 2, 128, 4096, 256, C.byref(tps), C.byref(ms), C.byref(ws)) == 0
+    assert (tps.value, ms.value) == (256, 16)
+    assert ws.value == 32 * 12 * 16 * (128 + 2) * 4
+    assert L.eh_decode_plan(1, 12, 2, 128, 100, 256, C.byref(tps), C.byref(ms), C.byref(ws)) == 0
+    assert ms.value == 1 and ws.value == 0
+    assert L.eh_decode_plan(1, 12, 5, 128, 100, 0, C.byref(tps), C.byref(ms), C.byref(ws)) == 21
+
+
+class HostCache:
+    """Thin driver of the product's host bookkeeping through the C-ABI."""
+
+    def __init__(self, *cfg):
+        self.L = _lib.load()
+        h = C.c_void_p()
+        check(self.L.eh_kvcache_new(*cfg, 0, C.byref(h)), host=True)
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.eh_kvcache_destroy(self.h)
+
+    def table(self, s):
+        n = self.L.eh_kvcache_block_table(self.h, s, None, 0)
+        out = np.zeros(max(n, 1), np.uint32)
+        self.L.eh_kvcache_block_table(self.h, s, out.ctypes.data, n)
+        return out[:n].tolist()
+
+    def reserve(self, s, n):
+        st = C.c_uint64()
+        check(self.L.eh_kvcache_reserve(self.h, s, n, C.byref(st)), host=True)
+        return st.value
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((0, 16, 1, 1), "n_blocks must be non-zero"),
+    ((1, 0, 1, 1), "block_tokens must be non-zero"),
+    ((1, 1, 0, 1), "heads and head_dim must be non-zero"),
+])
+def test_host_cache_invalid_config(args, msg):
+    with pytest.raises(KvCacheError) as e:
+        HostCache(*args)
+    assert e.value.kind == "InvalidArgs" and e.value.msg == msg
+
+
+def test_host_bookkeeping_matches_oracle_random_schedule():
+    """Random interleaving of new/append/free on both implementations: block
+    tables, counts, usage and exhaustion points agree exactly."""
+    rng = np.random.default_rng(1234)
+    nb, bt = 37, 5
+    o = orc.Cache(nb, bt, 1, 2)
+    order = rng.permutation(nb)
+    o.seed_free_list(order)
+    p = HostCache(nb, bt, 1, 2)
+    check(p.L.eh_kvcache_seed_free_list(p.h, order.astype(np.uint32).ctypes.data, nb), host=True)
+    seqs = []
+    row = np.zeros(2, np.float32)
+    for it in range(3000):
+        r = rng.random()
+        if r < 0.05 or not seqs:
+            seqs.append(o.new_sequence())
+            assert p.L.eh_kvcache_new_sequence(p.h) == seqs[-1]
+        elif r < 0.1:
+            s = int(rng.choice(seqs))
+            o.free_sequence(s)
+            p.L.eh_kvcache_free_sequence(p.h, s)
+        else:
+            s = int(rng.choice(seqs))
+            err_o = err_p = None
+            try:
+                o.append(s, row, row)
+            except orc.KvCacheError as e:
+                err_o = (e.kind, e.blocks_used, e.blocks_total)
+            try:
+                p.reserve(s, 1)
+            except KvCacheError as e:
+                err_p = (e.kind, e.blocks_used, e.blocks_total)
+            assert err_o == err_p
+        assert o.blocks_used() == p.L.eh_kvcache_blocks_used(p.h)
+    for s in seqs:
+        assert o.seq_block_table(s).tolist() == p.table(s)
+        assert o.token_count(s) == p.L.eh_kvcache_token_count(p.h, s)
+
+
+def test_host_reserve_many_equals_repeated_single():
+    o = orc.Cache(50, 4, 1, 2)
+    p = HostCache(50, 4, 1, 2)
+    s = o.new_sequence()
+    p.L.eh_kvcache_new_sequence(p.h)
+    row = np.zeros(2, np.float32)
+    for n in (3, 1, 9, 4, 0, 17):
+        for _ in range(n):
+            o.append(s, row, row)
+        p.reserve(s, n)
+        assert o.seq_block_table(s).tolist() == p.table(s)
+    # all-or-nothing exhaustion
+    with pytest.raises(KvCacheError) as e:
+        p.reserve(s, 1000)
+    assert e.value.kind == "PoolExhausted"
+    assert p.table(s) == o.seq_block_table(s).tolist()

@@ -1,0 +1,608 @@
+// engine_hip.cpp -- C-ABI launcher for the gfx950 paged KV-cache kernels.
+//
+// Replaces engine-cuda's NVRTC compile + cuModuleLoadData + cuLaunchKernel
+// (engine-cuda/src/paged_kv.rs:122-196, paged_attention.rs:58-134) with
+// hipModuleLoad of offline code objects and hipModuleLaunchKernel.  Sizes
+// are validated the way the reference validates DeviceBuffer sizes before
+// anything is launched; launches never allocate and never synchronise.
+
+#include "../../include/engine_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <dlfcn.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+struct eh_context {
+    int device = 0;
+    hipModule_t mod_kv = nullptr;
+    hipModule_t mod_decode = nullptr;
+    std::mutex mu;
+    std::unordered_map<std::string, hipFunction_t> fns;
+    // Split-K scratch for eh_flash_decoding, allocated once at creation
+    // (the reference does the same at paged_attention.rs:111-123).
+    float* scratch = nullptr;
+    uint64_t scratch_floats = 0;
+};
+
+namespace {
+
+struct err_state {
+    uint64_t expected = 0, actual = 0;
+    const char* site = "";
+    int hip = 0;
+};
+thread_local err_state g_err;
+
+eh_status fail(eh_status s, const char* site, uint64_t expected = 0, uint64_t actual = 0,
+               int hip = 0) {
+    g_err.expected = expected;
+    g_err.actual = actual;
+    g_err.site = site;
+    g_err.hip = hip;
+    return s;
+}
+
+eh_status invalid_size(uint64_t expected, uint64_t actual, const char* site = "InvalidSize") {
+    return fail(EH_INVALID_SIZE, site, expected, actual);
+}
+
+// Scratch capacity of eh_flash_decoding: 64 q heads x 256 splits x 256 dims.
+constexpr uint64_t kScratchFloats = 64ull * 256 * (256 + 2);
+
+eh_status bind(eh_context* c) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur != c->device) {
+        hipError_t e = hipSetDevice(c->device);
+        if (e != hipSuccess) return fail(EH_DRIVER, "hipSetDevice", 0, 0, (int)e);
+    }
+    return EH_OK;
+}
+
+eh_status get_fn(eh_context* c, hipModule_t mod, const char* name, hipFunction_t* f) {
+    std::lock_guard<std::mutex> lk(c->mu);
+    auto it = c->fns.find(name);
+    if (it != c->fns.end()) { *f = it->second; return EH_OK; }
+    hipFunction_t fn = nullptr;
+    hipError_t e = hipModuleGetFunction(&fn, mod, name);
+    if (e != hipSuccess || !fn) return fail(EH_KERNEL_LOAD, "hipModuleGetFunction", 0, 0, (int)e);
+    c->fns.emplace(name, fn);
+    *f = fn;
+    return EH_OK;
+}
+
+template <typename... A>
+eh_status launch(eh_context* c, hipModule_t mod, const char* name, dim3 grid, dim3 block,
+                 eh_stream stream, A... a) {
+    hipFunction_t f = nullptr;
+    eh_status st = get_fn(c, mod, name, &f);
+    if (st != EH_OK) return st;
+    void* argv[] = {static_cast<void*>(&a)...};
+    hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
+                                         (hipStream_t)stream, argv, nullptr);
+    if (e != hipSuccess) return fail(EH_KERNEL_LAUNCH, "hipModuleLaunchKernel", 0, 0, (int)e);
+    return EH_OK;
+}
+
+uint64_t elt_bytes(uint32_t dt) {
+    switch (dt) {
+        case EH_KV_F32: return 4;
+        case EH_KV_F16: return 2;
+        case EH_KV_BF16: return 2;
+        case EH_KV_FP8: return 1;
+        default: return 0;
+    }
+}
+
+uint64_t div_ceil(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// Largest copy chunk (16/8/4/2 bytes) dividing the row size and every base.
+int pick_chunk(uint64_t row_bytes, std::initializer_list<const void*> ptrs) {
+    for (int ch : {16, 8, 4, 2}) {
+        bool ok = row_bytes % ch == 0;
+        for (const void* p : ptrs) ok = ok && ((uintptr_t)p % ch == 0);
+        if (ok) return ch;
+    }
+    return 0;
+}
+
+uint32_t grid_for(uint64_t work, uint32_t per_block, uint32_t cap = 16384) {
+    uint64_t g = div_ceil(work, per_block);
+    if (g < 1) g = 1;
+    return (uint32_t)(g > cap ? cap : g);
+}
+
+const char* dt_name(uint32_t dt) {
+    switch (dt) {
+        case EH_KV_F32: return "f32";
+        case EH_KV_F16: return "f16";
+        case EH_KV_BF16: return "bf16";
+        default: return nullptr;
+    }
+}
+
+bool supported_hd(uint64_t hd) {
+    return hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
+}
+
+// Smallest compiled head-group width covering min(group, 8).
+uint32_t pick_g(uint32_t group) {
+    const uint32_t want = group < 8 ? group : 8;
+    for (uint32_t g : {1u, 2u, 4u, 6u, 7u, 8u})
+        if (g >= want) return g;
+    return 8;
+}
+
+int log2_exact(uint64_t v) {
+    if (v == 0 || (v & (v - 1))) return -1;
+    int s = 0;
+    while ((1ull << s) < v) ++s;
+    return s;
+}
+
+struct decode_args {
+    uint32_t kv_dtype;
+    const float* q;
+    const void* pool;
+    uint64_t n_blocks;
+    const uint32_t* bt;
+    uint32_t bt_stride;
+    const uint32_t* lens_ptr;
+    uint32_t lens_mode, seq_tokens, query_pos, causal;
+    uint32_t batch;
+    float* out;
+    uint32_t n_head, n_head_kv, head_dim, block_tokens;
+    uint32_t tps, max_splits;
+    float* part_acc;
+    float* part_ml;
+};
+
+eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
+    const char* dn = dt_name(a.kv_dtype);
+    if (!dn) return fail(EH_UNSUPPORTED, "kv_dtype");
+    if (!supported_hd(a.head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, a.head_dim);
+    const uint32_t group = a.n_head / a.n_head_kv;
+    const uint32_t g = pick_g(group);
+    const uint32_t chunks = (group + g - 1) / g;
+    char name[64];
+    std::snprintf(name, sizeof name, "eh_decode_split_%s_hd%u_g%u", dn, a.head_dim, g);
+    const float scale = 1.0f / std::sqrt((float)a.head_dim);  // paged_attention.rs:286
+    const float scale_log2 = scale * 1.4426950408889634f;
+    const int bt_shift = log2_exact(a.block_tokens);
+    eh_status st = launch(c, c->mod_decode, name, dim3(a.max_splits, a.n_head_kv * chunks, a.batch),
+                          dim3(256), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
+                          a.lens_ptr, a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.out,
+                          a.part_acc, a.part_ml, a.n_head, a.n_head_kv, a.block_tokens, bt_shift,
+                          a.tps, a.max_splits, scale_log2, a.n_blocks);
+    if (st != EH_OK || a.max_splits <= 1) return st;
+    return launch(c, c->mod_decode, "eh_decode_merge", dim3(a.n_head, a.batch), dim3(64), stream,
+                  (const float*)a.part_acc, (const float*)a.part_ml, a.out, a.lens_ptr,
+                  a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.n_head, a.head_dim, a.tps,
+                  a.max_splits);
+}
+
+// Splits: aim for enough workgroups to fill 256 CUs several times over.
+uint32_t auto_tps(uint64_t batch, uint64_t n_kv, uint64_t chunks, uint64_t max_ctx) {
+    const uint64_t target_wgs = 2048;
+    uint64_t tps = div_ceil(batch * n_kv * chunks * (max_ctx ? max_ctx : 1), target_wgs);
+    tps = div_ceil(tps, 64) * 64;
+    if (tps < 64) tps = 64;
+    if (tps > (1u << 30)) tps = 1u << 30;
+    return (uint32_t)tps;
+}
+
+// Checks shared by the single-sequence attention entry points
+// (paged_attention.rs:193-257), in the reference's order.
+eh_status validate_attention(uint32_t kv_dtype, uint64_t q_bytes, uint64_t pool_bytes,
+                             uint64_t bt_bytes, uint64_t out_bytes, uint64_t n_head,
+                             uint64_t n_head_kv, uint64_t head_dim, uint64_t block_tokens,
+                             uint64_t seq_tokens, uint64_t query_pos) {
+    if (n_head < 1) return invalid_size(1, n_head);
+    if (n_head_kv < 1) return invalid_size(1, n_head_kv);
+    if (n_head % n_head_kv != 0) return invalid_size(n_head_kv, n_head % n_head_kv);
+    if (head_dim < 1) return invalid_size(1, head_dim);
+    if (block_tokens < 1) return invalid_size(1, block_tokens);
+    if (seq_tokens < 1) return invalid_size(1, seq_tokens);
+    const uint64_t q_expected = n_head * head_dim * 4;
+    if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+    if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+    if (pool_bytes < 4) return invalid_size(4, pool_bytes);
+    const uint64_t bt_expected = div_ceil(seq_tokens, block_tokens) * 4;
+    if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes);
+    const uint64_t imax = 0x7FFFFFFFull;
+    for (uint64_t v : {n_head, n_head_kv, head_dim, block_tokens, seq_tokens, query_pos})
+        if (v > imax) return invalid_size(imax, v);
+    if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
+    if (!supported_hd(head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, head_dim);
+    return EH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* eh_status_name(eh_status s) {
+    switch (s) {
+        case EH_OK: return "Ok";
+        case EH_INVALID_SIZE: return "InvalidSize";
+        case EH_KERNEL_LOAD: return "KernelLoad";
+        case EH_KERNEL_LAUNCH: return "KernelLaunch";
+        case EH_ALLOC_FAILED: return "AllocFailed";
+        case EH_STREAM_FAILED: return "StreamFailed";
+        case EH_MEMCPY_FAILED: return "MemcpyFailed";
+        case EH_EVENT_FAILED: return "EventFailed";
+        case EH_GRAPH_FAILED: return "GraphFailed";
+        case EH_DRIVER: return "Driver";
+        case EH_POOL_EXHAUSTED: return "PoolExhausted";
+        case EH_INVALID_ARGS: return "InvalidArgs";
+        case EH_UNSUPPORTED: return "Unsupported";
+    }
+    return "Unknown";
+}
+
+eh_status eh_last_error(uint64_t* expected, uint64_t* actual, const char** site, int* hip_code) {
+    if (expected) *expected = g_err.expected;
+    if (actual) *actual = g_err.actual;
+    if (site) *site = g_err.site;
+    if (hip_code) *hip_code = g_err.hip;
+    return EH_OK;
+}
+
+uint64_t eh_kv_element_bytes(uint32_t data_type) { return elt_bytes(data_type); }
+
+uint64_t eh_kv_layout_bytes_total(const eh_kv_layout* l) {
+    return l->n_blocks * l->block_tokens * 2 * l->row_len * elt_bytes(l->data_type);
+}
+
+eh_status eh_create(int device, const char* code_object_dir, eh_context** out) {
+    if (!out) return fail(EH_INVALID_ARGS, "out is null");
+    *out = nullptr;
+    std::string dir;
+    if (code_object_dir && *code_object_dir) {
+        dir = code_object_dir;
+    } else {
+        Dl_info info;
+        if (dladdr((void*)&eh_create, &info) && info.dli_fname) {
+            dir = info.dli_fname;
+            size_t slash = dir.rfind('/');
+            dir = slash == std::string::npos ? "." : dir.substr(0, slash);
+        } else {
+            dir = ".";
+        }
+    }
+    eh_context* c = new eh_context();
+    c->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) { delete c; return fail(EH_DRIVER, "hipSetDevice", 0, 0, (int)e); }
+    const std::string kv = dir + "/paged_kv.hsaco", dec = dir + "/paged_decode.hsaco";
+    e = hipModuleLoad(&c->mod_kv, kv.c_str());
+    if (e != hipSuccess) { delete c; return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_kv)", 0, 0, (int)e); }
+    e = hipModuleLoad(&c->mod_decode, dec.c_str());
+    if (e != hipSuccess) {
+        hipModuleUnload(c->mod_kv);
+        delete c;
+        return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_decode)", 0, 0, (int)e);
+    }
+    e = hipMalloc((void**)&c->scratch, kScratchFloats * sizeof(float));
+    if (e != hipSuccess) {
+        hipModuleUnload(c->mod_kv);
+        hipModuleUnload(c->mod_decode);
+        delete c;
+        return fail(EH_ALLOC_FAILED, "hipMalloc(split-K scratch)", 0, 0, (int)e);
+    }
+    c->scratch_floats = kScratchFloats;
+    *out = c;
+    return EH_OK;
+}
+
+void eh_destroy(eh_context* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->scratch) hipFree(c->scratch);
+    if (c->mod_kv) hipModuleUnload(c->mod_kv);
+    if (c->mod_decode) hipModuleUnload(c->mod_decode);
+    delete c;
+}
+
+eh_status eh_append_kv(eh_context* c, eh_stream stream, const eh_kv_layout* l, void* pool,
+                       uint64_t pool_bytes, const void* keys, uint64_t keys_bytes,
+                       const void* values, uint64_t values_bytes, const uint32_t* bt,
+                       uint64_t bt_bytes, uint64_t start_token, uint64_t n_tokens,
+                       const uint32_t* pos_ptr) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    const uint64_t elt = elt_bytes(l->data_type);
+    if (!elt) return fail(EH_UNSUPPORTED, "data_type");
+    // paged_kv.rs:240-267 (element size taken from the layout, not fixed at 4).
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    const uint64_t kv_expected = n_tokens * l->row_len * elt;
+    if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
+    if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
+    if (bt_bytes == 0) return invalid_size(4, 0);
+    if (n_tokens == 0) return EH_OK;
+    // Added check: the table must cover start+n tokens when the host knows start.
+    if (!pos_ptr) {
+        const uint64_t need = div_ceil(start_token + n_tokens, l->block_tokens) * 4;
+        if (bt_bytes < need) return invalid_size(need, bt_bytes, "block_table");
+    }
+    const uint64_t row_bytes = l->row_len * elt;
+    const int ch = pick_chunk(row_bytes, {pool, keys, values});
+    if (!ch) return fail(EH_UNSUPPORTED, "row alignment", 2, row_bytes);
+    const uint64_t total = n_tokens * 2 * (row_bytes / ch);
+    if (total >= (1ull << 31) || start_token + n_tokens >= (1ull << 32) || l->block_tokens >= (1ull << 32))
+        return invalid_size((1ull << 31) - 1, total, "append too large");
+    eh_status st = bind(c);
+    if (st) return st;
+    char name[32];
+    std::snprintf(name, sizeof name, "eh_append_kv_c%d", ch);
+    return launch(c, c->mod_kv, name, dim3(grid_for(total, 256)), dim3(256), stream,
+                  (const uint8_t*)keys, (const uint8_t*)values, bt,
+                  (uint32_t)std::min<uint64_t>(bt_bytes / 4, 0xFFFFFFFFull), (uint8_t*)pool,
+                  (uint32_t)n_tokens, (uint32_t)start_token, pos_ptr, (const uint32_t*)nullptr,
+                  (const uint32_t*)nullptr, (uint32_t)1, (uint32_t)row_bytes,
+                  (uint32_t)l->block_tokens, (uint64_t)l->n_blocks);
+}
+
+eh_status eh_gather_kv(eh_context* c, eh_stream stream, const eh_kv_layout* l, const void* pool,
+                       uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes, void* out,
+                       uint64_t out_bytes, uint64_t start_token, uint64_t n_tokens, int is_value) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    const uint64_t elt = elt_bytes(l->data_type);
+    if (!elt) return fail(EH_UNSUPPORTED, "data_type");
+    // paged_kv.rs:391-416
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    const uint64_t out_expected = n_tokens * l->row_len * elt;
+    if (out_bytes < out_expected) return invalid_size(out_expected, out_bytes);
+    if (bt_bytes == 0) return invalid_size(4, 0);
+    if (n_tokens == 0) return EH_OK;
+    const uint64_t need = div_ceil(start_token + n_tokens, l->block_tokens) * 4;
+    if (bt_bytes < need) return invalid_size(need, bt_bytes, "block_table");
+    const uint64_t row_bytes = l->row_len * elt;
+    const int ch = pick_chunk(row_bytes, {pool, out});
+    if (!ch) return fail(EH_UNSUPPORTED, "row alignment", 2, row_bytes);
+    const uint64_t total = n_tokens * (row_bytes / ch);
+    if (total >= (1ull << 31) || start_token + n_tokens >= (1ull << 32))
+        return invalid_size((1ull << 31) - 1, total, "gather too large");
+    eh_status st = bind(c);
+    if (st) return st;
+    char name[32];
+    std::snprintf(name, sizeof name, "eh_gather_kv_c%d", ch);
+    return launch(c, c->mod_kv, name, dim3(grid_for(total, 256)), dim3(256), stream,
+                  (const uint8_t*)pool, bt, (uint32_t)std::min<uint64_t>(bt_bytes / 4, 0xFFFFFFFFull),
+                  (uint8_t*)out, (uint32_t)n_tokens, (uint32_t)start_token, (uint32_t)(is_value != 0),
+                  (uint32_t)row_bytes, (uint32_t)l->block_tokens, (uint64_t)l->n_blocks);
+}
+
+eh_status eh_append_kv_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l, void* pool,
+                               uint64_t pool_bytes, const void* keys, uint64_t keys_bytes,
+                               const void* values, uint64_t values_bytes, const uint32_t* bt,
+                               uint64_t bt_bytes, uint32_t bt_stride, const uint32_t* cu_seqlens,
+                               const uint32_t* start_pos, uint32_t batch, uint64_t total_tokens) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    const uint64_t elt = elt_bytes(l->data_type);
+    if (!elt) return fail(EH_UNSUPPORTED, "data_type");
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    const uint64_t kv_expected = total_tokens * l->row_len * elt;
+    if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
+    if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
+    if (total_tokens == 0 || batch == 0) return EH_OK;
+    if (!cu_seqlens || !start_pos) return fail(EH_INVALID_ARGS, "cu_seqlens/start_pos are null");
+    if (bt_stride == 0) return invalid_size(1, 0, "bt_stride");
+    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
+    const uint64_t row_bytes = l->row_len * elt;
+    const int ch = pick_chunk(row_bytes, {pool, keys, values});
+    if (!ch) return fail(EH_UNSUPPORTED, "row alignment", 2, row_bytes);
+    const uint64_t total = total_tokens * 2 * (row_bytes / ch);
+    if (total >= (1ull << 31)) return invalid_size((1ull << 31) - 1, total, "append too large");
+    eh_status st = bind(c);
+    if (st) return st;
+    char name[32];
+    std::snprintf(name, sizeof name, "eh_append_kv_c%d", ch);
+    return launch(c, c->mod_kv, name, dim3(grid_for(total, 256)), dim3(256), stream,
+                  (const uint8_t*)keys, (const uint8_t*)values, bt, bt_stride, (uint8_t*)pool,
+                  (uint32_t)total_tokens, (uint32_t)0, (const uint32_t*)nullptr, cu_seqlens,
+                  start_pos, batch, (uint32_t)row_bytes, (uint32_t)l->block_tokens,
+                  (uint64_t)l->n_blocks);
+}
+
+eh_status eh_copy_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l, void* pool,
+                        uint64_t pool_bytes, const uint32_t* src_ids, const uint32_t* dst_ids,
+                        uint32_t n_pairs) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    const uint64_t elt = elt_bytes(l->data_type);
+    if (!elt) return fail(EH_UNSUPPORTED, "data_type");
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    if (n_pairs == 0) return EH_OK;
+    if (!src_ids || !dst_ids) return fail(EH_INVALID_ARGS, "page id arrays are null");
+    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    const int ch = pick_chunk(page_bytes, {pool});
+    if (!ch) return fail(EH_UNSUPPORTED, "page alignment", 2, page_bytes);
+    eh_status st = bind(c);
+    if (st) return st;
+    char name[32];
+    std::snprintf(name, sizeof name, "eh_copy_pages_c%d", ch);
+    return launch(c, c->mod_kv, name, dim3(std::min<uint32_t>(n_pairs, 65535)), dim3(256), stream,
+                  (uint8_t*)pool, src_ids, dst_ids, n_pairs, page_bytes, (uint64_t)l->n_blocks);
+}
+
+eh_status eh_remap_block_tables(eh_context* c, eh_stream stream, uint32_t* bt, uint64_t n_entries,
+                                const uint32_t* remap, uint32_t n_remap) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (n_entries == 0) return EH_OK;
+    if (!bt || !remap) return fail(EH_INVALID_ARGS, "null block table or remap");
+    eh_status st = bind(c);
+    if (st) return st;
+    return launch(c, c->mod_kv, "eh_remap_block_tables", dim3(grid_for(n_entries, 256)), dim3(256),
+                  stream, bt, n_entries, remap, n_remap);
+}
+
+eh_status eh_page_refcounts(eh_context* c, eh_stream stream, const uint32_t* bt, uint32_t bt_stride,
+                            const uint32_t* n_used, uint32_t batch, uint32_t* counts,
+                            uint32_t n_blocks) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (n_blocks == 0) return EH_OK;
+    if (!counts) return fail(EH_INVALID_ARGS, "null counts");
+    eh_status st = bind(c);
+    if (st) return st;
+    st = launch(c, c->mod_kv, "eh_fill_u32", dim3(grid_for(n_blocks, 256)), dim3(256), stream,
+                counts, (uint64_t)n_blocks, (uint32_t)0);
+    if (st || batch == 0 || bt_stride == 0) return st;
+    if (!bt || !n_used) return fail(EH_INVALID_ARGS, "null block tables or n_used");
+    return launch(c, c->mod_kv, "eh_page_refcounts",
+                  dim3(grid_for((uint64_t)batch * bt_stride, 256)), dim3(256), stream, bt,
+                  bt_stride, n_used, batch, counts, n_blocks);
+}
+
+static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                      const float* q, uint64_t q_bytes, const void* pool,
+                                      uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes,
+                                      float* out, uint64_t out_bytes, uint64_t n_head,
+                                      uint64_t n_head_kv, uint64_t head_dim, uint64_t block_tokens,
+                                      uint64_t seq_tokens, uint64_t query_pos, int causal,
+                                      const uint32_t* pos_ptr, bool split) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    eh_status st = validate_attention(kv_dtype, q_bytes, pool_bytes, bt_bytes, out_bytes, n_head,
+                                      n_head_kv, head_dim, block_tokens, seq_tokens, query_pos);
+    if (st) return st;
+    st = bind(c);
+    if (st) return st;
+    const uint64_t page_bytes = block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
+    decode_args a{};
+    a.kv_dtype = kv_dtype;
+    a.q = q;
+    a.pool = pool;
+    a.n_blocks = pool_bytes / page_bytes;
+    a.bt = bt;
+    a.bt_stride = (uint32_t)std::min<uint64_t>(bt_bytes / 4, 0xFFFFFFFFull);
+    a.lens_ptr = pos_ptr;
+    a.lens_mode = pos_ptr ? 1u : 0u;
+    a.seq_tokens = (uint32_t)seq_tokens;
+    a.query_pos = (uint32_t)query_pos;
+    a.causal = causal ? 1u : 0u;
+    a.batch = 1;
+    a.out = out;
+    a.n_head = (uint32_t)n_head;
+    a.n_head_kv = (uint32_t)n_head_kv;
+    a.head_dim = (uint32_t)head_dim;
+    a.block_tokens = (uint32_t)block_tokens;
+    // Capacity bound: with pos_ptr the live length is only known on the
+    // device, so size the grid for everything the block table can address.
+    uint64_t cap = seq_tokens;
+    if (pos_ptr) cap = std::max<uint64_t>(cap, (uint64_t)a.bt_stride * block_tokens);
+    if (!split) {
+        a.tps = 1u << 30;
+        a.max_splits = 1;
+    } else {
+        const uint32_t group = (uint32_t)(n_head / n_head_kv);
+        const uint32_t chunks = (group + pick_g(group) - 1) / pick_g(group);
+        uint64_t tps = auto_tps(1, n_head_kv, chunks, cap);
+        // Grow the split size until the partials fit the context's scratch.
+        while (n_head * div_ceil(cap, tps) * (head_dim + 2) > c->scratch_floats) tps *= 2;
+        a.tps = (uint32_t)std::min<uint64_t>(tps, 1u << 30);
+        a.max_splits = (uint32_t)div_ceil(cap, a.tps);
+        a.part_acc = c->scratch;
+        a.part_ml = c->scratch + n_head * a.max_splits * head_dim;
+    }
+    return run_decode(c, stream, a);
+}
+
+eh_status eh_paged_attention(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
+                             uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                             const uint32_t* bt, uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                             uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                             uint64_t block_tokens, uint64_t seq_tokens, uint64_t query_pos,
+                             int causal, const uint32_t* pos_ptr) {
+    return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
+                                out_bytes, n_head, n_head_kv, head_dim, block_tokens, seq_tokens,
+                                query_pos, causal, pos_ptr, false);
+}
+
+eh_status eh_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
+                            uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                            const uint32_t* bt, uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                            uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                            uint64_t block_tokens, uint64_t seq_tokens, uint64_t query_pos,
+                            int causal, const uint32_t* pos_ptr) {
+    return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
+                                out_bytes, n_head, n_head_kv, head_dim, block_tokens, seq_tokens,
+                                query_pos, causal, pos_ptr, true);
+}
+
+eh_status eh_decode_plan(uint32_t batch, uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
+                         uint32_t max_ctx, uint32_t hint, uint32_t* tokens_per_split,
+                         uint32_t* max_splits, uint64_t* workspace_bytes) {
+    if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return fail(EH_INVALID_ARGS, "heads");
+    const uint32_t group = n_head / n_head_kv;
+    const uint32_t chunks = (group + pick_g(group) - 1) / pick_g(group);
+    uint32_t tps = hint ? hint : auto_tps(batch, n_head_kv, chunks, max_ctx);
+    uint32_t ms = (uint32_t)div_ceil(max_ctx ? max_ctx : 1, tps);
+    if (tokens_per_split) *tokens_per_split = tps;
+    if (max_splits) *max_splits = ms;
+    if (workspace_bytes)
+        *workspace_bytes = ms <= 1 ? 0 : (uint64_t)batch * n_head * ms * (head_dim + 2) * 4;
+    return EH_OK;
+}
+
+eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                  const float* q, uint64_t q_bytes, const void* pool,
+                                  uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes,
+                                  uint32_t bt_stride, const uint32_t* ctx_lens, uint32_t batch,
+                                  float* out, uint64_t out_bytes, uint32_t n_head,
+                                  uint32_t n_head_kv, uint32_t head_dim, uint32_t block_tokens,
+                                  uint32_t tps, uint32_t max_splits, void* ws, uint64_t ws_bytes) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (n_head < 1) return invalid_size(1, n_head);
+    if (n_head_kv < 1) return invalid_size(1, n_head_kv);
+    if (n_head % n_head_kv != 0) return invalid_size(n_head_kv, n_head % n_head_kv);
+    if (head_dim < 1) return invalid_size(1, head_dim);
+    if (block_tokens < 1) return invalid_size(1, block_tokens);
+    if (batch == 0) return EH_OK;
+    if (!ctx_lens) return fail(EH_INVALID_ARGS, "ctx_lens is null");
+    if (tps < 1) return invalid_size(1, tps, "tokens_per_split");
+    if (max_splits < 1) return invalid_size(1, max_splits, "max_splits");
+    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+    if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
+    if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
+    if (!supported_hd(head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, head_dim);
+    if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
+    const uint64_t ws_need = max_splits <= 1 ? 0 : (uint64_t)batch * n_head * max_splits * (head_dim + 2) * 4;
+    if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
+    eh_status st = bind(c);
+    if (st) return st;
+    decode_args a{};
+    a.kv_dtype = kv_dtype;
+    a.q = q;
+    a.pool = pool;
+    a.n_blocks = pool_bytes / page_bytes;
+    a.bt = bt;
+    a.bt_stride = bt_stride;
+    a.lens_ptr = ctx_lens;
+    a.lens_mode = 2;
+    a.batch = batch;
+    a.out = out;
+    a.n_head = n_head;
+    a.n_head_kv = n_head_kv;
+    a.head_dim = head_dim;
+    a.block_tokens = block_tokens;
+    a.tps = tps;
+    a.max_splits = max_splits;
+    a.part_acc = (float*)ws;
+    a.part_ml = (float*)ws + (uint64_t)batch * n_head * max_splits * head_dim;
+    return run_decode(c, stream, a);
+}
+
+}  // extern "C"

@@ -1,0 +1,196 @@
+// paged_kv.hip -- page-row data movement for the paged KV pool on gfx950.
+//
+// Pool layout (identical to engine-kvcache/src/cache.rs:3-7,181-188 and
+// engine-cuda/kernels/paged_kv.cu:3-11, so page bytes compare bit-exactly):
+//   page b        at byte  b * page_bytes,  page_bytes = block_tokens * 2 * row_bytes
+//   token slot s  at       + s * 2 * row_bytes
+//   K row         at       + 0 .. row_bytes
+//   V row         at       + row_bytes .. 2 * row_bytes
+// row_bytes = n_kv_heads * head_dim * element_bytes.
+//
+// Because a slot's K row and V row are contiguous, one token's page row is a
+// single 2*row_bytes run.  Every kernel here walks a flat index over
+// CHUNK-byte pieces of such runs, so consecutive lanes touch consecutive
+// bytes: 64 lanes x 16 B = one 1 KiB page row per wave instruction at the
+// decode shape (2 kv heads x 128 x f16).  Work is byte copies only: results
+// are bit-exact by construction.
+//
+// All integer kernels bound-check block-table indices and page ids so a bad
+// table skips the row instead of touching memory outside the pool.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+template <int CHUNK> struct chunk_type;
+template <> struct chunk_type<16> { using T = uint4; };
+template <> struct chunk_type<8> { using T = uint2; };
+template <> struct chunk_type<4> { using T = uint32_t; };
+template <> struct chunk_type<2> { using T = uint16_t; };
+
+// Sequence lookup for a ragged batch: largest b with cu[b] <= i.
+__device__ __forceinline__ uint32_t seq_of(const uint32_t* __restrict__ cu, uint32_t batch,
+                                           uint32_t i) {
+    uint32_t lo = 0, hi = batch;  // invariant: cu[lo] <= i < cu[hi]
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (cu[mid] <= i) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+// Scatter new K/V rows into their pages.
+//   single sequence : cu == nullptr; token i goes to logical position
+//                     (pos_ptr ? *pos_ptr : start) + i through `bt`.
+//   ragged batch    : token i belongs to b = seq_of(cu, i) and goes to
+//                     start_pos[b] + (i - cu[b]) through bt + b*bt_stride.
+template <int CHUNK>
+__device__ __forceinline__ void append_body(
+    const uint8_t* __restrict__ keys, const uint8_t* __restrict__ values,
+    const uint32_t* __restrict__ bt, uint32_t bt_stride, uint8_t* __restrict__ pool,
+    uint32_t n_tokens, uint32_t start, const uint32_t* __restrict__ pos_ptr,
+    const uint32_t* __restrict__ cu, const uint32_t* __restrict__ start_pos, uint32_t batch,
+    uint32_t row_bytes, uint32_t block_tokens, uint64_t n_blocks) {
+    using T = typename chunk_type<CHUNK>::T;
+    const uint32_t cpr = row_bytes / CHUNK;          // chunks per K (or V) row
+    const uint32_t cpt = 2 * cpr;                     // chunks per token page row
+    const uint32_t total = n_tokens * cpt;           // host guarantees < 2^31
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * row_bytes;
+    const uint32_t base_pos = pos_ptr ? *pos_ptr : start;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += gridDim.x * blockDim.x) {
+        const uint32_t tok = i / cpt;
+        const uint32_t c = i - tok * cpt;
+        uint32_t pos;
+        const uint32_t* row_bt = bt;
+        if (cu) {
+            const uint32_t b = seq_of(cu, batch, tok);
+            pos = start_pos[b] + (tok - cu[b]);
+            row_bt = bt + (uint64_t)b * bt_stride;
+        } else {
+            pos = base_pos + tok;
+        }
+        const uint32_t page = pos / block_tokens;
+        const uint32_t slot = pos - page * block_tokens;
+        if (page >= bt_stride) continue;
+        const uint32_t phys = row_bt[page];
+        if (phys >= n_blocks) continue;
+        const bool is_v = c >= cpr;
+        const T* src = reinterpret_cast<const T*>((is_v ? values : keys) + (uint64_t)tok * row_bytes) +
+                       (is_v ? c - cpr : c);
+        T* dst = reinterpret_cast<T*>(pool + (uint64_t)phys * page_bytes +
+                                      (uint64_t)slot * 2 * row_bytes) + c;
+        *dst = *src;
+    }
+}
+
+// Gather [n_tokens, row] K (is_value=0) or V rows of one sequence.
+template <int CHUNK>
+__device__ __forceinline__ void gather_body(
+    const uint8_t* __restrict__ pool, const uint32_t* __restrict__ bt, uint32_t bt_len,
+    uint8_t* __restrict__ out, uint32_t n_tokens, uint32_t start, uint32_t is_value,
+    uint32_t row_bytes, uint32_t block_tokens, uint64_t n_blocks) {
+    using T = typename chunk_type<CHUNK>::T;
+    const uint32_t cpr = row_bytes / CHUNK;
+    const uint32_t total = n_tokens * cpr;           // host guarantees < 2^31
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * row_bytes;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += gridDim.x * blockDim.x) {
+        const uint32_t tok = i / cpr;
+        const uint32_t c = i - tok * cpr;
+        const uint32_t pos = start + tok;
+        const uint32_t page = pos / block_tokens;
+        const uint32_t slot = pos - page * block_tokens;
+        if (page >= bt_len) continue;
+        const uint32_t phys = bt[page];
+        if (phys >= n_blocks) continue;
+        const T* src = reinterpret_cast<const T*>(pool + (uint64_t)phys * page_bytes +
+                                                  (uint64_t)slot * 2 * row_bytes +
+                                                  (is_value ? row_bytes : 0)) + c;
+        reinterpret_cast<T*>(out + (uint64_t)tok * row_bytes)[c] = *src;
+    }
+}
+
+// Whole-page copies dst_ids[k] <- src_ids[k]: copy-on-write of a shared tail
+// page and compaction of surviving pages.  One workgroup per page pair.
+template <int CHUNK>
+__device__ __forceinline__ void copy_pages_body(uint8_t* __restrict__ pool,
+                                                const uint32_t* __restrict__ src_ids,
+                                                const uint32_t* __restrict__ dst_ids,
+                                                uint32_t n_pairs, uint64_t page_bytes,
+                                                uint64_t n_blocks) {
+    using T = typename chunk_type<CHUNK>::T;
+    const uint64_t cpp = page_bytes / CHUNK;
+    for (uint32_t k = blockIdx.x; k < n_pairs; k += gridDim.x) {
+        const uint32_t s = src_ids[k], d = dst_ids[k];
+        if (s >= n_blocks || d >= n_blocks || s == d) continue;
+        const T* src = reinterpret_cast<const T*>(pool + (uint64_t)s * page_bytes);
+        T* dst = reinterpret_cast<T*>(pool + (uint64_t)d * page_bytes);
+        for (uint64_t c = threadIdx.x; c < cpp; c += blockDim.x) dst[c] = src[c];
+    }
+}
+
+}  // namespace
+
+#define EH_DEFINE_CHUNK(CH)                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void eh_append_kv_c##CH(                        \
+        const uint8_t* keys, const uint8_t* values, const uint32_t* bt, uint32_t bt_stride,      \
+        uint8_t* pool, uint32_t n_tokens, uint32_t start, const uint32_t* pos_ptr,               \
+        const uint32_t* cu, const uint32_t* start_pos, uint32_t batch, uint32_t row_bytes,       \
+        uint32_t block_tokens, uint64_t n_blocks) {                                              \
+        append_body<CH>(keys, values, bt, bt_stride, pool, n_tokens, start, pos_ptr, cu,         \
+                        start_pos, batch, row_bytes, block_tokens, n_blocks);                    \
+    }                                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void eh_gather_kv_c##CH(                        \
+        const uint8_t* pool, const uint32_t* bt, uint32_t bt_len, uint8_t* out,                  \
+        uint32_t n_tokens, uint32_t start, uint32_t is_value, uint32_t row_bytes,                \
+        uint32_t block_tokens, uint64_t n_blocks) {                                              \
+        gather_body<CH>(pool, bt, bt_len, out, n_tokens, start, is_value, row_bytes,             \
+                        block_tokens, n_blocks);                                                 \
+    }                                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void eh_copy_pages_c##CH(                       \
+        uint8_t* pool, const uint32_t* src_ids, const uint32_t* dst_ids, uint32_t n_pairs,       \
+        uint64_t page_bytes, uint64_t n_blocks) {                                                \
+        copy_pages_body<CH>(pool, src_ids, dst_ids, n_pairs, page_bytes, n_blocks);              \
+    }
+
+EH_DEFINE_CHUNK(16)
+EH_DEFINE_CHUNK(8)
+EH_DEFINE_CHUNK(4)
+EH_DEFINE_CHUNK(2)
+
+// Rewrite block-table entries through a page remap: e = remap[e] for every
+// entry below n_remap (padding entries >= n_remap are left alone).
+extern "C" __global__ __launch_bounds__(256) void eh_remap_block_tables(
+    uint32_t* bt, uint64_t n_entries, const uint32_t* remap, uint32_t n_remap) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_entries;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t e = bt[i];
+        if (e < n_remap) bt[i] = remap[e];
+    }
+}
+
+// Page reference counts: counts[p] += number of (row b, j < n_used[b])
+// block-table entries equal to p.  counts must be zeroed by the caller.
+extern "C" __global__ __launch_bounds__(256) void eh_page_refcounts(
+    const uint32_t* bt, uint32_t bt_stride, const uint32_t* n_used, uint32_t batch,
+    uint32_t* counts, uint32_t n_blocks) {
+    const uint64_t total = (uint64_t)batch * bt_stride;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t b = (uint32_t)(i / bt_stride);
+        const uint32_t j = (uint32_t)(i - (uint64_t)b * bt_stride);
+        if (j >= n_used[b]) continue;
+        const uint32_t p = bt[i];
+        if (p < n_blocks) atomicAdd(&counts[p], 1u);
+    }
+}
+
+// Clear a u32 array with vector stores (graph-capture safe, unlike a memset node).
+extern "C" __global__ __launch_bounds__(256) void eh_fill_u32(uint32_t* p, uint64_t n,
+                                                              uint32_t v) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}

@@ -1,0 +1,93 @@
+"""Paged-attention decode on gfx950 -- the engine-cuda `PagedAttention` surface.
+
+Mirrors engine-cuda/src/paged_attention.rs: `launch`, `launch_with_pos_ptr`
+and `launch_flash_decoding` with the reference's argument order and
+validation, plus `decode_batched` for B sequences in one launch.  The pool's
+element type is an extra keyword (`kv_dtype`, default F32 as in the
+reference).  MAX_* constants are kept for API compatibility; the HIP path
+itself attends every token (no 32-split cap).
+"""
+import ctypes as C
+
+import torch
+
+from . import _lib
+from .errors import check
+from .paged_kv import KvDataType
+from .runtime import buf, context, stream_handle
+
+MAX_FLASH_DECODING_SPLITS = 32   # paged_attention.rs:33
+MAX_ATTN_HEADS = 64              # paged_attention.rs:35
+MAX_HEAD_DIM = 128               # paged_attention.rs:37
+SUPPORTED_HEAD_DIMS = (4, 8, 16, 32, 64, 128, 256)
+
+
+class PagedAttention:
+    """engine-cuda/src/paged_attention.rs:40-490 on HIP code objects."""
+
+    def __init__(self, device=0):
+        self._ctx = context(device)
+        self._L = _lib.load()
+
+    def launch(self, stream, q, pool, block_table, out, n_head, n_head_kv, head_dim,
+               block_tokens, seq_tokens, query_pos, causal, kv_dtype=KvDataType.F32):
+        """paged_attention.rs:143-174"""
+        self.launch_with_pos_ptr(stream, q, pool, block_table, out, n_head, n_head_kv, head_dim,
+                                 block_tokens, seq_tokens, query_pos, causal, None, kv_dtype)
+
+    def launch_with_pos_ptr(self, stream, q, pool, block_table, out, n_head, n_head_kv, head_dim,
+                            block_tokens, seq_tokens, query_pos, causal, pos_ptr,
+                            kv_dtype=KvDataType.F32):
+        """paged_attention.rs:177-345 (single pass per kv head)."""
+        self._call(self._L.eh_paged_attention, stream, q, pool, block_table, out, n_head,
+                   n_head_kv, head_dim, block_tokens, seq_tokens, query_pos, causal, pos_ptr,
+                   kv_dtype)
+
+    def launch_flash_decoding(self, stream, q, pool, block_table, out, n_head, n_head_kv,
+                              head_dim, block_tokens, seq_tokens, query_pos, causal, pos_ptr=None,
+                              kv_dtype=KvDataType.F32):
+        """paged_attention.rs:352-490 (split-K + log-sum-exp merge)."""
+        self._call(self._L.eh_flash_decoding, stream, q, pool, block_table, out, n_head,
+                   n_head_kv, head_dim, block_tokens, seq_tokens, query_pos, causal, pos_ptr,
+                   kv_dtype)
+
+    def _call(self, fn, stream, q, pool, block_table, out, n_head, n_head_kv, head_dim,
+              block_tokens, seq_tokens, query_pos, causal, pos_ptr, kv_dtype):
+        qp, qb = buf(q)
+        pp, pb = buf(pool)
+        bp, bb = buf(block_table)
+        op, ob = buf(out)
+        check(fn(self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
+                 op, ob, int(n_head), int(n_head_kv), int(head_dim), int(block_tokens),
+                 int(seq_tokens), int(query_pos), 1 if causal else 0, buf(pos_ptr)[0]))
+
+    # ---- batched extension ---------------------------------------------------
+    @staticmethod
+    def plan(batch, n_head, n_head_kv, head_dim, max_ctx, tokens_per_split=0):
+        """(tokens_per_split, max_splits, workspace_bytes) for decode_batched."""
+        L = _lib.load()
+        tps, ms, ws = C.c_uint32(), C.c_uint32(), C.c_uint64()
+        check(L.eh_decode_plan(int(batch), int(n_head), int(n_head_kv), int(head_dim),
+                               int(max_ctx), int(tokens_per_split), C.byref(tps), C.byref(ms),
+                               C.byref(ws)))
+        return tps.value, ms.value, ws.value
+
+    @staticmethod
+    def workspace(plan, device="cuda"):
+        nbytes = max(plan[2], 4)
+        return torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+
+    def decode_batched(self, stream, q, pool, block_tables, ctx_lens, out, n_head, n_head_kv,
+                       head_dim, block_tokens, kv_dtype, plan, workspace):
+        """q/out [B, n_head, head_dim] f32, block_tables [B, stride] u32,
+        ctx_lens [B] u32 (each <= plan's max_ctx)."""
+        batch, stride = block_tables.shape
+        qp, qb = buf(q)
+        pp, pb = buf(pool)
+        bp, bb = buf(block_tables)
+        op, ob = buf(out)
+        wp, wb = buf(workspace)
+        check(self._L.eh_paged_decode_batched(
+            self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
+            int(stride), buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv),
+            int(head_dim), int(block_tokens), int(plan[0]), int(plan[1]), wp, wb))
