@@ -94,7 +94,7 @@ def main():
     start = torch.from_numpy(shape.ctx_lens.astype(np.int32)).to(dev)   # next write position
     lens = start + 1                                                     # tokens attended
     max_ctx = int(shape.ctx_lens.max()) + extra
-    plan = PagedAttention.plan(B, NQ, NKV, HD, max_ctx, args.tps)
+    plan = PagedAttention.plan(B, NQ, NKV, HD, BT, max_ctx, args.tps)
     ws = PagedAttention.workspace(plan)
     kv, pa = PagedKvGpu(0), PagedAttention(0)
 

@@ -123,8 +123,10 @@ eh_status eh_page_refcounts(eh_context* ctx, eh_stream stream, const uint32_t* b
                             uint32_t* counts, uint32_t n_blocks);
 
 /* ---- PagedAttention::launch / launch_with_pos_ptr (paged_attention.rs:143-345):
- * single-pass decode for one sequence; q/out [n_head, head_dim] f32, pool in
- * kv_dtype.  Validation follows paged_attention.rs:193-257. */
+ * decode for one sequence; q/out [n_head, head_dim] f32, pool in kv_dtype.
+ * Validation follows paged_attention.rs:193-257.  One pass per kv head when
+ * the context fits one split, otherwise the split-K path of
+ * eh_flash_decoding (same result within rounding). */
 eh_status eh_paged_attention(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
                              const float* q, uint64_t q_bytes, const void* pool,
                              uint64_t pool_bytes, const uint32_t* block_table, uint64_t bt_bytes,
@@ -145,15 +147,19 @@ eh_status eh_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype
                             uint64_t query_pos, int causal, const uint32_t* pos_ptr);
 
 /* ---- Batched decode (extension: B sequences in one launch).
- * eh_decode_plan picks tokens_per_split (0 = automatic) and the split
- * bound for contexts up to max_ctx, and the workspace size the call needs. */
-eh_status eh_decode_plan(uint32_t batch, uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
-                         uint32_t max_ctx, uint32_t tokens_per_split_hint,
-                         uint32_t* tokens_per_split, uint32_t* max_splits,
-                         uint64_t* workspace_bytes);
+ * eh_decode_plan picks tokens_per_split (0 = automatic; at most
+ * 1022 * block_tokens) and the split bound (at most 256) for contexts up to
+ * max_ctx, and the workspace size the call needs. */
+eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uint32_t n_head_kv,
+                         uint32_t head_dim, uint32_t block_tokens, uint32_t max_ctx,
+                         uint32_t tokens_per_split_hint, uint32_t* tokens_per_split,
+                         uint32_t* max_splits, uint64_t* workspace_bytes);
 /* q/out [batch, n_head, head_dim] f32; block_tables [batch, bt_stride] u32;
- * ctx_lens [batch] u32 = tokens each query attends (its own position + 1).
- * workspace/tokens_per_split/max_splits from eh_decode_plan. */
+ * ctx_lens [batch] u32 = tokens each query attends (its own position + 1),
+ * each at most tokens_per_split * max_splits.  workspace, tokens_per_split
+ * and max_splits come from eh_decode_plan; calls sharing one workspace must
+ * not overlap in time.  Runs one split kernel and, when max_splits > 1, one
+ * log-sum-exp merge kernel. */
 eh_status eh_paged_decode_batched(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
                                   const float* q, uint64_t q_bytes, const void* pool,
                                   uint64_t pool_bytes, const uint32_t* block_tables,

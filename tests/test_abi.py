@@ -38,12 +38,12 @@ def test_code_objects_contain_launched_kernels():
             assert f"{k}{ch}".encode() in kv
     for k in ("eh_remap_block_tables", "eh_page_refcounts", "eh_fill_u32"):
         assert k.encode() in kv
-    dec = open(os.path.join(_lib.LIB_DIR, "paged_decode.hsaco"), "rb").read()
-    assert b"eh_decode_merge" in dec
     for dt in ("f32", "f16", "bf16"):
+        dec = open(os.path.join(_lib.LIB_DIR, f"paged_decode_{dt}.hsaco"), "rb").read()
         for hd in (4, 8, 16, 32, 64, 128, 256):
             for g in (1, 2, 4, 6, 7, 8):
                 assert f"eh_decode_split_{dt}_hd{hd}_g{g}".encode() in dec
+        assert b"eh_decode_merge" in dec
 
 
 def test_status_names_and_layout_bytes():
@@ -64,12 +64,22 @@ def test_null_context_is_rejected_before_any_hip_call():
 def test_decode_plan():
     L = _lib.load()
     tps, ms, ws = C.c_uint32(), C.c_uint32(), C.c_uint64()
-    assert L.eh_decode_plan(32, 12, 2, 128, 4096, 256, C.byref(tps), C.byref(ms), C.byref(ws)) == 0
+    assert L.eh_decode_plan(1, 32, 12, 2, 128, 16, 4096, 256, C.byref(tps), C.byref(ms),
+                            C.byref(ws)) == 0
     assert (tps.value, ms.value) == (256, 16)
     assert ws.value == 32 * 12 * 16 * (128 + 2) * 4
-    assert L.eh_decode_plan(1, 12, 2, 128, 100, 256, C.byref(tps), C.byref(ms), C.byref(ws)) == 0
+    # the split bound is capped at 256 by growing the split size
+    assert L.eh_decode_plan(1, 1, 32, 8, 128, 16, 1 << 20, 64, C.byref(tps), C.byref(ms),
+                            C.byref(ws)) == 0
+    assert ms.value <= 256 and tps.value * ms.value >= 1 << 20
+    assert L.eh_decode_plan(1, 1, 12, 2, 128, 16, 100, 256, C.byref(tps), C.byref(ms),
+                            C.byref(ws)) == 0
     assert ms.value == 1 and ws.value == 0
-    assert L.eh_decode_plan(1, 12, 5, 128, 100, 0, C.byref(tps), C.byref(ms), C.byref(ws)) == 21
+    assert L.eh_decode_plan(1, 1, 12, 5, 128, 16, 100, 0, C.byref(tps), C.byref(ms),
+                            C.byref(ws)) == 21
+    # a split's block-table slice must fit the 1024-entry LDS stage
+    assert L.eh_decode_plan(1, 1, 12, 2, 128, 1, 100000, 2048, C.byref(tps), C.byref(ms),
+                            C.byref(ws)) == 1
 
 
 class HostCache:

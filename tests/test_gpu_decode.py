@@ -138,8 +138,8 @@ def test_batched_decode_ragged(dev, dtype):
     q = rng.standard_normal((len(lens), n_head, hd)).astype(np.float32)
     ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
     pa = PagedAttention(0)
-    for tps in (0, 16, 64, 1024):
-        plan = PagedAttention.plan(len(lens), n_head, n_kv, hd, int(lens.max()), tps)
+    for tps in (0, 16, 64, 100, 1024):
+        plan = PagedAttention.plan(len(lens), n_head, n_kv, hd, bt, int(lens.max()), tps, dtype)
         ws = PagedAttention.workspace(plan)
         out = torch.full((len(lens), n_head, hd), float("nan"), device=dev)
         pa.decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
@@ -199,7 +199,7 @@ def test_config2_one_layer_full_size(dev):
                          i32(s.ctx_lens, dev), 32)
     lens = s.ctx_lens + 1
     q = rng.standard_normal((32, 12, 128)).astype(np.float32)
-    plan = PagedAttention.plan(32, 12, 2, 128, int(lens.max()))
+    plan = PagedAttention.plan(32, 12, 2, 128, 16, int(lens.max()))
     ws = PagedAttention.workspace(plan)
     out = torch.empty((32, 12, 128), device=dev)
     pa.decode_batched(None, torch.from_numpy(q).to(dev), pool_dev, dt, i32(lens, dev), out, 12, 2,
@@ -236,7 +236,7 @@ def test_long_context_split_covers_all_tokens(dev):
     ref = orc.sdpa_decode_batched(pool_f32, table[None], np.array([ctx], np.uint32), bt, q,
                                   n_head, n_kv, hd)
     pa = PagedAttention(0)
-    plan = PagedAttention.plan(1, n_head, n_kv, hd, ctx)
+    plan = PagedAttention.plan(1, n_head, n_kv, hd, bt, ctx)
     ws = PagedAttention.workspace(plan)
     out = torch.empty((1, n_head, hd), device=dev)
     pa.decode_batched(None, torch.from_numpy(q).to(dev), pool16.to(dev), i32(table[None], dev),

@@ -2,7 +2,7 @@
 
 Outputs (git-ignored, shipped in-tree to the GPU box):
   titan_amd/lib/paged_kv.hsaco      append / gather / page copy / table kernels
-  titan_amd/lib/paged_decode.hsaco  split-K decode attention + merge
+  titan_amd/lib/paged_decode_{f32,f16,bf16}.hsaco  split-K decode attention
   titan_amd/lib/libengine_hip.so    hipModuleLoad / hipModuleLaunchKernel C-ABI
 """
 import os
@@ -17,7 +17,13 @@ LIB = os.path.join(PKG, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 ARCH = "gfx950"
-KERNELS = ["paged_kv", "paged_decode"]
+# (output code object, source, extra defines)
+KERNELS = [
+    ("paged_kv", "paged_kv", []),
+    ("paged_decode_f32", "paged_decode", ["-DEH_ONLY_DT=0"]),
+    ("paged_decode_f16", "paged_decode", ["-DEH_ONLY_DT=1"]),
+    ("paged_decode_bf16", "paged_decode", ["-DEH_ONLY_DT=2"]),
+]
 
 # Packed-FP32 instructions are disabled for all device code on this pool.
 HIP_DEVICE_FLAGS = [
@@ -58,10 +64,10 @@ def build(verbose=False):
     os.makedirs(LIB, exist_ok=True)
     hipcc = _hipcc()
     cmds = []
-    for k in KERNELS:
-        src = os.path.join(CSRC, "kernels", k + ".hip")
-        out = os.path.join(LIB, k + ".hsaco")
-        cmds.append((k, [hipcc, *HIP_DEVICE_FLAGS, src, "-o", out + ".tmp"]))
+    for name, srcname, defs in KERNELS:
+        src = os.path.join(CSRC, "kernels", srcname + ".hip")
+        out = os.path.join(LIB, name + ".hsaco")
+        cmds.append((name, [hipcc, *HIP_DEVICE_FLAGS, *defs, src, "-o", out + ".tmp"]))
     host_out = os.path.join(LIB, "libengine_hip.so")
     cmds.append(("libengine_hip", [
         "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
@@ -71,8 +77,8 @@ def build(verbose=False):
         f"-Wl,-rpath,{ROCM}/lib",
     ]))
     _run_parallel(cmds, verbose)
-    for k in KERNELS:
-        out = os.path.join(LIB, k + ".hsaco")
+    for name, _, _ in KERNELS:
+        out = os.path.join(LIB, name + ".hsaco")
         os.replace(out + ".tmp", out)
     os.replace(host_out + ".tmp", host_out)
     return LIB

@@ -22,7 +22,7 @@
 struct eh_context {
     int device = 0;
     hipModule_t mod_kv = nullptr;
-    hipModule_t mod_decode = nullptr;
+    hipModule_t mod_decode[3] = {nullptr, nullptr, nullptr};  // f32, f16, bf16
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
     // Split-K scratch for eh_flash_decoding, allocated once at creation
@@ -53,8 +53,15 @@ eh_status invalid_size(uint64_t expected, uint64_t actual, const char* site = "I
     return fail(EH_INVALID_SIZE, site, expected, actual);
 }
 
-// Scratch capacity of eh_flash_decoding: 64 q heads x 256 splits x 256 dims.
+// Scratch capacity of the single-sequence decode: 64 q heads x 256 splits x
+// 256 dims of partials.
 constexpr uint64_t kScratchFloats = 64ull * 256 * (256 + 2);
+// Splits one merge workgroup combines (LDS-resident weights).
+constexpr uint64_t kMaxSplits = 256;
+// Block-table entries a decode workgroup stages in LDS.
+constexpr uint64_t kBtSlice = 1024;
+// Decode workgroup: 4 waves.
+constexpr uint32_t kDecodeThreads = 256;
 
 eh_status bind(eh_context* c) {
     int cur = -1;
@@ -127,7 +134,9 @@ const char* dt_name(uint32_t dt) {
     }
 }
 
-bool supported_hd(uint64_t hd) {
+// Compiled decode head sizes.
+bool supported_hd(uint32_t kv_dtype, uint64_t hd) {
+    (void)kv_dtype;
     return hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
 }
 
@@ -144,6 +153,34 @@ int log2_exact(uint64_t v) {
     int s = 0;
     while ((1ull << s) < v) ++s;
     return s;
+}
+
+int dt_index(uint32_t dt) {
+    switch (dt) {
+        case EH_KV_F32: return 0;
+        case EH_KV_F16: return 1;
+        case EH_KV_BF16: return 2;
+        default: return -1;
+    }
+}
+
+// Workspace of the split-K decode: partial accumulators then (m, l) pairs.
+uint64_t decode_ws_floats(uint64_t rows, uint64_t max_splits, uint64_t head_dim) {
+    return max_splits <= 1 ? 0 : rows * max_splits * (head_dim + 2);
+}
+
+// Largest split that keeps a workgroup's block-table slice inside LDS.
+uint64_t max_tps(uint64_t block_tokens) { return (kBtSlice - 2) * block_tokens; }
+
+// Tokens one decode workgroup walks per unrolled chunk (mirrors the kernel:
+// 16-byte lane vectors, 4 waves, 16 wave steps capped at 512 tokens).
+uint64_t chunk_tokens(uint32_t kv_dtype, uint64_t head_dim) {
+    const uint64_t elt = elt_bytes(kv_dtype) ? elt_bytes(kv_dtype) : 4;
+    const uint64_t epl = std::min<uint64_t>(16 / elt, head_dim);
+    const uint64_t tpw = 64 / std::max<uint64_t>(head_dim / epl, 1);
+    const uint64_t nw = kDecodeThreads / 64;
+    const uint64_t steps = std::max<uint64_t>(1, std::min<uint64_t>(16, 512 / (nw * tpw)));
+    return nw * tpw * steps;
 }
 
 struct decode_args {
@@ -166,7 +203,8 @@ struct decode_args {
 eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
     const char* dn = dt_name(a.kv_dtype);
     if (!dn) return fail(EH_UNSUPPORTED, "kv_dtype");
-    if (!supported_hd(a.head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, a.head_dim);
+    if (!supported_hd(a.kv_dtype, a.head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, a.head_dim);
+    if (a.max_splits > kMaxSplits) return invalid_size(kMaxSplits, a.max_splits, "max_splits");
     const uint32_t group = a.n_head / a.n_head_kv;
     const uint32_t g = pick_g(group);
     const uint32_t chunks = (group + g - 1) / g;
@@ -175,26 +213,29 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
     const float scale = 1.0f / std::sqrt((float)a.head_dim);  // paged_attention.rs:286
     const float scale_log2 = scale * 1.4426950408889634f;
     const int bt_shift = log2_exact(a.block_tokens);
-    eh_status st = launch(c, c->mod_decode, name, dim3(a.max_splits, a.n_head_kv * chunks, a.batch),
-                          dim3(256), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
-                          a.lens_ptr, a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.out,
-                          a.part_acc, a.part_ml, a.n_head, a.n_head_kv, a.block_tokens, bt_shift,
-                          a.tps, a.max_splits, scale_log2, a.n_blocks);
+    if (a.tps > max_tps(a.block_tokens)) return invalid_size(max_tps(a.block_tokens), a.tps, "tokens_per_split");
+    const hipModule_t mod = c->mod_decode[dt_index(a.kv_dtype)];
+    eh_status st = launch(c, mod, name, dim3(a.max_splits, a.n_head_kv * chunks, a.batch),
+                          dim3(kDecodeThreads),
+                          stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride, a.lens_ptr,
+                          a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.out, a.part_acc,
+                          a.part_ml, a.n_head, a.n_head_kv, a.block_tokens, bt_shift, a.tps,
+                          a.max_splits, scale_log2, a.n_blocks);
     if (st != EH_OK || a.max_splits <= 1) return st;
-    return launch(c, c->mod_decode, "eh_decode_merge", dim3(a.n_head, a.batch), dim3(64), stream,
-                  (const float*)a.part_acc, (const float*)a.part_ml, a.out, a.lens_ptr,
-                  a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.n_head, a.head_dim, a.tps,
-                  a.max_splits);
+    return launch(c, mod, "eh_decode_merge", dim3(a.n_head, a.batch), dim3(128), stream,
+                  (const float*)a.part_acc, (const float*)a.part_ml, a.out, a.lens_ptr, a.lens_mode,
+                  a.seq_tokens, a.query_pos, a.causal, a.n_head, a.head_dim, a.tps, a.max_splits);
 }
 
-// Splits: aim for enough workgroups to fill 256 CUs several times over.
-uint32_t auto_tps(uint64_t batch, uint64_t n_kv, uint64_t chunks, uint64_t max_ctx) {
-    const uint64_t target_wgs = 2048;
+// Splits: aim for enough workgroups to fill 256 CUs several times over, with
+// at most kMaxSplits splits and a block-table slice that fits LDS.
+uint64_t auto_tps(uint64_t batch, uint64_t n_kv, uint64_t chunks, uint64_t max_ctx,
+                  uint64_t block_tokens, uint64_t chunk) {
+    const uint64_t target_wgs = 1024;
     uint64_t tps = div_ceil(batch * n_kv * chunks * (max_ctx ? max_ctx : 1), target_wgs);
-    tps = div_ceil(tps, 64) * 64;
-    if (tps < 64) tps = 64;
-    if (tps > (1u << 30)) tps = 1u << 30;
-    return (uint32_t)tps;
+    tps = std::max<uint64_t>(div_ceil(tps, chunk), 1) * chunk;
+    while (div_ceil(max_ctx ? max_ctx : 1, tps) > kMaxSplits) tps += chunk;
+    return std::min(tps, max_tps(block_tokens));
 }
 
 // Checks shared by the single-sequence attention entry points
@@ -219,7 +260,7 @@ eh_status validate_attention(uint32_t kv_dtype, uint64_t q_bytes, uint64_t pool_
     for (uint64_t v : {n_head, n_head_kv, head_dim, block_tokens, seq_tokens, query_pos})
         if (v > imax) return invalid_size(imax, v);
     if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
-    if (!supported_hd(head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, head_dim);
+    if (!supported_hd(kv_dtype, head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, head_dim);
     return EH_OK;
 }
 
@@ -280,20 +321,22 @@ eh_status eh_create(int device, const char* code_object_dir, eh_context** out) {
     c->device = device;
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) { delete c; return fail(EH_DRIVER, "hipSetDevice", 0, 0, (int)e); }
-    const std::string kv = dir + "/paged_kv.hsaco", dec = dir + "/paged_decode.hsaco";
+    const std::string kv = dir + "/paged_kv.hsaco";
     e = hipModuleLoad(&c->mod_kv, kv.c_str());
     if (e != hipSuccess) { delete c; return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_kv)", 0, 0, (int)e); }
-    e = hipModuleLoad(&c->mod_decode, dec.c_str());
-    if (e != hipSuccess) {
-        hipModuleUnload(c->mod_kv);
-        delete c;
-        return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_decode)", 0, 0, (int)e);
+    const char* dec_names[3] = {"/paged_decode_f32.hsaco", "/paged_decode_f16.hsaco",
+                                "/paged_decode_bf16.hsaco"};
+    for (int i = 0; i < 3; ++i) {
+        const std::string path = dir + dec_names[i];
+        e = hipModuleLoad(&c->mod_decode[i], path.c_str());
+        if (e != hipSuccess) {
+            eh_destroy(c);
+            return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_decode)", 0, 0, (int)e);
+        }
     }
     e = hipMalloc((void**)&c->scratch, kScratchFloats * sizeof(float));
     if (e != hipSuccess) {
-        hipModuleUnload(c->mod_kv);
-        hipModuleUnload(c->mod_decode);
-        delete c;
+        eh_destroy(c);
         return fail(EH_ALLOC_FAILED, "hipMalloc(split-K scratch)", 0, 0, (int)e);
     }
     c->scratch_floats = kScratchFloats;
@@ -306,7 +349,8 @@ void eh_destroy(eh_context* c) {
     hipSetDevice(c->device);
     if (c->scratch) hipFree(c->scratch);
     if (c->mod_kv) hipModuleUnload(c->mod_kv);
-    if (c->mod_decode) hipModuleUnload(c->mod_decode);
+    for (hipModule_t m : c->mod_decode)
+        if (m) hipModuleUnload(m);
     delete c;
 }
 
@@ -469,7 +513,7 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
                                       float* out, uint64_t out_bytes, uint64_t n_head,
                                       uint64_t n_head_kv, uint64_t head_dim, uint64_t block_tokens,
                                       uint64_t seq_tokens, uint64_t query_pos, int causal,
-                                      const uint32_t* pos_ptr, bool split) {
+                                      const uint32_t* pos_ptr, bool single_pass) {
     if (!c) return fail(EH_INVALID_ARGS, "null context");
     eh_status st = validate_attention(kv_dtype, q_bytes, pool_bytes, bt_bytes, out_bytes, n_head,
                                       n_head_kv, head_dim, block_tokens, seq_tokens, query_pos);
@@ -499,20 +543,21 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
     // device, so size the grid for everything the block table can address.
     uint64_t cap = seq_tokens;
     if (pos_ptr) cap = std::max<uint64_t>(cap, (uint64_t)a.bt_stride * block_tokens);
-    if (!split) {
-        a.tps = 1u << 30;
-        a.max_splits = 1;
-    } else {
-        const uint32_t group = (uint32_t)(n_head / n_head_kv);
-        const uint32_t chunks = (group + pick_g(group) - 1) / pick_g(group);
-        uint64_t tps = auto_tps(1, n_head_kv, chunks, cap);
-        // Grow the split size until the partials fit the context's scratch.
-        while (n_head * div_ceil(cap, tps) * (head_dim + 2) > c->scratch_floats) tps *= 2;
-        a.tps = (uint32_t)std::min<uint64_t>(tps, 1u << 30);
-        a.max_splits = (uint32_t)div_ceil(cap, a.tps);
-        a.part_acc = c->scratch;
-        a.part_ml = c->scratch + n_head * a.max_splits * head_dim;
-    }
+    const uint32_t group = (uint32_t)(n_head / n_head_kv);
+    const uint32_t chunks = (group + pick_g(group) - 1) / pick_g(group);
+    const uint64_t chunk = chunk_tokens(kv_dtype, head_dim);
+    uint64_t tps = auto_tps(1, n_head_kv, chunks, cap, block_tokens, chunk);
+    if (single_pass && cap <= max_tps(block_tokens)) tps = std::max<uint64_t>(cap, 1);
+    // Grow the split until the partials fit the context's scratch.
+    while (div_ceil(cap, tps) > 1 &&
+           decode_ws_floats(n_head, div_ceil(cap, tps), head_dim) > c->scratch_floats)
+        tps *= 2;
+    if (tps > max_tps(block_tokens) || div_ceil(cap, tps) > kMaxSplits)
+        return invalid_size(max_tps(block_tokens) * kMaxSplits, cap, "context too long");
+    a.tps = (uint32_t)tps;
+    a.max_splits = (uint32_t)div_ceil(cap, tps);
+    a.part_acc = c->scratch;
+    a.part_ml = c->scratch + n_head * a.max_splits * head_dim;
     return run_decode(c, stream, a);
 }
 
@@ -524,7 +569,7 @@ eh_status eh_paged_attention(eh_context* c, eh_stream stream, uint32_t kv_dtype,
                              int causal, const uint32_t* pos_ptr) {
     return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
                                 out_bytes, n_head, n_head_kv, head_dim, block_tokens, seq_tokens,
-                                query_pos, causal, pos_ptr, false);
+                                query_pos, causal, pos_ptr, true);
 }
 
 eh_status eh_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
@@ -535,21 +580,28 @@ eh_status eh_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype, 
                             int causal, const uint32_t* pos_ptr) {
     return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
                                 out_bytes, n_head, n_head_kv, head_dim, block_tokens, seq_tokens,
-                                query_pos, causal, pos_ptr, true);
+                                query_pos, causal, pos_ptr, false);
 }
 
-eh_status eh_decode_plan(uint32_t batch, uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
-                         uint32_t max_ctx, uint32_t hint, uint32_t* tokens_per_split,
-                         uint32_t* max_splits, uint64_t* workspace_bytes) {
+eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uint32_t n_head_kv,
+                         uint32_t head_dim, uint32_t block_tokens, uint32_t max_ctx,
+                         uint32_t hint, uint32_t* tokens_per_split, uint32_t* max_splits,
+                         uint64_t* workspace_bytes) {
     if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return fail(EH_INVALID_ARGS, "heads");
+    if (block_tokens < 1) return fail(EH_INVALID_ARGS, "block_tokens");
+    if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
     const uint32_t group = n_head / n_head_kv;
     const uint32_t chunks = (group + pick_g(group) - 1) / pick_g(group);
-    uint32_t tps = hint ? hint : auto_tps(batch, n_head_kv, chunks, max_ctx);
-    uint32_t ms = (uint32_t)div_ceil(max_ctx ? max_ctx : 1, tps);
-    if (tokens_per_split) *tokens_per_split = tps;
+    uint64_t tps = hint ? hint
+                        : auto_tps(batch, n_head_kv, chunks, max_ctx, block_tokens,
+                                   chunk_tokens(kv_dtype, head_dim));
+    while (div_ceil(max_ctx ? max_ctx : 1, tps) > kMaxSplits) tps *= 2;
+    if (tps > max_tps(block_tokens))
+        return invalid_size(max_tps(block_tokens), tps, "tokens_per_split");
+    const uint32_t ms = (uint32_t)div_ceil(max_ctx ? max_ctx : 1, tps);
+    if (tokens_per_split) *tokens_per_split = (uint32_t)tps;
     if (max_splits) *max_splits = ms;
-    if (workspace_bytes)
-        *workspace_bytes = ms <= 1 ? 0 : (uint64_t)batch * n_head * ms * (head_dim + 2) * 4;
+    if (workspace_bytes) *workspace_bytes = 4 * decode_ws_floats((uint64_t)batch * n_head, ms, head_dim);
     return EH_OK;
 }
 
@@ -577,9 +629,10 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
     const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
     if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
-    if (!supported_hd(head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, head_dim);
+    if (!supported_hd(kv_dtype, head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, head_dim);
     if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
-    const uint64_t ws_need = max_splits <= 1 ? 0 : (uint64_t)batch * n_head * max_splits * (head_dim + 2) * 4;
+    if (max_splits > kMaxSplits) return invalid_size(kMaxSplits, max_splits, "max_splits");
+    const uint64_t ws_need = 4 * decode_ws_floats((uint64_t)batch * n_head, max_splits, head_dim);
     if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
     eh_status st = bind(c);
     if (st) return st;

@@ -11,16 +11,27 @@
 //   * the workgroup serves every q head of the GQA group from ONE read of each
 //     K/V row, so each KV byte crosses HBM once per kv head, not once per q head;
 //   * a token's head row is split over LPT lanes with EPL elements (16 B) each;
-//     a wave instruction reads TPW = 64/LPT consecutive tokens' rows;
+//     each wave streams TPW = 64/LPT neighbouring tokens per wave step;
+//   * every lane keeps DEPTH token rows in flight in a register pipeline:
+//     a slot is refilled with the row DEPTH steps ahead as soon as it has
+//     been consumed; the steps of a chunk are fully unrolled so no in-flight
+//     load is carried across a loop edge (a loop-carried copy of an in-flight
+//     register would drain the pipeline);
+//   * the split's block-table slice is staged once in LDS, so page lookups
+//     never wait on global memory;
 //   * q.k partial sums are reduced inside each LPT-lane group with DPP
 //     butterflies (bitwise-identical result in every lane of the group);
-//   * online softmax runs in the log2 domain (q pre-scaled by scale*log2 e),
-//     rescaling once per U-token chunk, not once per token;
-//   * split results (m, l, acc) go to a workspace; eh_decode_merge does the
-//     log-sum-exp merge.  A split count of one writes the output directly.
+//   * online softmax runs in the log2 domain (q pre-scaled by scale*log2 e)
+//     and rescales the accumulators only when the running max moves;
+//   * split results (m, l, acc) go to a workspace; eh_decode_merge combines
+//     them in a second launch (a kernel boundary instead of device-scope
+//     fences, which write back the whole L2 per workgroup on this part).
+//     A split count of one writes the output directly.
 // Sequence lengths are read on the device (pos_ptr or ctx_lens), so a grid
 // sized for the capacity bound stays correct under graph replay as the
 // context grows: splits past the live length exit at once.
+// The file is compiled once per KV element type (EH_ONLY_DT) so the three
+// code objects build in parallel.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -28,7 +39,6 @@
 namespace {
 
 constexpr int NW = 4;  // waves per workgroup
-constexpr int U = 4;   // tokens per stream per iteration
 
 enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
@@ -111,21 +121,37 @@ __device__ __forceinline__ uint32_t split_count(uint32_t n, uint32_t tps, uint32
     return s < max_splits ? s : max_splits;
 }
 
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Block-table entries one workgroup stages in LDS: every page its split
+// touches.  The host keeps tokens_per_split <= (BT_SLICE - 2) * block_tokens.
+constexpr uint32_t BT_SLICE = 1024;
+// Wave steps per chunk: 16, fewer for narrow heads so that a chunk stays at
+// most 512 tokens.  tokens_per_split should be a multiple of the chunk
+// NW * TPW * chunk_steps(TPW) (the host derives the same value).
+__host__ __device__ constexpr int chunk_steps(int tpw) {
+    return (512 / (NW * tpw)) < 1 ? 1 : ((512 / (NW * tpw)) > 16 ? 16 : 512 / (NW * tpw));
+}
+
 template <int DT, int HD, int G>
 __device__ __forceinline__ void decode_split(
     const float* __restrict__ q, const uint8_t* __restrict__ pool,
     const uint32_t* __restrict__ bt, uint32_t bt_stride, len_src L, float* __restrict__ out,
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t n_head,
-    uint32_t n_head_kv, uint32_t block_tokens, int bt_shift, uint32_t tps,
-    uint32_t max_splits, float scale_log2, uint64_t n_blocks) {
+    uint32_t n_head_kv, uint32_t block_tokens, int bt_shift, uint32_t tps, uint32_t max_splits,
+    float scale_log2, uint64_t n_blocks) {
     constexpr int ELT = dt_info<DT>::bytes;
     constexpr int EPL = (16 / ELT) < HD ? (16 / ELT) : HD;  // elements per lane
     constexpr int LPT = HD / EPL;                            // lanes per token row
-    constexpr int TPW = 64 / LPT;                            // tokens per wave instruction
-    constexpr int R = NW * TPW;                              // token streams per workgroup
+    constexpr int TPW = 64 / LPT;                            // tokens per wave step
     constexpr int NWORDS = EPL * ELT / 4;
     static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "head_dim/lane mapping");
+    static_assert(EPL % 4 == 0 || EPL == HD, "query vector loads");
+    constexpr int STEPS = chunk_steps(TPW);
+    constexpr uint32_t CHUNK = (uint32_t)(NW * TPW * STEPS);
+    constexpr int DEPTH = STEPS < 4 ? STEPS : 4;
 
+    __shared__ uint32_t s_bt[BT_SLICE];
     __shared__ float s_m[NW][G], s_l[NW][G];
     __shared__ float s_acc[NW][G][HD];
 
@@ -135,10 +161,18 @@ __device__ __forceinline__ void decode_split(
     const uint32_t hk = blockIdx.y / n_chunks;
     const uint32_t hc = blockIdx.y - hk * n_chunks;
     const uint32_t b = blockIdx.z;
+    const uint32_t qh0 = hk * group + hc * G;
 
     const uint32_t n = live_tokens(L, b);
     const uint32_t t0 = split * tps;
-    if (t0 >= n) return;
+    if (t0 >= n) {
+        // No live tokens at all: the output is zero (forward_cpu.rs:436-439).
+        if (n == 0 && split == 0)
+            for (int idx = threadIdx.x; idx < G * HD; idx += NW * 64)
+                if (hc * G + idx / HD < group)
+                    out[((uint64_t)b * n_head + qh0 + idx / HD) * HD + idx % HD] = 0.0f;
+        return;
+    }
     const uint32_t t1 = (n - t0 < tps) ? n : t0 + tps;
     const uint32_t nsplit = split_count(n, tps, max_splits);
 
@@ -146,7 +180,6 @@ __device__ __forceinline__ void decode_split(
     const int wave = threadIdx.x >> 6;
     const int grp = lane / LPT;
     const int sub = lane - grp * LPT;
-    const int stream = wave * TPW + grp;
 
     const uint32_t row_bytes = n_head_kv * HD * ELT;
     const uint64_t tok_bytes = 2ull * row_bytes;
@@ -154,15 +187,38 @@ __device__ __forceinline__ void decode_split(
     const uint32_t* bt_row = bt + (uint64_t)b * bt_stride;
     const uint8_t* kbase = pool + (uint64_t)hk * HD * ELT + (uint64_t)sub * EPL * ELT;
 
-    // Query slice for every head of this chunk, pre-scaled into the log2 domain.
+    auto page_of = [&](uint32_t t) -> uint32_t {
+        return bt_shift >= 0 ? (t >> bt_shift) : (t / block_tokens);
+    };
+
+    // Stage the block-table slice of this split (invalid entries -> ~0).
+    const uint32_t pg0 = page_of(t0);
+    const uint32_t npg = page_of(t1 - 1) - pg0 + 1;
+    for (uint32_t i = threadIdx.x; i < npg && i < BT_SLICE; i += NW * 64) {
+        const uint32_t pg = pg0 + i;
+        s_bt[i] = pg < bt_stride ? bt_row[pg] : 0xFFFFFFFFu;
+    }
+
+    // Query slice of every head in this chunk, pre-scaled into the log2
+    // domain.  Loads are unconditional (heads past the group re-read the last
+    // valid head and are zeroed), so they issue back to back.
     float qv[G][EPL];
-    const uint32_t qh0 = hk * group + hc * G;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const bool hv = hc * G + h < group;
-        const float* qp = q + ((uint64_t)b * n_head + qh0 + h) * HD + sub * EPL;
+        const uint32_t hh = (hc * G + h < group) ? hc * G + h : group - 1;
+        const float sc = (hc * G + h < group) ? scale_log2 : 0.0f;
+        const float* qp = q + ((uint64_t)b * n_head + hk * group + hh) * HD + sub * EPL;
+        if constexpr (EPL % 4 == 0) {
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) qv[h][e] = hv ? qp[e] * scale_log2 : 0.0f;
+            for (int e = 0; e < EPL; e += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(qp + e);
+                qv[h][e] = v.x * sc; qv[h][e + 1] = v.y * sc;
+                qv[h][e + 2] = v.z * sc; qv[h][e + 3] = v.w * sc;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) qv[h][e] = qp[e] * sc;
+        }
     }
 
     float m[G], l[G], acc[G][EPL];
@@ -172,62 +228,70 @@ __device__ __forceinline__ void decode_split(
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[h][e] = 0.0f;
     }
+    __syncthreads();
 
-    for (uint32_t tb = t0 + stream; tb < t1; tb += R * U) {
-        raw_t<NWORDS> kr[U], vr[U];
-        bool ok[U];
+    // The split is walked in chunks of NW * TPW * STEPS tokens.  Inside a
+    // chunk each wave streams STEPS consecutive wave steps (TPW neighbouring
+    // tokens each, one per lane group) through a DEPTH-deep register
+    // pipeline.  The steps are fully unrolled, so slot indices are compile
+    // time constants and no in-flight load crosses a loop back edge.
+    for (uint32_t c0 = t0; c0 < t1; c0 += CHUNK) {
+        const uint32_t w0 = c0 + (uint32_t)wave * TPW * STEPS;
+        const uint32_t w1 = (w0 + TPW * STEPS < t1) ? w0 + TPW * STEPS : t1;
+        if (w0 >= w1) continue;  // wave-uniform: nothing left for this wave
+        raw_t<NWORDS> kr[DEPTH], vr[DEPTH];
+        bool ok[DEPTH];
+        // Loads of wave step k into slot k % DEPTH.  Steps past the end of
+        // the range re-read the wave's first row (masked), staying in bounds.
+        auto issue = [&](int k) {
+            const int j = k % DEPTH;
+            const uint32_t t = w0 + (uint32_t)(k * TPW) + grp;
+            const bool valid = t < w1;
+            const uint32_t tc = valid ? t : w0;
+            const uint32_t pg = page_of(tc);
+            const uint32_t rel = pg - pg0;
+            const uint32_t phys = rel < BT_SLICE ? s_bt[rel] : 0xFFFFFFFFu;
+            const bool pv = phys < n_blocks;
+            const uint8_t* p = kbase + (uint64_t)(pv ? phys : 0u) * page_bytes +
+                               (uint64_t)(tc - pg * block_tokens) * tok_bytes;
+            kr[j] = load_raw<NWORDS>(p);
+            vr[j] = load_raw<NWORDS>(p + row_bytes);
+            ok[j] = valid && pv;
+        };
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t t = tb + u * R;
+        for (int k = 0; k < DEPTH; ++k) issue(k);
 #pragma unroll
-            for (int w = 0; w < NWORDS; ++w) { kr[u].w[w] = 0u; vr[u].w[w] = 0u; }
-            ok[u] = false;
-            if (t < t1) {
-                const uint32_t page = bt_shift >= 0 ? (t >> bt_shift) : (t / block_tokens);
-                const uint32_t slot = t - page * block_tokens;
-                const uint32_t phys = page < bt_stride ? bt_row[page] : 0xFFFFFFFFu;
-                if (phys < n_blocks) {
-                    const uint8_t* p = kbase + (uint64_t)phys * page_bytes + (uint64_t)slot * tok_bytes;
-                    kr[u] = load_raw<NWORDS>(p);
-                    vr[u] = load_raw<NWORDS>(p + row_bytes);
-                    ok[u] = true;
-                }
-            }
-        }
-        float s[U][G];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int k = 0; k < STEPS; ++k) {
+            const int j = k % DEPTH;
+            if (w0 + (uint32_t)(k * TPW) >= w1) break;  // wave-uniform tail exit
+            float s[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 float p = 0.0f;
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) p = fmaf(qv[h][e], elem<DT>(kr[u], e), p);
-                p = group_sum<LPT>(p);
-                s[u][h] = ok[u] ? p : -INFINITY;
+                for (int e = 0; e < EPL; ++e) p = fmaf(qv[h][e], elem<DT>(kr[j], e), p);
+                s[h] = group_sum<LPT>(p);
             }
-        }
+            const bool okj = ok[j];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float mc = m[h];
+            for (int h = 0; h < G; ++h) {
+                if (okj && s[h] > m[h]) {  // rescale only when the running max moves
+                    const float corr = fast_exp2(m[h] - s[h]);
+                    l[h] *= corr;
 #pragma unroll
-            for (int u = 0; u < U; ++u) mc = fmaxf(mc, s[u][h]);
-            if (mc == -INFINITY) continue;
-            const float corr = exp2f(m[h] - mc);
-            l[h] *= corr;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[h][e] *= corr;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const float p = exp2f(s[u][h] - mc);
+                    for (int e = 0; e < EPL; ++e) acc[h][e] *= corr;
+                    m[h] = s[h];
+                }
+                const float p = okj ? fast_exp2(s[h] - m[h]) : 0.0f;
                 l[h] += p;
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p, elem<DT>(vr[u], e), acc[h][e]);
+                for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p, elem<DT>(vr[j], e), acc[h][e]);
             }
-            m[h] = mc;
+            if (k + DEPTH < STEPS) issue(k + DEPTH);  // refill the slot DEPTH steps ahead
         }
     }
 
-    // Merge the TPW token streams of this wave (lanes sub, sub+LPT, ...).
+    // Merge the TPW lane groups of this wave (lanes sub, sub+LPT, ...).
 #pragma unroll
     for (int off = LPT; off < 64; off <<= 1) {
 #pragma unroll
@@ -235,8 +299,8 @@ __device__ __forceinline__ void decode_split(
             const float mo = __shfl_xor(m[h], off, 64);
             const float lo = __shfl_xor(l[h], off, 64);
             const float M = fmaxf(m[h], mo);
-            const float fa = (M == -INFINITY) ? 0.0f : exp2f(m[h] - M);
-            const float fb = (M == -INFINITY) ? 0.0f : exp2f(mo - M);
+            const float fa = (M == -INFINITY) ? 0.0f : fast_exp2(m[h] - M);
+            const float fb = (M == -INFINITY) ? 0.0f : fast_exp2(mo - M);
             l[h] = l[h] * fa + lo * fb;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
@@ -256,7 +320,8 @@ __device__ __forceinline__ void decode_split(
     }
     __syncthreads();
 
-    // Merge the NW waves and emit: final output for a single split, else a partial.
+    // Merge the NW waves: final output for a single split, else a partial
+    // that eh_decode_merge combines.
     for (int idx = threadIdx.x; idx < G * HD; idx += NW * 64) {
         const int h = idx / HD;
         const int d = idx - h * HD;
@@ -267,7 +332,7 @@ __device__ __forceinline__ void decode_split(
         float Ls = 0.0f, A = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            const float f = (s_m[w][h] == -INFINITY) ? 0.0f : exp2f(s_m[w][h] - M);
+            const float f = (s_m[w][h] == -INFINITY) ? 0.0f : fast_exp2(s_m[w][h] - M);
             Ls = fmaf(s_l[w][h], f, Ls);
             A = fmaf(s_acc[w][h][d], f, A);
         }
@@ -282,37 +347,61 @@ __device__ __forceinline__ void decode_split(
     }
 }
 
+// Splits one merge workgroup combines (LDS-resident weights).
+constexpr uint32_t MERGE_MAX_SPLITS = 256;
+
 }  // namespace
 
-// Log-sum-exp merge of split partials.  grid (n_head, batch), 64 threads.
-extern "C" __global__ __launch_bounds__(64) void eh_decode_merge(
+// Log-sum-exp merge of split partials: out = sum_s w_s acc_s / sum_s w_s l_s
+// with w_s = exp2(m_s - max m).  grid (n_head, batch), 128 threads; wave 0
+// reduces over splits (lanes stride the split index), then all threads
+// combine the partial vectors with independent, unrolled loads.
+extern "C" __global__ __launch_bounds__(128) void eh_decode_merge(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
     const uint32_t* lens_ptr, uint32_t lens_mode, uint32_t seq_tokens, uint32_t query_pos,
     uint32_t causal, uint32_t n_head, uint32_t head_dim, uint32_t tps, uint32_t max_splits) {
+    __shared__ float s_w[MERGE_MAX_SPLITS];
+    __shared__ float s_inv;
     const len_src L{lens_ptr, lens_mode, seq_tokens, query_pos, causal};
     const uint32_t qh = blockIdx.x, b = blockIdx.y;
     const uint32_t n = live_tokens(L, b);
+    uint32_t nsplit = split_count(n, tps, max_splits);
+    if (nsplit > MERGE_MAX_SPLITS) nsplit = MERGE_MAX_SPLITS;
+    if (n == 0 || nsplit <= 1) return;  // the split kernel wrote the output
     const uint64_t qrow = (uint64_t)b * n_head + qh;
-    if (n == 0) {
-        for (uint32_t d = threadIdx.x; d < head_dim; d += 64) out[qrow * head_dim + d] = 0.0f;
-        return;
-    }
-    const uint32_t nsplit = split_count(n, tps, max_splits);
-    if (nsplit <= 1) return;  // the split kernel wrote the output
     const float* ml = part_ml + qrow * max_splits * 2;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < nsplit; ++s)
-        if (ml[2 * s + 1] > 0.0f) M = fmaxf(M, ml[2 * s]);
-    float Ls = 0.0f;
-    for (uint32_t s = 0; s < nsplit; ++s)
-        if (ml[2 * s + 1] > 0.0f) Ls = fmaf(ml[2 * s + 1], exp2f(ml[2 * s] - M), Ls);
-    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-    for (uint32_t d = threadIdx.x; d < head_dim; d += 64) {
-        float A = 0.0f;
-        for (uint32_t s = 0; s < nsplit; ++s)
-            if (ml[2 * s + 1] > 0.0f)
-                A = fmaf(part_acc[(qrow * max_splits + s) * head_dim + d], exp2f(ml[2 * s] - M), A);
-        out[qrow * head_dim + d] = A * inv;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float M = -INFINITY;
+        for (uint32_t s = lane; s < nsplit; s += 64)
+            if (ml[2 * s + 1] > 0.0f) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        float Ls = 0.0f;
+        for (uint32_t s = lane; s < nsplit; s += 64) {
+            const float ls = ml[2 * s + 1];
+            const float w = ls > 0.0f ? fast_exp2(ml[2 * s] - M) : 0.0f;
+            s_w[s] = w;
+            Ls = fmaf(ls, w, Ls);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) Ls += __shfl_xor(Ls, off, 64);
+        if (lane == 0) s_inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (uint32_t d = threadIdx.x; d < head_dim; d += 128) {
+        const float* pa = part_acc + qrow * max_splits * head_dim + d;
+        float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f;
+        uint32_t s = 0;
+        for (; s + 4 <= nsplit; s += 4) {
+            A0 = fmaf(pa[(uint64_t)s * head_dim], s_w[s], A0);
+            A1 = fmaf(pa[(uint64_t)(s + 1) * head_dim], s_w[s + 1], A1);
+            A2 = fmaf(pa[(uint64_t)(s + 2) * head_dim], s_w[s + 2], A2);
+            A3 = fmaf(pa[(uint64_t)(s + 3) * head_dim], s_w[s + 3], A3);
+        }
+        for (; s < nsplit; ++s) A0 = fmaf(pa[(uint64_t)s * head_dim], s_w[s], A0);
+        out[qrow * head_dim + d] = ((A0 + A1) + (A2 + A3)) * inv;
     }
 }
 
@@ -346,6 +435,12 @@ extern "C" __global__ __launch_bounds__(64) void eh_decode_merge(
     EH_DECODE_G(DTN, DT, 128) \
     EH_DECODE_G(DTN, DT, 256)
 
+#if !defined(EH_ONLY_DT) || EH_ONLY_DT == 0
 EH_DECODE_HD(f32, DT_F32)
+#endif
+#if !defined(EH_ONLY_DT) || EH_ONLY_DT == 1
 EH_DECODE_HD(f16, DT_F16)
+#endif
+#if !defined(EH_ONLY_DT) || EH_ONLY_DT == 2
 EH_DECODE_HD(bf16, DT_BF16)
+#endif

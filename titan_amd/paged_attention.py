@@ -63,17 +63,19 @@ class PagedAttention:
 
     # ---- batched extension ---------------------------------------------------
     @staticmethod
-    def plan(batch, n_head, n_head_kv, head_dim, max_ctx, tokens_per_split=0):
+    def plan(batch, n_head, n_head_kv, head_dim, block_tokens, max_ctx, tokens_per_split=0,
+             kv_dtype=KvDataType.F16):
         """(tokens_per_split, max_splits, workspace_bytes) for decode_batched."""
         L = _lib.load()
         tps, ms, ws = C.c_uint32(), C.c_uint32(), C.c_uint64()
-        check(L.eh_decode_plan(int(batch), int(n_head), int(n_head_kv), int(head_dim),
-                               int(max_ctx), int(tokens_per_split), C.byref(tps), C.byref(ms),
-                               C.byref(ws)))
+        check(L.eh_decode_plan(int(kv_dtype), int(batch), int(n_head), int(n_head_kv), int(head_dim),
+                               int(block_tokens), int(max_ctx), int(tokens_per_split),
+                               C.byref(tps), C.byref(ms), C.byref(ws)))
         return tps.value, ms.value, ws.value
 
     @staticmethod
     def workspace(plan, device="cuda"):
+        """Workspace for the split partials of decode_batched."""
         nbytes = max(plan[2], 4)
         return torch.empty(nbytes // 4, dtype=torch.float32, device=device)
 
