@@ -351,3 +351,66 @@ class Radix:
     def set_ref_count(self, tokens, ref):
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         return lib().orc_radix_set_ref_count(self._h, _p(t), t.size, ref)
+
+
+class Streaming:
+    """StreamingKvConfig / StreamingKvManager restatement (engine-kvcache/src/streaming.rs)."""
+
+    class Cfg(C.Structure):
+        _fields_ = [("sink_tokens", C.c_size_t), ("recent_window_tokens", C.c_size_t),
+                    ("max_budget_tokens", C.c_size_t), ("block_tokens", C.c_size_t)]
+
+    def __init__(self, sink=None, recent=None, budget=None, bt=None):
+        L = lib()
+        L.orc_stream_cfg_new.restype = Streaming.Cfg
+        L.orc_stream_cfg_new.argtypes = [C.c_size_t] * 4
+        L.orc_stream_cfg_default.restype = Streaming.Cfg
+        L.orc_stream_cfg_default.argtypes = []
+        for f in ("orc_stream_sink_blocks", "orc_stream_recent_blocks",
+                  "orc_stream_max_active_blocks"):
+            getattr(L, f).restype = C.c_size_t
+            getattr(L, f).argtypes = [Streaming.Cfg]
+        L.orc_stream_new.restype = C.c_void_p
+        L.orc_stream_new.argtypes = [Streaming.Cfg]
+        L.orc_stream_destroy.restype = None
+        L.orc_stream_destroy.argtypes = [C.c_void_p]
+        L.orc_stream_record_attention_mass.restype = None
+        L.orc_stream_record_attention_mass.argtypes = [C.c_void_p, C.c_uint32, C.c_float]
+        L.orc_stream_scores_len.restype = C.c_size_t
+        L.orc_stream_scores_len.argtypes = [C.c_void_p]
+        L.orc_stream_prune_blocks.restype = None
+        L.orc_stream_prune_blocks.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
+                                              C.POINTER(C.c_size_t), C.c_void_p,
+                                              C.POINTER(C.c_size_t)]
+        self.cfg = L.orc_stream_cfg_default() if sink is None else L.orc_stream_cfg_new(
+            sink, recent, budget, bt)
+        self._h = L.orc_stream_new(self.cfg)
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_stream_destroy(self._h)
+            self._h = None
+
+    def sink_blocks(self):
+        return lib().orc_stream_sink_blocks(self.cfg)
+
+    def recent_blocks(self):
+        return lib().orc_stream_recent_blocks(self.cfg)
+
+    def max_active_blocks(self):
+        return lib().orc_stream_max_active_blocks(self.cfg)
+
+    def record_attention_mass(self, block, mass):
+        lib().orc_stream_record_attention_mass(self._h, block, mass)
+
+    def scores_len(self):
+        return lib().orc_stream_scores_len(self._h)
+
+    def prune_blocks(self, table):
+        t = np.ascontiguousarray(table, dtype=np.uint32)
+        r = np.zeros(max(t.size, 1), np.uint32)
+        e = np.zeros(max(t.size, 1), np.uint32)
+        nr, ne = C.c_size_t(), C.c_size_t()
+        lib().orc_stream_prune_blocks(self._h, _p(t), t.size, _p(r), C.byref(nr), _p(e),
+                                      C.byref(ne))
+        return [int(x) for x in r[:nr.value]], [int(x) for x in e[:ne.value]]
