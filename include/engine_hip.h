@@ -169,6 +169,38 @@ eh_status eh_paged_decode_batched(eh_context* ctx, eh_stream stream, uint32_t kv
                                   uint32_t tokens_per_split, uint32_t max_splits, void* workspace,
                                   uint64_t workspace_bytes);
 
+/* ---- FlashAttention2::launch / launch_with_pos_ptr (flash_attention.rs:95-225):
+ * causal chunked prefill.  q/out [q_tokens, n_head, head_dim] f32; query i
+ * sits at position p0 + i (p0 = *pos_ptr when given, else pos_offset) and
+ * attends keys 0..=p0+i through the block table (flash_attention_2.cu:44-68);
+ * a row with no valid key is zero.  Size checks follow
+ * flash_attention.rs:142-164 (q, out, ceil((pos_offset+q_tokens)/block_tokens)
+ * table entries).  QK^T and PV run on MFMA: f16 KV with f16 operands, bf16 KV
+ * with hi+lo bf16 operand pairs, f32 KV with f32 MFMA.  head_dim 64 or 128.
+ * Keys whose block-table entry lies past the table or past the pool are
+ * masked. */
+eh_status eh_flash_attention_prefill(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                                     const float* q, uint64_t q_bytes, const void* pool,
+                                     uint64_t pool_bytes, const uint32_t* block_table,
+                                     uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                                     uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                                     uint64_t block_tokens, uint64_t q_tokens,
+                                     uint64_t pos_offset, const uint32_t* pos_ptr);
+
+/* ---- Batched chunked prefill (extension of flash_attention.rs:95 for B
+ * sequences in one launch): rows cu_q[b] .. cu_q[b+1] of q/out
+ * [total_q_tokens, n_head, head_dim] belong to sequence b, whose first query
+ * sits at position start_pos[b], through block_tables + b*bt_stride.
+ * cu_q [batch+1] and start_pos [batch] are device arrays; max_q_tokens must
+ * be >= every cu_q[b+1]-cu_q[b] (it sizes the grid). */
+eh_status eh_prefill_batched(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                             const float* q, uint64_t q_bytes, const void* pool,
+                             uint64_t pool_bytes, const uint32_t* block_tables, uint64_t bt_bytes,
+                             uint32_t bt_stride, const uint32_t* cu_q, const uint32_t* start_pos,
+                             uint32_t batch, uint32_t max_q_tokens, uint32_t total_q_tokens,
+                             float* out, uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                             uint32_t head_dim, uint32_t block_tokens);
+
 #ifdef __cplusplus
 }
 #endif

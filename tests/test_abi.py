@@ -44,6 +44,10 @@ def test_code_objects_contain_launched_kernels():
             for g in (1, 2, 4, 6, 7, 8):
                 assert f"eh_decode_split_{dt}_hd{hd}_g{g}".encode() in dec
         assert b"eh_decode_merge" in dec
+    pf = open(os.path.join(_lib.LIB_DIR, "paged_prefill.hsaco"), "rb").read()
+    for dt in ("f32", "f16", "bf16"):
+        for hd in (64, 128):
+            assert f"eh_prefill_{dt}_hd{hd}".encode() in pf
 
 
 def test_status_names_and_layout_bytes():

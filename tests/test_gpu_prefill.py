@@ -1,0 +1,253 @@
+"""GPU parity of the MFMA causal chunked prefill against the oracle.
+
+The oracle's prefill_causal restates the reference's causal window
+(flash_attention_2.cu:44-68: query i at p0+i attends keys 0..=p0+i) with the
+f64 sdpa of forward_cpu.rs:424-510, on the exactly widened f32 pool.
+Tolerances: f32 KV max-abs 1e-5; f16 and bf16 KV |gpu - ref| <= 2e-3 +
+1e-3*|ref| (bf16 uses hi+lo operand pairs to meet it).  Shapes: the
+reference's own FA2 test (flash_attention_parity.rs:45-207), ragged chunks on
+scattered pages, GQA groups 1..8, both compiled head sizes, and benchmark
+config 3 (sampled rows at full size).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import orc
+from titan_amd import HipError, KvDataType, PagedKvGpu, PagedKvLayout
+from titan_amd.flash_attention import FlashAttention2
+
+pytestmark = pytest.mark.gpu
+
+TD = {KvDataType.F32: torch.float32, KvDataType.F16: torch.float16,
+      KvDataType.BF16: torch.bfloat16}
+
+
+def i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev)
+
+
+def check_close(gpu, ref, dtype, what=""):
+    gpu, ref = np.asarray(gpu, np.float64), np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(gpu)), what
+    if dtype == KvDataType.F32:
+        err = np.max(np.abs(gpu - ref))
+        assert err <= 1e-5, f"{what}: max abs err {err}"
+    else:
+        bad = np.abs(gpu - ref) > 2e-3 + 1e-3 * np.abs(ref)
+        assert not bad.any(), f"{what}: max abs err {np.max(np.abs(gpu - ref))}"
+
+
+def cosine(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return a @ b / (np.linalg.norm(a) * np.linalg.norm(b))
+
+
+def make_pool(rng, n_blocks, bt, n_kv, hd, dtype, dev):
+    host = rng.standard_normal(n_blocks * bt * 2 * n_kv * hd).astype(np.float32)
+    t = torch.from_numpy(host).to(TD[dtype])
+    return t.to(dev), t.to(torch.float32).numpy()
+
+
+@pytest.mark.parametrize("seq_tokens", [1, 4, 16, 64, 128])
+def test_fa2_reference_shapes(dev, seq_tokens):
+    # flash_attention_parity.rs:45-207: 16/2 heads, hd 128, page 64, pool of 4
+    # pages mapped 0..3, K/V appended through PagedKvGpu, pos_offset 0.
+    nh, nkv, hd, bt = 16, 2, 128, 64
+    layout = PagedKvLayout(4, bt, nkv * hd, KvDataType.F32)
+    pool = torch.zeros(layout.floats_total(), device=dev)
+    table = np.arange(4, dtype=np.uint32)
+    t = np.arange(seq_tokens)[:, None, None]
+    kvh = np.arange(nkv)[None, :, None]
+    hq = np.arange(nh)[None, :, None]
+    d = np.arange(hd)[None, None, :]
+    keys = (np.sin(((t * 100 + kvh * 10 + d).astype(np.float32) * np.float32(0.013)))
+            * np.float32(0.5)).astype(np.float32)
+    vals = (np.cos(((t * 100 + kvh * 10 + d).astype(np.float32) * np.float32(0.017)))
+            * np.float32(0.5)).astype(np.float32)
+    q = (np.sin(((t * 50 + hq * 5 + d).astype(np.float32) * np.float32(0.019)))
+         * np.float32(0.5)).astype(np.float32)
+    PagedKvGpu(0).append_kv(None, layout, pool, torch.from_numpy(keys.reshape(seq_tokens, -1)).to(dev),
+                            torch.from_numpy(vals.reshape(seq_tokens, -1)).to(dev), i32(table, dev),
+                            0, seq_tokens)
+    out = torch.empty((seq_tokens, nh, hd), device=dev)
+    FlashAttention2(0).launch(None, torch.from_numpy(q).to(dev), pool, i32(table, dev), out, nh,
+                              nkv, hd, bt, seq_tokens, 0)
+    torch.cuda.synchronize()
+    ref = orc.prefill_causal(pool.cpu().numpy(), table, bt, q, seq_tokens, 0, nh, nkv, hd)
+    g = out.cpu().numpy()
+    for qp in range(seq_tokens):
+        for h in range(nh):
+            assert cosine(g[qp, h], ref[qp, h]) >= 0.9999
+    check_close(g, ref, KvDataType.F32)
+
+
+CASES = [
+    # (dtype, n_head, n_kv, hd, bt, pos_offset, q_tokens)
+    (KvDataType.F32, 8, 2, 128, 16, 0, 1),
+    (KvDataType.F32, 8, 8, 64, 16, 37, 45),
+    (KvDataType.F32, 14, 2, 64, 16, 511, 1),
+    (KvDataType.F32, 32, 4, 128, 16, 100, 70),
+    (KvDataType.F16, 12, 2, 128, 16, 0, 1),
+    (KvDataType.F16, 12, 2, 128, 16, 3, 5),
+    (KvDataType.F16, 32, 8, 128, 16, 300, 200),
+    (KvDataType.F16, 8, 1, 64, 32, 1000, 33),
+    (KvDataType.F16, 7, 7, 128, 8, 65, 130),
+    (KvDataType.BF16, 32, 8, 128, 16, 0, 1),
+    (KvDataType.BF16, 32, 8, 128, 16, 2, 14),
+    (KvDataType.BF16, 32, 8, 128, 16, 500, 300),
+    (KvDataType.BF16, 16, 2, 64, 16, 64, 64),
+    (KvDataType.BF16, 4, 4, 128, 1, 20, 31),
+    (KvDataType.BF16, 12, 4, 128, 6, 90, 77),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{c[0].name}-{c[1]}x{c[2]}-hd{c[3]}"
+                         f"-bt{c[4]}-p{c[5]}-q{c[6]}")
+def test_chunk_on_scattered_context(dev, case):
+    dtype, nh, nkv, hd, bt, p0, nq = case
+    rng = np.random.default_rng(1000 + CASES.index(case))
+    total = p0 + nq
+    n_pages = -(-total // bt)
+    pool_pages = n_pages + 5
+    table = rng.permutation(pool_pages)[:n_pages].astype(np.uint32)
+    dpool, hpool = make_pool(rng, pool_pages, bt, nkv, hd, dtype, dev)
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    out = torch.full((nq, nh, hd), float("nan"), device=dev)
+    FlashAttention2(0).launch(None, torch.from_numpy(q).to(dev), dpool, i32(table, dev), out, nh,
+                              nkv, hd, bt, nq, p0, kv_dtype=dtype)
+    torch.cuda.synchronize()
+    ref = orc.prefill_causal(hpool, table, bt, q, nq, p0, nh, nkv, hd)
+    check_close(out.cpu().numpy(), ref, dtype, str(case))
+
+
+def test_pos_ptr_overrides_offset(dev):
+    # flash_attention_2.cu:43: a device position replaces the host pos_offset.
+    dtype, nh, nkv, hd, bt = KvDataType.F16, 8, 2, 128, 16
+    rng = np.random.default_rng(7)
+    table = rng.permutation(40).astype(np.uint32)
+    dpool, hpool = make_pool(rng, 40, bt, nkv, hd, dtype, dev)
+    nq = 24
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    fa = FlashAttention2(0)
+    dq, dt = torch.from_numpy(q).to(dev), i32(table, dev)
+    for pos in (0, 17, 200, 40 * bt - nq):
+        pos_t = torch.tensor([pos], dtype=torch.int32, device=dev)
+        out = torch.empty((nq, nh, hd), device=dev)
+        fa.launch_with_pos_ptr(None, dq, dpool, dt, out, nh, nkv, hd, bt, nq, 0, pos_t,
+                               kv_dtype=dtype)
+        torch.cuda.synchronize()
+        ref = orc.prefill_causal(hpool, table, bt, q, nq, pos, nh, nkv, hd)
+        check_close(out.cpu().numpy(), ref, dtype, f"pos {pos}")
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16, KvDataType.F32])
+def test_batched_ragged_chunks(dev, dtype):
+    nh, nkv, hd, bt = 16, 4, 128, 16
+    rng = np.random.default_rng(11 + int(dtype))
+    starts = [0, 5, 130, 1000]
+    lens = [33, 1, 200, 64]
+    stride = max(-(-(s + n) // bt) for s, n in zip(starts, lens)) + 2
+    n_pages = sum(-(-(s + n) // bt) for s, n in zip(starts, lens)) + 3
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    tables = np.full((len(starts), stride), 0xFFFFFFFF, np.uint32)
+    o = 0
+    for b, (s, n) in enumerate(zip(starts, lens)):
+        k = -(-(s + n) // bt)
+        tables[b, :k] = perm[o:o + k]
+        o += k
+    dpool, hpool = make_pool(rng, n_pages, bt, nkv, hd, dtype, dev)
+    total = sum(lens)
+    q = rng.standard_normal((total, nh, hd)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    out = torch.full((total, nh, hd), float("nan"), device=dev)
+    FlashAttention2(0).launch_batched(None, torch.from_numpy(q).to(dev), dpool, i32(tables, dev),
+                                      i32(cu, dev), i32(np.array(starts, np.uint32), dev), out,
+                                      nh, nkv, hd, bt, max(lens), kv_dtype=dtype)
+    torch.cuda.synchronize()
+    g = out.cpu().numpy()
+    for b, (s, n) in enumerate(zip(starts, lens)):
+        k = -(-(s + n) // bt)
+        ref = orc.prefill_causal(hpool, tables[b, :k], bt, q[cu[b]:cu[b + 1]], n, s, nh, nkv, hd)
+        check_close(g[cu[b]:cu[b + 1]], ref, dtype, f"seq {b}")
+
+
+def test_invalid_pages_are_masked(dev):
+    # Entries past the pool mask their keys: the result equals attention over
+    # the remaining keys (a sequence whose first page is invalid).
+    dtype, nh, nkv, hd, bt = KvDataType.F16, 4, 1, 64, 16
+    rng = np.random.default_rng(5)
+    dpool, hpool = make_pool(rng, 8, bt, nkv, hd, dtype, dev)
+    table = np.array([0xFFFFFF, 3, 5], np.uint32)
+    nq, p0 = 8, 40
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    out = torch.empty((nq, nh, hd), device=dev)
+    FlashAttention2(0).launch(None, torch.from_numpy(q).to(dev), dpool, i32(table, dev), out, nh,
+                              nkv, hd, bt, nq, p0, kv_dtype=dtype)
+    torch.cuda.synchronize()
+    # Masking page 0's keys equals attention over keys bt..p0+i, i.e. the
+    # oracle's prefill over the table without its first entry, bt earlier.
+    ref = orc.prefill_causal(hpool, table[1:], bt, q, nq, p0 - bt, nh, nkv, hd)
+    check_close(out.cpu().numpy(), ref, dtype, "masked first page")
+
+
+def test_config3_sampled_rows(dev):
+    """Benchmark config 3 at full size: 8 sequences each append a 512-token
+    chunk onto 2048 cached tokens (32/8 heads, hd 128, page 16, bf16 KV) and
+    run causal prefill over the chunk.  The append is checked bit-exactly by
+    gathering the chunk back; attention is checked on 96 sampled query rows
+    against the oracle (full-size oracle runs take minutes)."""
+    from titan_amd import synth
+    dtype, B, nh, nkv, hd, bt = KvDataType.BF16, 8, 32, 8, 128, 16
+    shape = synth.config3(0)
+    assert (shape.batch, shape.n_head, shape.n_head_kv, shape.head_dim) == (B, nh, nkv, hd)
+    rl = nkv * hd
+    rng = np.random.default_rng(3)
+    tables = synth.block_tables(shape, extra_tokens=512)
+    layout = PagedKvLayout(shape.n_blocks, bt, rl, dtype)
+    dpool, _ = make_pool(rng, shape.n_blocks, bt, nkv, hd, dtype, dev)
+    newk = torch.randn((B * 512, rl), device=dev).to(torch.bfloat16)
+    newv = torch.randn((B * 512, rl), device=dev).to(torch.bfloat16)
+    cu = np.arange(0, B * 512 + 1, 512, dtype=np.uint32)
+    starts = np.full(B, 2048, np.uint32)
+    dtab, dcu, dst = i32(tables, dev), i32(cu, dev), i32(starts, dev)
+    PagedKvGpu(0).append_kv_batched(None, layout, dpool, newk, newv, dtab, dcu, dst, B * 512)
+    q = torch.randn((B * 512, nh, hd), device=dev)
+    out = torch.empty_like(q)
+    FlashAttention2(0).launch_batched(None, q, dpool, dtab, dcu, dst, out, nh, nkv, hd, bt, 512,
+                                      kv_dtype=dtype)
+    torch.cuda.synchronize()
+    hpool = dpool.to(torch.float32).cpu().numpy()
+    # append bit-exactness: the chunk read back through the tables
+    kv = PagedKvGpu(0)
+    for b in (0, B - 1):
+        got = torch.empty((512, rl), device=dev, dtype=torch.bfloat16)
+        kv.read_keys(None, layout, dpool, dtab[b], got, 2048, 512)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), newk[b * 512:(b + 1) * 512].cpu())
+    g = out.cpu().numpy()
+    hq = q.cpu().numpy()
+    picks = np.random.default_rng(9).integers(0, B * 512, size=96)
+    for r in np.concatenate([[0, 511, 512 * 7 + 511], picks]):
+        b, i = divmod(int(r), 512)
+        ref = orc.prefill_causal(hpool, tables[b], bt, hq[r:r + 1], 1, 2048 + i, nh, nkv, hd)
+        check_close(g[r:r + 1], ref, dtype, f"row {r}")
+
+
+def test_validation_errors(dev):
+    fa = FlashAttention2(0)
+    q = torch.zeros((4, 8, 128), device=dev)
+    out = torch.zeros_like(q)
+    pool = torch.zeros(16 * 2 * 2 * 128 * 4, device=dev)
+    table = torch.zeros(1, dtype=torch.int32, device=dev)
+    with pytest.raises(HipError) as e:
+        fa.launch(None, q[:2], pool, table, out, 8, 2, 128, 16, 4, 0)
+    assert e.value.kind == "InvalidSize" and e.value.expected == 4 * 8 * 128 * 4
+    with pytest.raises(HipError) as e:   # table must cover pos_offset + q_tokens
+        fa.launch(None, q, pool, table, out, 8, 2, 128, 16, 4, 13)
+    assert e.value.kind == "InvalidSize" and e.value.expected == 8
+    with pytest.raises(HipError) as e:
+        fa.launch(None, q, pool, table, out, 8, 2, 96, 16, 4, 0)
+    assert e.value.kind == "Unsupported"
+    # zero tokens is a no-op success
+    fa.launch(None, q, pool, table, out, 8, 2, 128, 16, 0, 0)

@@ -9,10 +9,12 @@ from .errors import HipError, KvCacheError
 from .paged_kv import KvDataType, PagedKvGpu, PagedKvLayout
 from .paged_attention import (MAX_ATTN_HEADS, MAX_FLASH_DECODING_SPLITS, MAX_HEAD_DIM,
                               PagedAttention)
+from .flash_attention import FlashAttention2
 from .kvcache import PagedKvCache, PagedKvCacheConfig
 
 __all__ = [
     "HipError", "KvCacheError", "KvDataType", "PagedKvGpu", "PagedKvLayout", "PagedAttention",
+    "FlashAttention2",
     "PagedKvCache", "PagedKvCacheConfig", "MAX_ATTN_HEADS", "MAX_FLASH_DECODING_SPLITS",
     "MAX_HEAD_DIM",
 ]

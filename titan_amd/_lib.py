@@ -44,6 +44,10 @@ _SIGS = {
     "eh_decode_plan": (i32, [u32, u32, u32, u32, u32, u32, u32, u32, P(u32), P(u32), P(u64)]),
     "eh_paged_decode_batched": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, u32, vp, u64,
                                       u32, u32, u32, u32, u32, u32, vp, u64]),
+    "eh_flash_attention_prefill": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64,
+                                         u64, u64, u64, u64, vp]),
+    "eh_prefill_batched": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, vp, u32, u32, u32,
+                                 vp, u64, u32, u32, u32, u32]),
     # host bookkeeping (kv_host.h)
     "eh_kvcache_new": (i32, [u64, u64, u64, u64, u32, P(vp)]),
     "eh_kvcache_destroy": (None, [vp]),

@@ -3,6 +3,7 @@
 Outputs (git-ignored, shipped in-tree to the GPU box):
   titan_amd/lib/paged_kv.hsaco      append / gather / page copy / table kernels
   titan_amd/lib/paged_decode_{f32,f16,bf16}.hsaco  split-K decode attention
+  titan_amd/lib/paged_prefill.hsaco  MFMA causal chunked prefill
   titan_amd/lib/libengine_hip.so    hipModuleLoad / hipModuleLaunchKernel C-ABI
 """
 import os
@@ -23,6 +24,7 @@ KERNELS = [
     ("paged_decode_f32", "paged_decode", ["-DEH_ONLY_DT=0"]),
     ("paged_decode_f16", "paged_decode", ["-DEH_ONLY_DT=1"]),
     ("paged_decode_bf16", "paged_decode", ["-DEH_ONLY_DT=2"]),
+    ("paged_prefill", "paged_prefill", []),
 ]
 
 # Packed-FP32 instructions are disabled for all device code on this pool.

@@ -23,6 +23,7 @@ struct eh_context {
     int device = 0;
     hipModule_t mod_kv = nullptr;
     hipModule_t mod_decode[3] = {nullptr, nullptr, nullptr};  // f32, f16, bf16
+    hipModule_t mod_prefill = nullptr;
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
     // Split-K scratch for eh_flash_decoding, allocated once at creation
@@ -264,6 +265,55 @@ eh_status validate_attention(uint32_t kv_dtype, uint64_t q_bytes, uint64_t pool_
     return EH_OK;
 }
 
+// Compiled prefill head sizes (MFMA tiles need multiples of 32).
+bool prefill_hd(uint64_t hd) { return hd == 64 || hd == 128; }
+
+struct prefill_args {
+    uint32_t kv_dtype;
+    const float* q;
+    const void* pool;
+    uint64_t n_blocks;
+    const uint32_t* bt;
+    uint32_t bt_stride, bt_entries;
+    const uint32_t* cu_q;
+    const uint32_t* start_pos;
+    const uint32_t* pos_ptr;
+    uint32_t q_tokens, pos_offset, batch, max_q;
+    float* out;
+    uint32_t n_head, n_head_kv, head_dim, block_tokens;
+};
+
+// One launch: grid (128-row tiles, kv heads, sequences) of 256 threads.
+eh_status run_prefill(eh_context* c, eh_stream stream, const prefill_args& a) {
+    char name[48];
+    std::snprintf(name, sizeof name, "eh_prefill_%s_hd%u", dt_name(a.kv_dtype), a.head_dim);
+    const uint32_t group = a.n_head / a.n_head_kv;
+    const uint64_t tiles = div_ceil((uint64_t)a.max_q * group, 128);
+    if (tiles > 0x7FFFFFFFull) return invalid_size(0x7FFFFFFFull, tiles, "row tiles");
+    const float scale = 1.0f / std::sqrt((float)a.head_dim);  // flash_attention.rs:166
+    const float scale_log2 = scale * 1.4426950408889634f;
+    const uint32_t row_bytes = a.n_head_kv * a.head_dim * (uint32_t)elt_bytes(a.kv_dtype);
+    return launch(c, c->mod_prefill, name, dim3((uint32_t)tiles, a.n_head_kv, a.batch),
+                  dim3(256), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
+                  a.bt_entries, a.cu_q, a.start_pos, a.pos_ptr, a.q_tokens, a.pos_offset, a.out,
+                  a.n_head, a.n_head_kv, a.block_tokens, log2_exact(a.block_tokens), row_bytes,
+                  scale_log2, a.n_blocks);
+}
+
+// Shape checks shared by the prefill entry points (beyond the reference's
+// size checks, which come first): the kernel set and a pool of >= 1 page.
+eh_status validate_prefill_shape(uint32_t kv_dtype, uint64_t n_head, uint64_t n_head_kv,
+                                 uint64_t head_dim, uint64_t block_tokens, uint64_t pool_bytes) {
+    if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
+    if (!prefill_hd(head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 128, head_dim);
+    const uint64_t page_bytes = block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
+    if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
+    const uint64_t imax = 0x7FFFFFFFull;
+    for (uint64_t v : {n_head, n_head_kv, block_tokens})
+        if (v > imax) return invalid_size(imax, v);
+    return EH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -334,6 +384,12 @@ eh_status eh_create(int device, const char* code_object_dir, eh_context** out) {
             return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_decode)", 0, 0, (int)e);
         }
     }
+    const std::string pf = dir + "/paged_prefill.hsaco";
+    e = hipModuleLoad(&c->mod_prefill, pf.c_str());
+    if (e != hipSuccess) {
+        eh_destroy(c);
+        return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_prefill)", 0, 0, (int)e);
+    }
     e = hipMalloc((void**)&c->scratch, kScratchFloats * sizeof(float));
     if (e != hipSuccess) {
         eh_destroy(c);
@@ -351,6 +407,7 @@ void eh_destroy(eh_context* c) {
     if (c->mod_kv) hipModuleUnload(c->mod_kv);
     for (hipModule_t m : c->mod_decode)
         if (m) hipModuleUnload(m);
+    if (c->mod_prefill) hipModuleUnload(c->mod_prefill);
     delete c;
 }
 
@@ -656,6 +713,101 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     a.part_acc = (float*)ws;
     a.part_ml = (float*)ws + (uint64_t)batch * n_head * max_splits * head_dim;
     return run_decode(c, stream, a);
+}
+
+eh_status eh_flash_attention_prefill(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                     const float* q, uint64_t q_bytes, const void* pool,
+                                     uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes,
+                                     float* out, uint64_t out_bytes, uint64_t n_head,
+                                     uint64_t n_head_kv, uint64_t head_dim, uint64_t block_tokens,
+                                     uint64_t q_tokens, uint64_t pos_offset,
+                                     const uint32_t* pos_ptr) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (n_head < 1) return invalid_size(1, n_head);
+    if (n_head_kv < 1) return invalid_size(1, n_head_kv);
+    if (n_head % n_head_kv != 0) return invalid_size(n_head_kv, n_head % n_head_kv);
+    if (head_dim < 1) return invalid_size(1, head_dim);
+    if (block_tokens < 1) return invalid_size(1, block_tokens);
+    // flash_attention.rs:142-169: q, out, then the block table of
+    // ceil((pos_offset + q_tokens) / block_tokens) entries.
+    const uint64_t q_expected = q_tokens * n_head * head_dim * 4;
+    if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+    if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+    const uint64_t bt_expected = div_ceil(pos_offset + q_tokens, block_tokens) * 4;
+    if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes);
+    eh_status st = validate_prefill_shape(kv_dtype, n_head, n_head_kv, head_dim, block_tokens,
+                                          pool_bytes);
+    if (st) return st;
+    if (q_tokens > 0x7FFFFFFFull) return invalid_size(0x7FFFFFFFull, q_tokens);
+    if (pos_offset > 0xFFFFFFFFull) return invalid_size(0xFFFFFFFFull, pos_offset);
+    if (q_tokens == 0) return EH_OK;
+    st = bind(c);
+    if (st) return st;
+    prefill_args a{};
+    a.kv_dtype = kv_dtype;
+    a.q = q;
+    a.pool = pool;
+    a.n_blocks = pool_bytes / (block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype));
+    a.bt = bt;
+    a.bt_stride = 0;
+    a.bt_entries = (uint32_t)std::min<uint64_t>(bt_bytes / 4, 0xFFFFFFFFull);
+    a.pos_ptr = pos_ptr;
+    a.q_tokens = (uint32_t)q_tokens;
+    a.pos_offset = (uint32_t)pos_offset;
+    a.batch = 1;
+    a.max_q = (uint32_t)q_tokens;
+    a.out = out;
+    a.n_head = (uint32_t)n_head;
+    a.n_head_kv = (uint32_t)n_head_kv;
+    a.head_dim = (uint32_t)head_dim;
+    a.block_tokens = (uint32_t)block_tokens;
+    return run_prefill(c, stream, a);
+}
+
+eh_status eh_prefill_batched(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
+                             uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                             const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                             const uint32_t* cu_q, const uint32_t* start_pos, uint32_t batch,
+                             uint32_t max_q_tokens, uint32_t total_q_tokens, float* out,
+                             uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                             uint32_t head_dim, uint32_t block_tokens) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (n_head < 1) return invalid_size(1, n_head);
+    if (n_head_kv < 1) return invalid_size(1, n_head_kv);
+    if (n_head % n_head_kv != 0) return invalid_size(n_head_kv, n_head % n_head_kv);
+    if (head_dim < 1) return invalid_size(1, head_dim);
+    if (block_tokens < 1) return invalid_size(1, block_tokens);
+    const uint64_t q_expected = (uint64_t)total_q_tokens * n_head * head_dim * 4;
+    if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+    if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
+    eh_status st = validate_prefill_shape(kv_dtype, n_head, n_head_kv, head_dim, block_tokens,
+                                          pool_bytes);
+    if (st) return st;
+    if (batch == 0 || total_q_tokens == 0 || max_q_tokens == 0) return EH_OK;
+    if (!cu_q || !start_pos) return fail(EH_INVALID_ARGS, "cu_q / start_pos is null");
+    st = bind(c);
+    if (st) return st;
+    prefill_args a{};
+    a.kv_dtype = kv_dtype;
+    a.q = q;
+    a.pool = pool;
+    a.n_blocks = pool_bytes / ((uint64_t)block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype));
+    a.bt = bt;
+    a.bt_stride = bt_stride;
+    a.bt_entries = bt_stride;
+    a.cu_q = cu_q;
+    a.start_pos = start_pos;
+    a.q_tokens = total_q_tokens;
+    a.batch = batch;
+    a.max_q = max_q_tokens;
+    a.out = out;
+    a.n_head = n_head;
+    a.n_head_kv = n_head_kv;
+    a.head_dim = head_dim;
+    a.block_tokens = block_tokens;
+    return run_prefill(c, stream, a);
 }
 
 }  // extern "C"

@@ -1,0 +1,482 @@
+// paged_prefill.hip -- causal chunked-prefill attention over paged KV for gfx950.
+//
+// Semantics follow the reference FlashAttention-2 prefill kernel
+// (engine-cuda/kernels/flash_attention_2.cu:22-106, launcher
+// engine-cuda/src/flash_attention.rs:95-225): query i of a chunk sits at
+// global position p0 + i (p0 = pos_offset, or *pos_ptr when given) and
+// attends keys 0..=p0+i of its sequence through the block table, q head qh
+// reading kv head qh / (n_head / n_head_kv); scale 1/sqrt(head_dim); a row
+// with no attended key yields zeros (flash_attention_2.cu:98).
+//
+// Work decomposition (MI355X-first; the reference runs one warp per
+// (q head, query) and re-reads K/V for each):
+//   * one workgroup of 4 waves per (128-row tile, kv head, sequence); the
+//     rows of a tile are (query token, q head of the GQA group) pairs, so one
+//     K/V tile in LDS serves every q head of the group;
+//   * K/V tiles of N keys are gathered through the block table into LDS,
+//     K row-major and V transposed, double-buffered: the global loads of the
+//     next tile are in flight while MFMAs consume the current one;
+//   * each wave owns 32 rows: S^T = K Q^T on 32x32 MFMA tiles, online softmax
+//     in the log2 domain on the accumulator registers (the S^T layout puts one
+//     query row per lane column, so row statistics stay lane-local up to one
+//     exchange between the two lane halves), then O^T += V^T P^T with P taken
+//     straight from registers (keys permuted consistently between P and V^T);
+//   * the accumulators are rescaled only when a row maximum grows by more
+//     than 2^8 (exact: every term uses the same stale maximum);
+//   * operands: f16 KV -> f16 MFMA with f16 Q and P; bf16 KV -> bf16 MFMA
+//     with Q and P each split into hi + lo bf16 parts (two MFMAs per product,
+//     ~16 significant bits, so short contexts stay within 2e-3); f32 KV ->
+//     f32 MFMA (no operand rounding);
+//   * workgroups are mapped XCD-major so the tiles of one (sequence, kv head)
+//     share one XCD's L2.
+// Invalid block-table entries (beyond the table or >= n_blocks) mask their
+// keys instead of reading outside the pool.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+constexpr int NT = 256;           // threads per workgroup (4 waves)
+constexpr uint32_t SLICE = 1024;  // block-table entries staged in LDS at once
+constexpr float RESCALE_LOG2 = 8.0f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int DT> struct op_t;
+template <> struct op_t<DT_F16> {
+    typedef f16x8 v;
+    static constexpr int KS = 16;  // contraction depth of one MFMA
+    static constexpr int ELT = 2;
+    static constexpr bool SPLIT = false;
+    static __device__ __forceinline__ f32x16 mma(v a, v b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct op_t<DT_BF16> {
+    typedef bf16x8 v;
+    static constexpr int KS = 16;
+    static constexpr int ELT = 2;
+    static constexpr bool SPLIT = true;
+    static __device__ __forceinline__ f32x16 mma(v a, v b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct op_t<DT_F32> {
+    typedef float v;
+    static constexpr int KS = 2;
+    static constexpr int ELT = 4;
+    static constexpr bool SPLIT = false;
+    static __device__ __forceinline__ f32x16 mma(v a, v b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+};
+
+// 8 f32 -> MFMA operand (hi part, and lo = x - hi for split types).
+template <int DT>
+__device__ __forceinline__ void pack8(const float* x, typename op_t<DT>::v& hi,
+                                      typename op_t<DT>::v& lo) {
+    if constexpr (DT == DT_F16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hi[e] = (_Float16)x[e];
+    } else if constexpr (DT == DT_BF16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const __bf16 h = (__bf16)x[e];
+            hi[e] = h;
+            lo[e] = (__bf16)(x[e] - (float)h);
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+// Geometry per (type, head_dim): one load item = 4 consecutive keys x 16
+// bytes of a head row; N keys per tile so that the 256 threads own one item.
+template <int DT, int HD>
+struct geo {
+    static constexpr int ELT = op_t<DT>::ELT;
+    static constexpr int EPC = 16 / ELT;          // elements per 16-byte chunk
+    static constexpr int PARTS = HD / EPC;        // chunks per head row
+    static constexpr int N = 4 * NT / PARTS;      // keys per tile
+    static constexpr int SUB = N / 32;            // 32-key sub-blocks per tile
+    static constexpr int KPITCH = HD * ELT + 16;  // bytes per K row in LDS
+    static constexpr int VPITCH = N * ELT + (ELT == 4 ? 16 : 8);  // bytes per V^T row
+    static constexpr int KBYTES = N * KPITCH;
+    static constexpr int VBYTES = HD * VPITCH;
+    static constexpr int STAGE = KBYTES + VBYTES;
+    static_assert(N % 32 == 0 && N >= 32, "tile must hold whole 32-key sub-blocks");
+    static_assert(HD % 32 == 0, "head_dim must be a multiple of 32");
+};
+
+struct lds_hdr {
+    uint32_t tile_bad[2];  // tile index whose keys include an invalid page
+    uint32_t slice_base;
+};
+
+template <int DT, int HD>
+__device__ __forceinline__ void prefill(
+    const float* __restrict__ q, const uint8_t* __restrict__ pool,
+    const uint32_t* __restrict__ bt_all, uint32_t bt_stride, uint32_t bt_entries,
+    const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ start_pos,
+    const uint32_t* __restrict__ pos_ptr, uint32_t q_tokens, uint32_t pos_offset,
+    float* __restrict__ out, uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens,
+    int bt_shift, uint32_t row_bytes, float scale_log2, uint64_t n_blocks, uint8_t* smem) {
+    typedef op_t<DT> O;
+    typedef typename O::v opv;
+    typedef geo<DT, HD> Gm;
+    constexpr int N = Gm::N;
+
+    // ---- XCD-major workgroup order: consecutive ids of one (sequence, kv
+    // head) land on one XCD (dispatch is round-robin over 8 XCDs).
+    const uint32_t gx = gridDim.x, gy = gridDim.y;
+    const uint32_t total = gx * gy * gridDim.z;
+    uint32_t lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    if ((total & 7u) == 0u) lin = (lin & 7u) * (total >> 3) + (lin >> 3);
+    const uint32_t tile = lin % gx;
+    const uint32_t hk = (lin / gx) % gy;
+    const uint32_t b = lin / (gx * gy);
+
+    uint32_t qoff, n_q, p0;
+    const uint32_t* bt;
+    if (cu_q) {  // ragged batch; q_tokens is the total row count of q / out
+        qoff = min(cu_q[b], q_tokens);
+        const uint32_t end = min(cu_q[b + 1], q_tokens);
+        n_q = end > qoff ? end - qoff : 0u;
+        p0 = start_pos[b];
+        bt = bt_all + (uint64_t)b * bt_stride;
+    } else {
+        qoff = 0;
+        n_q = q_tokens;
+        p0 = pos_ptr ? pos_ptr[0] : pos_offset;
+        bt = bt_all;
+    }
+    const uint32_t group = n_head / n_head_kv;
+    const uint32_t rows = n_q * group;
+    const uint32_t row0 = tile * 128u;
+    if (row0 >= rows) return;  // uniform over the workgroup
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int h = lane >> 5;
+
+    // ---- this lane's query row (column of S^T / O^T)
+    const uint32_t row_raw = row0 + wave * 32 + l32;
+    const bool row_ok = row_raw < rows;
+    const uint32_t row = row_ok ? row_raw : rows - 1u;
+    const uint32_t tok = row / group;
+    const uint32_t head = hk * group + (row - tok * group);
+    // Key positions are capped at the block table's capacity: keys past it
+    // have no page (masked), and the cap bounds the loop for any device-side
+    // position.
+    const uint64_t cap = (uint64_t)bt_entries * block_tokens - 1u;
+    auto clamp_pos = [&](uint32_t t) -> uint32_t {
+        const uint64_t v = (uint64_t)p0 + t;
+        return (uint32_t)(v < cap ? v : cap);
+    };
+    const uint32_t lim = clamp_pos(tok);  // attends keys <= lim
+    // wave / workgroup bounds (rows are ordered by token)
+    const uint32_t wr0 = min(row0 + wave * 32u, rows - 1u);
+    const uint32_t wr1 = min(row0 + wave * 32u + 31u, rows - 1u);
+    const uint32_t wave_min = clamp_pos(wr0 / group);
+    const uint32_t wave_max = clamp_pos(wr1 / group);
+    const uint32_t kmax = clamp_pos(min(row0 + 127u, rows - 1u) / group);  // workgroup bound
+    const uint32_t n_tiles = kmax / N + 1u;
+
+    // ---- LDS carve-up
+    lds_hdr* hdr = reinterpret_cast<lds_hdr*>(smem);
+    uint32_t* slice = reinterpret_cast<uint32_t*>(smem + 64);
+    uint8_t* kflag = smem + 64 + SLICE * 4;                 // [2][N] key valid bytes
+    uint8_t* stage = smem + 64 + SLICE * 4 + 2 * 128;       // [2][STAGE]
+
+    auto entry_of = [&](uint32_t key) -> uint32_t {
+        return bt_shift >= 0 ? (key >> bt_shift) : key / block_tokens;
+    };
+    auto stage_slice = [&](uint32_t base) {
+        for (uint32_t i = tid; i < SLICE; i += NT) {
+            const uint32_t e = base + i;
+            uint32_t v = 0xFFFFFFFFu;
+            if (e < bt_entries) {
+                const uint32_t p = bt[e];
+                if ((uint64_t)p < n_blocks) v = p;
+            }
+            slice[i] = v;
+        }
+        if (tid == 0) hdr->slice_base = base;
+    };
+
+    // ---- load item of this thread: keys 4*kg .. 4*kg+3 of a tile, chunk `part`
+    const int part = tid % Gm::PARTS;
+    const int kg = tid / Gm::PARTS;
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2u * row_bytes;
+    const uint32_t head_off = hk * HD * Gm::ELT + part * 16;
+    uint4 kr[4], vr[4];
+    uint32_t okbits = 0;  // bit j: key 4*kg+j loadable; bit 4+j: key <= kmax with a bad page
+
+    auto issue = [&](uint32_t t) {
+        const uint32_t base = hdr->slice_base;
+        okbits = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t key = t * N + 4 * kg + j;
+            const uint32_t e = entry_of(key);
+            const uint32_t phys = slice[e - base];
+            const uint32_t slot = key - e * block_tokens;
+            const bool live = key <= kmax;
+            const bool ok = live && phys != 0xFFFFFFFFu;
+            okbits |= (ok ? 1u : 0u) << j;
+            okbits |= (live && !ok ? 1u : 0u) << (4 + j);
+            const uint8_t* p = ok ? pool + (uint64_t)phys * page_bytes +
+                                        (uint64_t)slot * (2u * row_bytes) + head_off
+                                  : pool;
+            kr[j] = *reinterpret_cast<const uint4*>(p);
+            vr[j] = *reinterpret_cast<const uint4*>(p + (ok ? row_bytes : 0u));
+        }
+    };
+
+    auto commit = [&](uint32_t t, int buf) {
+        uint8_t* ks = stage + buf * Gm::STAGE;
+        uint8_t* vs = ks + Gm::KBYTES;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (!((okbits >> j) & 1u)) {
+                kr[j] = make_uint4(0, 0, 0, 0);
+                vr[j] = make_uint4(0, 0, 0, 0);
+            }
+            *reinterpret_cast<uint4*>(ks + (4 * kg + j) * Gm::KPITCH + part * 16) = kr[j];
+        }
+        if constexpr (Gm::ELT == 2) {
+            // V^T rows: element d of the chunk, 4 keys -> 8 bytes
+            const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
+            const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+            const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
+            const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint2 ev, od;
+                ev.x = perm(w1[i], w0[i], 0x05040100u);
+                ev.y = perm(w3[i], w2[i], 0x05040100u);
+                od.x = perm(w1[i], w0[i], 0x07060302u);
+                od.y = perm(w3[i], w2[i], 0x07060302u);
+                const int d = part * 8 + 2 * i;
+                *reinterpret_cast<uint2*>(vs + d * Gm::VPITCH + 4 * kg * 2) = ev;
+                *reinterpret_cast<uint2*>(vs + (d + 1) * Gm::VPITCH + 4 * kg * 2) = od;
+            }
+        } else {
+            const uint32_t w[4][4] = {{vr[0].x, vr[0].y, vr[0].z, vr[0].w},
+                                      {vr[1].x, vr[1].y, vr[1].z, vr[1].w},
+                                      {vr[2].x, vr[2].y, vr[2].z, vr[2].w},
+                                      {vr[3].x, vr[3].y, vr[3].z, vr[3].w}};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = part * 4 + i;
+                *reinterpret_cast<uint4*>(vs + d * Gm::VPITCH + 4 * kg * 4) =
+                    make_uint4(w[0][i], w[1][i], w[2][i], w[3][i]);
+            }
+        }
+        if (part == 0) {
+            uint32_t f = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f |= ((okbits >> j) & 1u) << (8 * j);
+            *reinterpret_cast<uint32_t*>(kflag + buf * 128 + 4 * kg) = f;
+        }
+        if (okbits >> 4) hdr->tile_bad[buf] = t;
+    };
+
+    // ---- Q operands for this lane's row: contraction index mapping
+    //   16-bit: step t, half h -> dims 16t + 8h + e (e < 8)
+    //   f32:    step t = 4u + e, half h -> dim 8u + 4h + e
+    constexpr int QSTEPS = HD / O::KS;
+    opv qa[QSTEPS], qb[O::SPLIT ? QSTEPS : 1];
+    {
+        const float* qrow = q + ((uint64_t)(qoff + tok) * n_head + head) * HD;
+        if constexpr (Gm::ELT == 2) {
+#pragma unroll
+            for (int t = 0; t < QSTEPS; ++t) {
+                const float4 a = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h);
+                const float4 c = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h + 4);
+                const float x[8] = {a.x * scale_log2, a.y * scale_log2, a.z * scale_log2,
+                                    a.w * scale_log2, c.x * scale_log2, c.y * scale_log2,
+                                    c.z * scale_log2, c.w * scale_log2};
+                pack8<DT>(x, qa[t], qb[O::SPLIT ? t : 0]);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < HD / 8; ++u) {
+                const float4 a = *reinterpret_cast<const float4*>(qrow + 8 * u + 4 * h);
+                qa[4 * u + 0] = a.x * scale_log2;
+                qa[4 * u + 1] = a.y * scale_log2;
+                qa[4 * u + 2] = a.z * scale_log2;
+                qa[4 * u + 3] = a.w * scale_log2;
+            }
+        }
+    }
+
+    f32x16 acc[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) acc[i] = f32x16{};
+    float m_run = -1e30f, l_run = 0.f;
+
+    // ---- prologue
+    if (tid == 0) { hdr->tile_bad[0] = 0xFFFFFFFFu; hdr->tile_bad[1] = 0xFFFFFFFFu; }
+    stage_slice(0);
+    __syncthreads();
+    issue(0);
+
+    for (uint32_t j = 0; j < n_tiles; ++j) {
+        const int buf = j & 1;
+        commit(j, buf);
+        if (j + 1 < n_tiles) {
+            const uint32_t e_last = entry_of((j + 1) * N + N - 1);
+            if (e_last >= hdr->slice_base + SLICE) {  // uniform
+                __syncthreads();
+                stage_slice(entry_of((j + 1) * N));
+            }
+        }
+        __syncthreads();
+        if (j + 1 < n_tiles) issue(j + 1);
+
+        const uint8_t* ks = stage + buf * Gm::STAGE;
+        const uint8_t* vs = ks + Gm::KBYTES;
+        const bool bad = hdr->tile_bad[buf] == j;
+#pragma unroll
+        for (int sb = 0; sb < Gm::SUB; ++sb) {
+            const uint32_t kb = j * N + sb * 32;
+            if (kb > wave_max) break;
+            // S^T (32 keys x 32 rows) = K Q^T
+            f32x16 s = f32x16{};
+            const uint8_t* krow = ks + (sb * 32 + l32) * Gm::KPITCH;
+            if constexpr (Gm::ELT == 2) {
+#pragma unroll
+                for (int t = 0; t < QSTEPS; ++t) {
+                    const opv a = *reinterpret_cast<const opv*>(krow + (16 * t + 8 * h) * 2);
+                    s = O::mma(a, qa[t], s);
+                    if constexpr (O::SPLIT) s = O::mma(a, qb[t], s);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < HD / 8; ++u) {
+                    const float4 a = *reinterpret_cast<const float4*>(krow + (8 * u + 4 * h) * 4);
+                    s = O::mma(a.x, qa[4 * u + 0], s);
+                    s = O::mma(a.y, qa[4 * u + 1], s);
+                    s = O::mma(a.z, qa[4 * u + 2], s);
+                    s = O::mma(a.w, qa[4 * u + 3], s);
+                }
+            }
+            // causal / page mask; key of register r: kb + 8(r/4) + 4h + r%4
+            if (bad || kb + 31u > wave_min) {
+                const uint8_t* fl = kflag + buf * 128 + sb * 32;
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int ko = 8 * g4 + 4 * h;
+                    const uint32_t f = bad ? *reinterpret_cast<const uint32_t*>(fl + ko) : 0x01010101u;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool ok = (kb + ko + e <= lim) && ((f >> (8 * e)) & 1u);
+                        s[4 * g4 + e] = ok ? s[4 * g4 + e] : -__builtin_inff();
+                    }
+                }
+            }
+            float mx = s[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            if (__builtin_amdgcn_ballot_w64(mx > m_run + RESCALE_LOG2)) {
+                const float mn = fmaxf(m_run, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+                l_run *= alpha;
+#pragma unroll
+                for (int i = 0; i < HD / 32; ++i) acc[i] *= alpha;
+                m_run = mn;
+            }
+            float p[16];
+            float ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                p[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
+                ps += p[r];
+            }
+            l_run += ps;
+            // O^T (HD x 32 rows) += V^T P^T
+            if constexpr (Gm::ELT == 2) {
+                opv pa[2], pb[2];
+                pack8<DT>(p, pa[0], pb[0]);
+                pack8<DT>(p + 8, pa[1], pb[1]);
+#pragma unroll
+                for (int db = 0; db < HD / 32; ++db) {
+                    const uint8_t* vrow = vs + (db * 32 + l32) * Gm::VPITCH + (sb * 32) * 2;
+#pragma unroll
+                    for (int st = 0; st < 2; ++st) {
+                        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + (16 * st + 4 * h) * 2);
+                        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + (16 * st + 8 + 4 * h) * 2);
+                        const uint4 w = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+                        const opv a = __builtin_bit_cast(opv, w);
+                        acc[db] = O::mma(a, pa[st], acc[db]);
+                        if constexpr (O::SPLIT) acc[db] = O::mma(a, pb[st], acc[db]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int db = 0; db < HD / 32; ++db) {
+                    const uint8_t* vrow = vs + (db * 32 + l32) * Gm::VPITCH + (sb * 32) * 4;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float4 a = *reinterpret_cast<const float4*>(vrow + (8 * u + 4 * h) * 4);
+                        acc[db] = O::mma(a.x, p[4 * u + 0], acc[db]);
+                        acc[db] = O::mma(a.y, p[4 * u + 1], acc[db]);
+                        acc[db] = O::mma(a.z, p[4 * u + 2], acc[db]);
+                        acc[db] = O::mma(a.w, p[4 * u + 3], acc[db]);
+                    }
+                }
+            }
+        }
+    }
+
+    // ---- epilogue: combine the two halves' sums, normalise, store
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    if (row_ok) {
+        float* orow = out + ((uint64_t)(qoff + tok) * n_head + head) * HD;
+#pragma unroll
+        for (int db = 0; db < HD / 32; ++db) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = db * 32 + 8 * g4 + 4 * h;
+                *reinterpret_cast<float4*>(orow + d) =
+                    make_float4(acc[db][4 * g4 + 0] * inv, acc[db][4 * g4 + 1] * inv,
+                                acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+#define EH_PREFILL(DTN, DT, HD)                                                                   \
+    extern "C" __global__ __launch_bounds__(NT, 2) void eh_prefill_##DTN##_hd##HD(              \
+        const float* q, const uint8_t* pool, const uint32_t* bt, uint32_t bt_stride,             \
+        uint32_t bt_entries, const uint32_t* cu_q, const uint32_t* start_pos,                    \
+        const uint32_t* pos_ptr, uint32_t q_tokens, uint32_t pos_offset, float* out,             \
+        uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens, int bt_shift,                \
+        uint32_t row_bytes, float scale_log2, uint64_t n_blocks) {                               \
+        constexpr int BYTES = 64 + SLICE * 4 + 2 * 128 + 2 * geo<DT, HD>::STAGE;                 \
+        __shared__ __attribute__((aligned(16))) uint8_t smem[BYTES];                             \
+        prefill<DT, HD>(q, pool, bt, bt_stride, bt_entries, cu_q, start_pos, pos_ptr, q_tokens,  \
+                        pos_offset, out, n_head, n_head_kv, block_tokens, bt_shift, row_bytes,   \
+                        scale_log2, n_blocks, smem);                                             \
+    }
+
+EH_PREFILL(f16, DT_F16, 64)
+EH_PREFILL(f16, DT_F16, 128)
+EH_PREFILL(bf16, DT_BF16, 64)
+EH_PREFILL(bf16, DT_BF16, 128)
+EH_PREFILL(f32, DT_F32, 64)
+EH_PREFILL(f32, DT_F32, 128)

@@ -66,6 +66,18 @@ def config2(seed=0, extra_tokens=64):
     return DecodeShape(32, 12, 2, 128, 16, KvDataType.F16, lens, n_blocks, perm, {"seed": seed})
 
 
+def config3(seed=0, chunk=512, cached=2048):
+    """B=8, 32/8 heads, hd 128, page 16, bf16: each sequence holds `cached`
+    tokens and appends a `chunk`-token prefill chunk.  Pool = ceil(1.2 x the
+    pages the chunks end on), seeded shuffled free list."""
+    rng = np.random.default_rng(seed)
+    need = 8 * ((cached + chunk + 15) // 16)
+    n_blocks = int(np.ceil(1.2 * need))
+    perm = rng.permutation(n_blocks).astype(np.uint32)
+    return DecodeShape(8, 32, 8, 128, 16, KvDataType.BF16, np.full(8, cached, dtype=np.int64),
+                       n_blocks, perm, {"seed": seed, "chunk": chunk})
+
+
 def config5(seed=0, n_blocks=None, batch=4, ctx=32768):
     """B=4 at 32768 tokens, 32/8 heads, hd 128, page 16, f16.  Pages scattered
     by a seeded permutation over `n_blocks` pages."""
