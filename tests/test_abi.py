@@ -18,7 +18,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_symbols():
     names = set()
-    for h in ("engine_hip.h", "kv_host.h"):
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
         text = open(os.path.join(ROOT, "include", h)).read()
         names |= set(re.findall(r"\b(eh_\w+)\s*\(", text))
     return names

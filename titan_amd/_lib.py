@@ -23,6 +23,11 @@ class eh_kv_layout(C.Structure):
                 ("data_type", u32), ("reserved", u32)]
 
 
+class eh_stream_cfg(C.Structure):
+    _fields_ = [("sink_tokens", u64), ("recent_window_tokens", u64), ("max_budget_tokens", u64),
+                ("block_tokens", u64)]
+
+
 _SIGS = {
     "eh_create": (i32, [i32, C.c_char_p, P(vp)]),
     "eh_destroy": (None, [vp]),
@@ -63,6 +68,40 @@ _SIGS = {
     "eh_kvcache_block_table": (i64, [vp, u64, vp, u64]),
     "eh_kvcache_reserve": (i32, [vp, u64, u64, P(u64)]),
     "eh_kvcache_export_tables": (i32, [vp, vp, u64, vp, u64, vp]),
+    # prefix sharing (kv_share.h)
+    "eh_cow_new": (vp, []),
+    "eh_cow_fork": (vp, [vp]),
+    "eh_cow_destroy": (None, [vp]),
+    "eh_cow_append_block": (None, [vp, u32]),
+    "eh_cow_is_shared": (i32, [vp, u64]),
+    "eh_cow_tail_needs_cow": (i32, [vp]),
+    "eh_cow_perform_tail_cow": (None, [vp, u32]),
+    "eh_cow_block_ids": (u64, [vp, vp, u64]),
+    "eh_cow_len": (u64, [vp]),
+    "eh_cow_is_dirty": (i32, [vp, u64]),
+    "eh_cow_ref_count": (u64, [vp, u64]),
+    "eh_cow_seq_len": (u64, [vp]),
+    "eh_cow_set_seq_len": (None, [vp, u64]),
+    "eh_radix_new": (vp, [u64]),
+    "eh_radix_destroy": (None, [vp]),
+    "eh_radix_match_prefix": (u64, [vp, vp, u64, vp, u64, P(u64)]),
+    "eh_radix_insert": (None, [vp, vp, u64, vp, u64, i32]),
+    "eh_radix_evict_lru": (u64, [vp, u64, vp, u64]),
+    "eh_radix_total_cached_blocks": (u64, [vp]),
+    "eh_radix_invalidate_physical_blocks": (None, [vp, vp, u64]),
+    "eh_radix_set_ref_count": (i32, [vp, vp, u64, u64]),
+    "eh_stream_cfg_new": (eh_stream_cfg, [u64, u64, u64, u64]),
+    "eh_stream_cfg_default": (eh_stream_cfg, []),
+    "eh_stream_sink_blocks": (u64, [eh_stream_cfg]),
+    "eh_stream_recent_blocks": (u64, [eh_stream_cfg]),
+    "eh_stream_max_active_blocks": (u64, [eh_stream_cfg]),
+    "eh_stream_new": (vp, [eh_stream_cfg]),
+    "eh_stream_destroy": (None, [vp]),
+    "eh_stream_record_attention_mass": (None, [vp, u32, f32]),
+    "eh_stream_scores_len": (u64, [vp]),
+    "eh_stream_score": (f32, [vp, u32]),
+    "eh_stream_prune_blocks": (None, [vp, vp, u64, vp, P(u64), vp, P(u64)]),
+    "eh_compaction_plan": (i64, [vp, u64, vp, u64, u32, vp, vp, vp]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -75,6 +75,7 @@ def build(verbose=False):
         "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
         os.path.join(CSRC, "engine_hip.cpp"), os.path.join(CSRC, "kv_host.cpp"),
+        os.path.join(CSRC, "kv_share.cpp"),
         "-o", host_out + ".tmp", f"-L{ROCM}/lib", "-lamdhip64", "-ldl",
         f"-Wl,-rpath,{ROCM}/lib",
     ]))

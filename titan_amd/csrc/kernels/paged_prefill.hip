@@ -108,6 +108,10 @@ struct geo {
     static constexpr int SUB = N / 32;            // 32-key sub-blocks per tile
     static constexpr int KPITCH = HD * ELT + 16;  // bytes per K row in LDS
     static constexpr int VPITCH = N * ELT + (ELT == 4 ? 16 : 8);  // bytes per V^T row
+    // V^T rows hold N/4 groups of 4 keys; group g of row d is stored at
+    // g ^ (row block of d) so that the transposing stores spread over banks.
+    static constexpr int GMASK = N / 4 - 1;
+    static constexpr int GBYTES = 4 * ELT;
     static constexpr int KBYTES = N * KPITCH;
     static constexpr int VBYTES = HD * VPITCH;
     static constexpr int STAGE = KBYTES + VBYTES;
@@ -164,7 +168,7 @@ __device__ __forceinline__ void prefill(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int h = lane >> 5;
 
@@ -221,24 +225,45 @@ __device__ __forceinline__ void prefill(
     uint4 kr[4], vr[4];
     uint32_t okbits = 0;  // bit j: key 4*kg+j loadable; bit 4+j: key <= kmax with a bad page
 
+    const uint32_t slot_bytes = 2u * row_bytes;
+    const bool page4 = (block_tokens & 3u) == 0u;  // 4 aligned keys share a page
     auto issue = [&](uint32_t t) {
         const uint32_t base = hdr->slice_base;
+        const uint32_t key0 = t * N + 4 * kg;
         okbits = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t key = t * N + 4 * kg + j;
-            const uint32_t e = entry_of(key);
+        if (page4) {
+            const uint32_t e = entry_of(key0);
             const uint32_t phys = slice[e - base];
-            const uint32_t slot = key - e * block_tokens;
-            const bool live = key <= kmax;
-            const bool ok = live && phys != 0xFFFFFFFFu;
-            okbits |= (ok ? 1u : 0u) << j;
-            okbits |= (live && !ok ? 1u : 0u) << (4 + j);
-            const uint8_t* p = ok ? pool + (uint64_t)phys * page_bytes +
-                                        (uint64_t)slot * (2u * row_bytes) + head_off
-                                  : pool;
-            kr[j] = *reinterpret_cast<const uint4*>(p);
-            vr[j] = *reinterpret_cast<const uint4*>(p + (ok ? row_bytes : 0u));
+            const uint32_t slot = key0 - e * block_tokens;
+            const bool pv = phys != 0xFFFFFFFFu;
+            const uint8_t* p = pool + (uint64_t)(pv ? phys : 0u) * page_bytes +
+                               (uint64_t)(pv ? slot * slot_bytes + head_off : 0u);
+            const uint32_t step = pv ? slot_bytes : 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool live = key0 + j <= kmax;
+                okbits |= (live && pv ? 1u : 0u) << j;
+                okbits |= (live && !pv ? 1u : 0u) << (4 + j);
+                kr[j] = *reinterpret_cast<const uint4*>(p + j * step);
+                vr[j] = *reinterpret_cast<const uint4*>(p + j * step + (pv ? row_bytes : 0u));
+            }
+        } else {
+            uint32_t phys[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) phys[j] = slice[entry_of(key0 + j) - base];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t key = key0 + j;
+                const uint32_t slot = key - entry_of(key) * block_tokens;
+                const bool live = key <= kmax;
+                const bool pv = phys[j] != 0xFFFFFFFFu;
+                okbits |= (live && pv ? 1u : 0u) << j;
+                okbits |= (live && !pv ? 1u : 0u) << (4 + j);
+                const uint8_t* p = pool + (uint64_t)(pv ? phys[j] : 0u) * page_bytes +
+                                   (uint64_t)(pv ? slot * slot_bytes + head_off : 0u);
+                kr[j] = *reinterpret_cast<const uint4*>(p);
+                vr[j] = *reinterpret_cast<const uint4*>(p + (pv ? row_bytes : 0u));
+            }
         }
     };
 
@@ -247,9 +272,12 @@ __device__ __forceinline__ void prefill(
         uint8_t* vs = ks + Gm::KBYTES;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            if (!((okbits >> j) & 1u)) {
-                kr[j] = make_uint4(0, 0, 0, 0);
-                vr[j] = make_uint4(0, 0, 0, 0);
+            if (okbits != 0xFu) {  // rare: keys past the window or on a bad page
+                const bool z = !((okbits >> j) & 1u);
+                vr[j].x = z ? 0u : vr[j].x;
+                vr[j].y = z ? 0u : vr[j].y;
+                vr[j].z = z ? 0u : vr[j].z;
+                vr[j].w = z ? 0u : vr[j].w;
             }
             *reinterpret_cast<uint4*>(ks + (4 * kg + j) * Gm::KPITCH + part * 16) = kr[j];
         }
@@ -267,8 +295,9 @@ __device__ __forceinline__ void prefill(
                 od.x = perm(w1[i], w0[i], 0x07060302u);
                 od.y = perm(w3[i], w2[i], 0x07060302u);
                 const int d = part * 8 + 2 * i;
-                *reinterpret_cast<uint2*>(vs + d * Gm::VPITCH + 4 * kg * 2) = ev;
-                *reinterpret_cast<uint2*>(vs + (d + 1) * Gm::VPITCH + 4 * kg * 2) = od;
+                const int col = (kg ^ (part & Gm::GMASK)) * Gm::GBYTES;  // d >> 3 == part
+                *reinterpret_cast<uint2*>(vs + d * Gm::VPITCH + col) = ev;
+                *reinterpret_cast<uint2*>(vs + (d + 1) * Gm::VPITCH + col) = od;
             }
         } else {
             const uint32_t w[4][4] = {{vr[0].x, vr[0].y, vr[0].z, vr[0].w},
@@ -278,7 +307,8 @@ __device__ __forceinline__ void prefill(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int d = part * 4 + i;
-                *reinterpret_cast<uint4*>(vs + d * Gm::VPITCH + 4 * kg * 4) =
+                const int col = (kg ^ (part & Gm::GMASK)) * Gm::GBYTES;  // d >> 2 == part
+                *reinterpret_cast<uint4*>(vs + d * Gm::VPITCH + col) =
                     make_uint4(w[0][i], w[1][i], w[2][i], w[3][i]);
             }
         }
@@ -412,11 +442,14 @@ __device__ __forceinline__ void prefill(
                 pack8<DT>(p + 8, pa[1], pb[1]);
 #pragma unroll
                 for (int db = 0; db < HD / 32; ++db) {
-                    const uint8_t* vrow = vs + (db * 32 + l32) * Gm::VPITCH + (sb * 32) * 2;
+                    const int d = db * 32 + l32;
+                    const uint8_t* vrow = vs + d * Gm::VPITCH;
+                    const int sw = (d >> 3) & Gm::GMASK;
 #pragma unroll
                     for (int st = 0; st < 2; ++st) {
-                        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + (16 * st + 4 * h) * 2);
-                        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + (16 * st + 8 + 4 * h) * 2);
+                        const int g = sb * 8 + 4 * st + h;  // keys 16st+4h.. and 16st+8+4h..
+                        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + (g ^ sw) * Gm::GBYTES);
+                        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + ((g + 2) ^ sw) * Gm::GBYTES);
                         const uint4 w = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
                         const opv a = __builtin_bit_cast(opv, w);
                         acc[db] = O::mma(a, pa[st], acc[db]);
@@ -426,10 +459,13 @@ __device__ __forceinline__ void prefill(
             } else {
 #pragma unroll
                 for (int db = 0; db < HD / 32; ++db) {
-                    const uint8_t* vrow = vs + (db * 32 + l32) * Gm::VPITCH + (sb * 32) * 4;
+                    const int d = db * 32 + l32;
+                    const uint8_t* vrow = vs + d * Gm::VPITCH;
+                    const int sw = (d >> 2) & Gm::GMASK;
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
-                        const float4 a = *reinterpret_cast<const float4*>(vrow + (8 * u + 4 * h) * 4);
+                        const int g = sb * 8 + 2 * u + h;  // keys 8u+4h..
+                        const float4 a = *reinterpret_cast<const float4*>(vrow + (g ^ sw) * Gm::GBYTES);
                         acc[db] = O::mma(a.x, p[4 * u + 0], acc[db]);
                         acc[db] = O::mma(a.y, p[4 * u + 1], acc[db]);
                         acc[db] = O::mma(a.z, p[4 * u + 2], acc[db]);
