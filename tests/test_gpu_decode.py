@@ -148,6 +148,41 @@ def test_batched_decode_ragged(dev, dtype):
         check_close(out.cpu().numpy(), ref, dtype)
 
 
+SHAPES = [  # (n_head, n_kv, head_dim, block_tokens): every slot-major head grouping,
+    (8, 8, 128, 16), (16, 8, 64, 16), (6, 2, 64, 16), (4, 1, 128, 32), (8, 1, 128, 16),
+    (14, 2, 128, 16), (24, 2, 128, 8), (32, 1, 64, 16), (64, 2, 128, 16), (10, 2, 64, 16),
+    (12, 4, 128, 1), (12, 3, 128, 16), (12, 4, 128, 6), (8, 2, 32, 16)]  # ... and fallbacks
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_batched_decode_head_groupings(dev, dtype, shape):
+    n_head, n_kv, hd, bt = shape
+    rng = np.random.default_rng(sum(shape))
+    lens = np.array([0, 1, 33, 250, 700], np.int64)
+    stride = int(max((l + bt - 1) // bt for l in lens))
+    nb = int(sum((l + bt - 1) // bt for l in lens)) + 3
+    perm = rng.permutation(nb).astype(np.uint32)
+    tab = np.full((len(lens), stride), 0xFFFFFFFF, np.uint32)
+    pos = 0
+    for b, l in enumerate(lens):
+        c = (int(l) + bt - 1) // bt
+        tab[b, :c] = perm[pos:pos + c]
+        pos += c
+    pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, dtype, dev)
+    q = rng.standard_normal((len(lens), n_head, hd)).astype(np.float32)
+    ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
+    pa = PagedAttention(0)
+    for tps in (0, 128):
+        plan = PagedAttention.plan(len(lens), n_head, n_kv, hd, bt, int(lens.max()), tps, dtype)
+        ws = PagedAttention.workspace(plan)
+        out = torch.full((len(lens), n_head, hd), float("nan"), device=dev)
+        pa.decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                          i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, plan, ws)
+        torch.cuda.synchronize()
+        check_close(out.cpu().numpy(), ref, dtype)
+
+
 def test_config1_append_then_decode(dev):
     """Benchmark config 1: f32, B=1, 14/2 heads, hd 64, page 16; 511 cached
     tokens + 1 appended token (512 attended) on the first 32 pages of a seeded

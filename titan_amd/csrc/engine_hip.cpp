@@ -171,7 +171,9 @@ uint64_t decode_ws_floats(uint64_t rows, uint64_t max_splits, uint64_t head_dim)
 }
 
 // Largest split that keeps a workgroup's block-table slice inside LDS.
-uint64_t max_tps(uint64_t block_tokens) { return (kBtSlice - 2) * block_tokens; }
+uint64_t max_tps(uint64_t block_tokens, uint64_t chunk = 1) {
+    return std::max<uint64_t>((kBtSlice - 2) * block_tokens / chunk, 1) * chunk;
+}
 
 // Tokens one decode workgroup walks per unrolled chunk (mirrors the kernel:
 // 16-byte lane vectors, 4 waves, 16 wave steps capped at 512 tokens).
@@ -182,6 +184,53 @@ uint64_t chunk_tokens(uint32_t kv_dtype, uint64_t head_dim) {
     const uint64_t nw = kDecodeThreads / 64;
     const uint64_t steps = std::max<uint64_t>(1, std::min<uint64_t>(16, 512 / (nw * tpw)));
     return nw * tpw * steps;
+}
+
+// Which split kernel serves a decode shape, and its work granularity.
+//   slot-major (eh_decode_slots_*): 16-bit KV, head_dim 64/128, power-of-two
+//     pages and at most 8 kv heads (a power of two); one workgroup serves
+//     every kv head, lanes split a group's q heads into head groups of gh;
+//   head-major (eh_decode_split_*): everything else; one workgroup per kv head.
+struct decode_kernel {
+    bool slots = false;
+    uint32_t gh = 1, hgr = 1, tpi = 1;  // slot-major: heads per lane, head groups, tokens per step
+    uint32_t g = 1;                     // head-major: compiled head-group width
+    uint32_t chunks = 1;                // workgroups per (split, sequence) along the heads
+    uint64_t chunk = 1;                 // tokens one workgroup walks per unrolled chunk
+    uint64_t units = 1;                 // workgroups per (split, sequence)
+};
+
+constexpr uint32_t kSlotSteps = 16;  // mirrors SLOT_STEPS in paged_decode.hip
+
+decode_kernel pick_decode_kernel(uint32_t kv_dtype, uint64_t head_dim, uint64_t n_head,
+                                 uint64_t n_head_kv, uint64_t block_tokens) {
+    decode_kernel k;
+    const uint32_t group = (uint32_t)(n_head / n_head_kv);
+    const bool pow2_kv = n_head_kv && !(n_head_kv & (n_head_kv - 1));
+    const bool pow2_bt = block_tokens && !(block_tokens & (block_tokens - 1));
+    if ((kv_dtype == EH_KV_F16 || kv_dtype == EH_KV_BF16) && (head_dim == 64 || head_dim == 128) &&
+        pow2_kv && pow2_bt && n_head_kv <= 8 && group >= 1) {
+        const uint32_t gh = group % 4 == 0 ? 4 : group % 3 == 0 ? 3 : group <= 4 ? group : 4;
+        const uint32_t need = (group + gh - 1) / gh;  // head groups per kv head
+        uint32_t hgr = 1;
+        while (hgr < need && n_head_kv * hgr * 2 <= 8) hgr *= 2;
+        const uint32_t tpi = (uint32_t)(64 / (n_head_kv * hgr * 8));
+        if (block_tokens % tpi == 0) {
+            k.slots = true;
+            k.gh = gh;
+            k.hgr = hgr;
+            k.tpi = tpi;
+            k.chunks = (need + hgr - 1) / hgr;
+            k.chunk = (uint64_t)(kDecodeThreads / 64) * kSlotSteps * tpi;
+            k.units = k.chunks;
+            return k;
+        }
+    }
+    k.g = pick_g(group);
+    k.chunks = (group + k.g - 1) / k.g;
+    k.chunk = chunk_tokens(kv_dtype, head_dim);
+    k.units = n_head_kv * k.chunks;
+    return k;
 }
 
 struct decode_args {
@@ -206,22 +255,33 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
     if (!dn) return fail(EH_UNSUPPORTED, "kv_dtype");
     if (!supported_hd(a.kv_dtype, a.head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, a.head_dim);
     if (a.max_splits > kMaxSplits) return invalid_size(kMaxSplits, a.max_splits, "max_splits");
-    const uint32_t group = a.n_head / a.n_head_kv;
-    const uint32_t g = pick_g(group);
-    const uint32_t chunks = (group + g - 1) / g;
+    const decode_kernel dk =
+        pick_decode_kernel(a.kv_dtype, a.head_dim, a.n_head, a.n_head_kv, a.block_tokens);
     char name[64];
-    std::snprintf(name, sizeof name, "eh_decode_split_%s_hd%u_g%u", dn, a.head_dim, g);
+    if (dk.slots)
+        std::snprintf(name, sizeof name, "eh_decode_slots_%s_hd%u_h%u", dn, a.head_dim, dk.gh);
+    else
+        std::snprintf(name, sizeof name, "eh_decode_split_%s_hd%u_g%u", dn, a.head_dim, dk.g);
+    if (a.tps % dk.chunk) return invalid_size(dk.chunk, a.tps, "tokens_per_split % chunk");
     const float scale = 1.0f / std::sqrt((float)a.head_dim);  // paged_attention.rs:286
     const float scale_log2 = scale * 1.4426950408889634f;
     const int bt_shift = log2_exact(a.block_tokens);
-    if (a.tps > max_tps(a.block_tokens)) return invalid_size(max_tps(a.block_tokens), a.tps, "tokens_per_split");
+    if (a.tps > max_tps(a.block_tokens, dk.chunk))
+        return invalid_size(max_tps(a.block_tokens, dk.chunk), a.tps, "tokens_per_split");
     const hipModule_t mod = c->mod_decode[dt_index(a.kv_dtype)];
-    eh_status st = launch(c, mod, name, dim3(a.max_splits, a.n_head_kv * chunks, a.batch),
-                          dim3(kDecodeThreads),
-                          stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride, a.lens_ptr,
-                          a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.out, a.part_acc,
-                          a.part_ml, a.n_head, a.n_head_kv, a.block_tokens, bt_shift, a.tps,
-                          a.max_splits, scale_log2, a.n_blocks);
+    eh_status st;
+    if (dk.slots)
+        st = launch(c, mod, name, dim3(a.max_splits, dk.chunks, a.batch), dim3(kDecodeThreads),
+                    stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride, a.lens_ptr, a.lens_mode,
+                    a.seq_tokens, a.query_pos, a.causal, a.out, a.part_acc, a.part_ml, a.n_head,
+                    a.n_head_kv, dk.hgr, a.block_tokens, bt_shift, a.tps, a.max_splits, scale_log2,
+                    a.n_blocks);
+    else
+        st = launch(c, mod, name, dim3(a.max_splits, a.n_head_kv * dk.chunks, a.batch),
+                    dim3(kDecodeThreads), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
+                    a.lens_ptr, a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.out,
+                    a.part_acc, a.part_ml, a.n_head, a.n_head_kv, a.block_tokens, bt_shift, a.tps,
+                    a.max_splits, scale_log2, a.n_blocks);
     if (st != EH_OK || a.max_splits <= 1) return st;
     return launch(c, mod, "eh_decode_merge", dim3(a.n_head, a.batch), dim3(128), stream,
                   (const float*)a.part_acc, (const float*)a.part_ml, a.out, a.lens_ptr, a.lens_mode,
@@ -230,13 +290,13 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
 
 // Splits: aim for enough workgroups to fill 256 CUs several times over, with
 // at most kMaxSplits splits and a block-table slice that fits LDS.
-uint64_t auto_tps(uint64_t batch, uint64_t n_kv, uint64_t chunks, uint64_t max_ctx,
-                  uint64_t block_tokens, uint64_t chunk) {
+uint64_t auto_tps(uint64_t batch, uint64_t units, uint64_t max_ctx, uint64_t block_tokens,
+                  uint64_t chunk) {
     const uint64_t target_wgs = 1024;
-    uint64_t tps = div_ceil(batch * n_kv * chunks * (max_ctx ? max_ctx : 1), target_wgs);
+    uint64_t tps = div_ceil(batch * units * (max_ctx ? max_ctx : 1), target_wgs);
     tps = std::max<uint64_t>(div_ceil(tps, chunk), 1) * chunk;
     while (div_ceil(max_ctx ? max_ctx : 1, tps) > kMaxSplits) tps += chunk;
-    return std::min(tps, max_tps(block_tokens));
+    return std::min(tps, max_tps(block_tokens, chunk));
 }
 
 // Checks shared by the single-sequence attention entry points
@@ -600,17 +660,17 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
     // device, so size the grid for everything the block table can address.
     uint64_t cap = seq_tokens;
     if (pos_ptr) cap = std::max<uint64_t>(cap, (uint64_t)a.bt_stride * block_tokens);
-    const uint32_t group = (uint32_t)(n_head / n_head_kv);
-    const uint32_t chunks = (group + pick_g(group) - 1) / pick_g(group);
-    const uint64_t chunk = chunk_tokens(kv_dtype, head_dim);
-    uint64_t tps = auto_tps(1, n_head_kv, chunks, cap, block_tokens, chunk);
-    if (single_pass && cap <= max_tps(block_tokens)) tps = std::max<uint64_t>(cap, 1);
+    const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
+    const uint64_t chunk = dk.chunk;
+    uint64_t tps = auto_tps(1, dk.units, cap, block_tokens, chunk);
+    if (single_pass && cap <= max_tps(block_tokens, chunk))
+        tps = std::max<uint64_t>(div_ceil(cap, chunk), 1) * chunk;
     // Grow the split until the partials fit the context's scratch.
     while (div_ceil(cap, tps) > 1 &&
            decode_ws_floats(n_head, div_ceil(cap, tps), head_dim) > c->scratch_floats)
         tps *= 2;
-    if (tps > max_tps(block_tokens) || div_ceil(cap, tps) > kMaxSplits)
-        return invalid_size(max_tps(block_tokens) * kMaxSplits, cap, "context too long");
+    if (tps > max_tps(block_tokens, chunk) || div_ceil(cap, tps) > kMaxSplits)
+        return invalid_size(max_tps(block_tokens, chunk) * kMaxSplits, cap, "context too long");
     a.tps = (uint32_t)tps;
     a.max_splits = (uint32_t)div_ceil(cap, tps);
     a.part_acc = c->scratch;
@@ -647,14 +707,12 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
     if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return fail(EH_INVALID_ARGS, "heads");
     if (block_tokens < 1) return fail(EH_INVALID_ARGS, "block_tokens");
     if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
-    const uint32_t group = n_head / n_head_kv;
-    const uint32_t chunks = (group + pick_g(group) - 1) / pick_g(group);
-    uint64_t tps = hint ? hint
-                        : auto_tps(batch, n_head_kv, chunks, max_ctx, block_tokens,
-                                   chunk_tokens(kv_dtype, head_dim));
+    const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
+    uint64_t tps = hint ? div_ceil(hint, dk.chunk) * dk.chunk
+                        : auto_tps(batch, dk.units, max_ctx, block_tokens, dk.chunk);
     while (div_ceil(max_ctx ? max_ctx : 1, tps) > kMaxSplits) tps *= 2;
-    if (tps > max_tps(block_tokens))
-        return invalid_size(max_tps(block_tokens), tps, "tokens_per_split");
+    if (tps > max_tps(block_tokens, dk.chunk))
+        return invalid_size(max_tps(block_tokens, dk.chunk), tps, "tokens_per_split");
     const uint32_t ms = (uint32_t)div_ceil(max_ctx ? max_ctx : 1, tps);
     if (tokens_per_split) *tokens_per_split = (uint32_t)tps;
     if (max_splits) *max_splits = ms;

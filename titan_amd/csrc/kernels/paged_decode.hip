@@ -55,7 +55,14 @@ template <int NWORDS> struct raw_t { uint32_t w[NWORDS]; };
 template <int NWORDS>
 __device__ __forceinline__ raw_t<NWORDS> load_raw(const uint8_t* p) {
     raw_t<NWORDS> r;
-    if constexpr (NWORDS == 4) {
+    if constexpr (NWORDS > 4) {  // several 16-byte vectors
+        static_assert(NWORDS % 4 == 0, "unsupported vector width");
+#pragma unroll
+        for (int i = 0; i < NWORDS / 4; ++i) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p + 16 * i);
+            r.w[4 * i] = v.x; r.w[4 * i + 1] = v.y; r.w[4 * i + 2] = v.z; r.w[4 * i + 3] = v.w;
+        }
+    } else if constexpr (NWORDS == 4) {
         const uint4 v = *reinterpret_cast<const uint4*>(p);
         r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
     } else if constexpr (NWORDS == 2) {
@@ -80,6 +87,10 @@ __device__ __forceinline__ float elem(const raw_t<NWORDS>& r, int e) {
         const uint32_t w = r.w[e >> 1];
         return __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
     }
+}
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
 template <int CTRL>
@@ -347,6 +358,334 @@ __device__ __forceinline__ void decode_split(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Slot-major split (16-bit KV, head_dim 64/128, power-of-two kv-head counts
+// and pages): one workgroup per (split, head chunk, sequence) serves every kv
+// head, so each wave step reads whole token slots (the K row of all heads,
+// then the V row) -- contiguous pages -- rather than one head's slice.
+//
+// Lane layout: lane = ((tk * n_kv + hk) * HGR + hg) * 8 + sub.  Eight lanes
+// cover one head row (16 dims each for head_dim 128, 8 for 64); HGR head
+// groups of GH q heads each share that K/V slice (the duplicate lanes load the
+// same bytes within one instruction, so HBM traffic is unchanged), which cuts
+// the per-lane reduction and softmax work to GH heads.  TPI = 64 / (8 n_kv
+// HGR) tokens per wave step; a step never straddles a page, so its page is
+// wave-uniform and its block-table entry a scalar load.
+//
+// Arithmetic: q.k with packed dot2 and q split into hi + lo 16-bit parts (a
+// single rounded q is too coarse for large scores); f16 P.V pairs two tokens
+// per dot2 (P rounded to f16, well inside the tolerance); bf16 P.V widens V
+// and uses f32 fma.  Invalid tokens enter the softmax as -inf scores.
+constexpr int SLOT_STEPS = 16;   // unrolled wave steps per chunk (even, power of two <= 64)
+constexpr int SLOT_DEPTH = 4;    // wave steps in flight (even)
+constexpr int SLOT_HMAX = 64;    // q heads one workgroup may serve
+
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+
+// Dims of lane `sub` within a head row (8 lanes per row): 8-dim pieces at
+// sub*8 and, for head_dim 128, 64 + sub*8, so that every 16-byte load
+// instruction covers a contiguous run of the row across the 8 lanes.
+template <int HD>
+__device__ __forceinline__ uint32_t slot_dim(uint32_t sub, int e) {
+    return (uint32_t)(e < 8 ? (int)sub * 8 + e : 64 + (int)sub * 8 + (e - 8));
+}
+
+template <int NWD>
+__device__ __forceinline__ raw_t<NWD> load_slot_row(const uint8_t* p) {
+    raw_t<NWD> r;
+#pragma unroll
+    for (int i = 0; i < NWD / 4; ++i) {  // 16-byte pieces 128 bytes apart
+        const uint4 v = *reinterpret_cast<const uint4*>(p + 128 * i);
+        r.w[4 * i] = v.x; r.w[4 * i + 1] = v.y; r.w[4 * i + 2] = v.z; r.w[4 * i + 3] = v.w;
+    }
+    return r;
+}
+
+template <int DT, int HD, int GH>
+__device__ __forceinline__ void decode_slots(
+    const float* __restrict__ q, const uint8_t* __restrict__ pool,
+    const uint32_t* __restrict__ bt, uint32_t bt_stride, len_src L, float* __restrict__ out,
+    float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t n_head,
+    uint32_t n_head_kv, uint32_t hgr, uint32_t block_tokens, int bt_shift, uint32_t tps,
+    uint32_t max_splits, float scale_log2, uint64_t n_blocks) {
+    static_assert(DT == DT_F16 || DT == DT_BF16, "16-bit KV only");
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    constexpr int EPL = HD / 8;       // dims per lane (8 lanes per head row)
+    constexpr int NWD = EPL / 2;      // 32-bit words per lane row
+    constexpr int NP = EPL / 2;       // packed pairs per lane row
+
+    __shared__ float s_m[NW][SLOT_HMAX], s_l[NW][SLOT_HMAX];
+    __shared__ float s_acc[SLOT_HMAX][HD];
+
+    const uint32_t split = blockIdx.x;
+    const uint32_t hc = blockIdx.y;
+    const uint32_t b = blockIdx.z;
+    const uint32_t group = n_head / n_head_kv;
+    const uint32_t lpt = n_head_kv * hgr * 8;  // lanes per token (power of two <= 64)
+    const uint32_t tpi = 64u / lpt;            // tokens per wave step
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tk = (uint32_t)lane / lpt;
+    const uint32_t r = (uint32_t)lane - tk * lpt;
+    const uint32_t hk = r / (hgr * 8);
+    const uint32_t hg = (r >> 3) - hk * hgr;
+    const uint32_t sub = r & 7u;
+    const uint32_t hbase = (hc * hgr + hg) * GH;  // first head of this lane, within the group
+    const uint32_t n_wg_heads = n_head_kv * hgr * GH;
+
+    const uint32_t t0 = split * tps;
+    const uint32_t row_bytes = n_head_kv * HD * 2;
+    const uint32_t slot_bytes = 2u * row_bytes;
+    const uint64_t page_bytes = (uint64_t)block_tokens * slot_bytes;
+    const uint32_t bsh = (uint32_t)bt_shift;  // power-of-two pages here
+    const uint32_t* bt_row = bt + (uint64_t)b * bt_stride;
+    const uint32_t lane_off = hk * HD * 2 + sub * 16;
+
+    const uint32_t wtoks = tpi * SLOT_STEPS;  // tokens per wave per chunk
+    // Page entry of step `lane` of the chunk starting at w0 (one vector load
+    // per chunk; steps read it back with readlane).  Entries past the table
+    // read its last entry and are invalidated at use.
+    auto load_pages = [&](uint32_t w0) -> uint32_t {
+        const uint32_t pg = (w0 + (uint32_t)(lane & (SLOT_STEPS - 1)) * tpi) >> bsh;
+        return bt_row[pg < bt_stride ? pg : bt_stride - 1u];
+    };
+    uint32_t pv_next = load_pages(t0 + wave * wtoks);
+
+    // q of this lane's GH heads and EPL dims, pre-scaled into the log2
+    // domain, as hi + lo 16-bit pairs (heads past the group are zero).
+    uint32_t qa[GH][NP], qb[GH][NP];
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+        const bool hv = hbase + h < group;
+        const uint32_t hh = hv ? hbase + h : group - 1;
+        const float sc = hv ? scale_log2 : 0.0f;
+        const float* qp = q + ((uint64_t)b * n_head + hk * group + hh) * HD;
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(qp + slot_dim<HD>(sub, e));
+            const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                if constexpr (DT == DT_F16) {
+                    const _Float16 a0 = (_Float16)x[2 * u], a1 = (_Float16)x[2 * u + 1];
+                    const half2_v hi = {a0, a1};
+                    const half2_v lo = {(_Float16)(x[2 * u] - (float)a0),
+                                        (_Float16)(x[2 * u + 1] - (float)a1)};
+                    qa[h][e / 2 + u] = __builtin_bit_cast(uint32_t, hi);
+                    qb[h][e / 2 + u] = __builtin_bit_cast(uint32_t, lo);
+                } else {
+                    const __bf16 a0 = (__bf16)x[2 * u], a1 = (__bf16)x[2 * u + 1];
+                    const bf16x2_v hi = {a0, a1};
+                    const bf16x2_v lo = {(__bf16)(x[2 * u] - (float)a0),
+                                         (__bf16)(x[2 * u + 1] - (float)a1)};
+                    qa[h][e / 2 + u] = __builtin_bit_cast(uint32_t, hi);
+                    qb[h][e / 2 + u] = __builtin_bit_cast(uint32_t, lo);
+                }
+            }
+        }
+    }
+
+    const uint32_t n = live_tokens(L, b);
+    if (t0 >= n) {
+        if (n == 0 && split == 0)
+            for (uint32_t idx = threadIdx.x; idx < n_wg_heads * HD; idx += NW * 64) {
+                const uint32_t hh = idx / HD;
+                const uint32_t kv = hh / (hgr * GH), w = hh - kv * hgr * GH;
+                const uint32_t hin = hc * hgr * GH + w;
+                if (hin < group) out[((uint64_t)b * n_head + kv * group + hin) * HD + idx % HD] = 0.0f;
+            }
+        return;
+    }
+    const uint32_t t1 = (n - t0 < tps) ? n : t0 + tps;
+    const uint32_t nsplit = split_count(n, tps, max_splits);
+
+    for (uint32_t i = threadIdx.x; i < n_wg_heads * HD; i += NW * 64) (&s_acc[0][0])[i] = 0.0f;
+
+    float m[GH], l[GH], acc[GH][EPL];
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+        m[h] = -1e30f; l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[h][e] = 0.0f;
+    }
+
+    // q.k of one step for every head of the lane, reduced over the 8 lanes
+    // of the head row; invalid tokens score -inf.
+    auto scores = [&](const raw_t<NWD>& kr, bool ok, float* s) {
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            float d = 0.0f;
+#pragma unroll
+            for (int u = 0; u < NP; ++u) {
+                if constexpr (DT == DT_F16) {
+                    const half2_v kk = __builtin_bit_cast(half2_v, kr.w[u]);
+                    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_v, qa[h][u]), kk, d, false);
+                    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_v, qb[h][u]), kk, d, false);
+                } else {
+                    const bf16x2_v kk = __builtin_bit_cast(bf16x2_v, kr.w[u]);
+                    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, qa[h][u]), kk, d, false);
+                    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, qb[h][u]), kk, d, false);
+                }
+            }
+            d = group_sum<8>(d);
+            s[h] = ok ? d : -INFINITY;
+        }
+    };
+    // Lazy rescale: the running maximum only moves when a score exceeds it by
+    // more than 2^8 (wave-uniform branch); otherwise every weight uses the
+    // stale maximum, exactly.
+    auto rescale_if = [&](const float* s0, const float* s1) {
+        bool need = false;
+#pragma unroll
+        for (int h = 0; h < GH; ++h) need |= fmaxf(s0[h], s1[h]) > m[h] + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+            for (int h = 0; h < GH; ++h) {
+                const float mn = fmaxf(m[h], fmaxf(s0[h], s1[h]));
+                const float corr = fast_exp2(m[h] - mn);
+                l[h] *= corr;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[h][e] *= corr;
+                m[h] = mn;
+            }
+        }
+    };
+
+    for (uint32_t c0 = t0; c0 < t1; c0 += NW * wtoks) {
+        const uint32_t w0 = c0 + wave * wtoks;
+        const uint32_t w1 = (w0 + wtoks < t1) ? w0 + wtoks : t1;
+        if (w0 >= w1) continue;  // wave-uniform
+        const uint32_t pv_cur = pv_next;
+        if (c0 + NW * wtoks < t1) pv_next = load_pages(w0 + NW * wtoks);  // next chunk, early
+        raw_t<NWD> kr[SLOT_DEPTH], vr[SLOT_DEPTH];
+        bool ok[SLOT_DEPTH];
+        auto issue = [&](int k) {
+            const int j = k % SLOT_DEPTH;
+            const uint32_t ts = w0 + (uint32_t)k * tpi;  // first token of the step (uniform)
+            const uint32_t tsc = ts < w1 ? ts : w0;
+            const uint32_t phys = ((ts >> bsh) < bt_stride)
+                                      ? (uint32_t)__builtin_amdgcn_readlane((int)pv_cur, k)
+                                      : 0xFFFFFFFFu;
+            const bool pv = phys < n_blocks;
+            const uint32_t t = ts + tk;
+            const bool valid = t < w1;
+            const uint32_t tc = valid ? t : tsc;
+            const uint8_t* p = pool + (uint64_t)(pv ? phys : 0u) * page_bytes +
+                               (uint64_t)((tc & ((1u << bsh) - 1u)) * slot_bytes + lane_off);
+            kr[j] = load_slot_row<NWD>(p);
+            vr[j] = load_slot_row<NWD>(p + row_bytes);
+            ok[j] = valid && pv;
+        };
+#pragma unroll
+        for (int k = 0; k < SLOT_DEPTH; ++k) issue(k);
+#pragma unroll
+        for (int k = 0; k < SLOT_STEPS; k += 2) {  // steps in pairs: P.V packs two tokens
+            const int j0 = k % SLOT_DEPTH, j1 = (k + 1) % SLOT_DEPTH;
+            float s0[GH], s1[GH];
+            scores(kr[j0], ok[j0], s0);
+            scores(kr[j1], ok[j1], s1);
+            rescale_if(s0, s1);
+            if constexpr (DT == DT_F16) {
+                uint32_t vp[EPL];  // (token k, token k+1) pairs per dim
+#pragma unroll
+                for (int w = 0; w < NWD; ++w) {
+                    vp[2 * w] = perm(vr[j1].w[w], vr[j0].w[w], 0x05040100u);
+                    vp[2 * w + 1] = perm(vr[j1].w[w], vr[j0].w[w], 0x07060302u);
+                }
+#pragma unroll
+                for (int h = 0; h < GH; ++h) {
+                    const float p0 = fast_exp2(s0[h] - m[h]), p1 = fast_exp2(s1[h] - m[h]);
+                    l[h] += p0 + p1;
+                    const half2_v pp = {(_Float16)p0, (_Float16)p1};
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e)
+                        acc[h][e] = __builtin_amdgcn_fdot2(pp, __builtin_bit_cast(half2_v, vp[e]),
+                                                           acc[h][e], false);
+                }
+            } else {
+                float v0[EPL], v1[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    v0[e] = elem<DT>(vr[j0], e);
+                    v1[e] = elem<DT>(vr[j1], e);
+                }
+#pragma unroll
+                for (int h = 0; h < GH; ++h) {
+                    const float p0 = fast_exp2(s0[h] - m[h]), p1 = fast_exp2(s1[h] - m[h]);
+                    l[h] += p0 + p1;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p1, v1[e], fmaf(p0, v0[e], acc[h][e]));
+                }
+            }
+            if (k + SLOT_DEPTH < SLOT_STEPS) issue(k + SLOT_DEPTH);
+            if (k + 1 + SLOT_DEPTH < SLOT_STEPS) issue(k + 1 + SLOT_DEPTH);
+        }
+    }
+
+    // Merge the TPI token lanes of this wave (lanes r, r + lpt, ...).
+    for (uint32_t off = lpt; off < 64u; off <<= 1) {
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            const float mo = __shfl_xor(m[h], (int)off, 64);
+            const float lo = __shfl_xor(l[h], (int)off, 64);
+            const float M = fmaxf(m[h], mo);
+            const float fa = fast_exp2(m[h] - M), fb = fast_exp2(mo - M);
+            l[h] = l[h] * fa + lo * fb;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float ao = __shfl_xor(acc[h][e], (int)off, 64);
+                acc[h][e] = acc[h][e] * fa + ao * fb;
+            }
+            m[h] = M;
+        }
+    }
+    // Merge the waves in LDS: maxima first, then scaled accumulators.
+    // Workgroup head index hh = (hk * HGR + hg) * GH + h.
+    const uint32_t hh0 = (hk * hgr + hg) * GH;
+    if (tk == 0 && sub == 0) {
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            s_m[wave][hh0 + h] = m[h];
+            s_l[wave][hh0 + h] = l[h];
+        }
+    }
+    __syncthreads();
+    if (tk == 0) {
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            float M = -1e30f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][hh0 + h]);
+            const float f = fast_exp2(m[h] - M);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e)
+                atomicAdd(&s_acc[hh0 + h][slot_dim<HD>(sub, e)], acc[h][e] * f);
+        }
+    }
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < n_wg_heads * HD; idx += NW * 64) {
+        const uint32_t hh = idx / HD, d = idx - hh * HD;
+        const uint32_t kv = hh / (hgr * GH), w = hh - kv * hgr * GH;
+        const uint32_t hin = hc * hgr * GH + w;  // head index within the kv group
+        if (hin >= group) continue;
+        float M = -1e30f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, s_m[ww][hh]);
+        float Ls = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) Ls = fmaf(s_l[ww][hh], fast_exp2(s_m[ww][hh] - M), Ls);
+        const float A = s_acc[hh][d];
+        const uint64_t qrow = (uint64_t)b * n_head + kv * group + hin;
+        if (nsplit == 1) {
+            out[qrow * HD + d] = Ls > 0.0f ? A / Ls : 0.0f;
+        } else {
+            const uint64_t slot = qrow * max_splits + split;
+            part_acc[slot * HD + d] = A;
+            if (d == 0) { part_ml[slot * 2] = M; part_ml[slot * 2 + 1] = Ls; }
+        }
+    }
+}
+
 // Splits one merge workgroup combines (LDS-resident weights).
 constexpr uint32_t MERGE_MAX_SPLITS = 256;
 
@@ -435,12 +774,37 @@ extern "C" __global__ __launch_bounds__(128) void eh_decode_merge(
     EH_DECODE_G(DTN, DT, 128) \
     EH_DECODE_G(DTN, DT, 256)
 
+#define EH_SLOTS(DTN, DT, HD, GH)                                                               \
+    extern "C" __global__ __launch_bounds__(NW * 64, 2) void eh_decode_slots_##DTN##_hd##HD##_h##GH( \
+        const float* q, const uint8_t* pool, const uint32_t* bt, uint32_t bt_stride,              \
+        const uint32_t* lens_ptr, uint32_t lens_mode, uint32_t seq_tokens, uint32_t query_pos,    \
+        uint32_t causal, float* out, float* part_acc, float* part_ml, uint32_t n_head,            \
+        uint32_t n_head_kv, uint32_t hgr, uint32_t block_tokens, int bt_shift, uint32_t tps,      \
+        uint32_t max_splits, float scale_log2, uint64_t n_blocks) {                               \
+        const len_src L{lens_ptr, lens_mode, seq_tokens, query_pos, causal};                      \
+        decode_slots<DT, HD, GH>(q, pool, bt, bt_stride, L, out, part_acc, part_ml, n_head,       \
+                                 n_head_kv, hgr, block_tokens, bt_shift, tps, max_splits,         \
+                                 scale_log2, n_blocks);                                           \
+    }
+
+#define EH_SLOTS_ALL(DTN, DT) \
+    EH_SLOTS(DTN, DT, 64, 1)  \
+    EH_SLOTS(DTN, DT, 64, 2)  \
+    EH_SLOTS(DTN, DT, 64, 3)  \
+    EH_SLOTS(DTN, DT, 64, 4)  \
+    EH_SLOTS(DTN, DT, 128, 1) \
+    EH_SLOTS(DTN, DT, 128, 2) \
+    EH_SLOTS(DTN, DT, 128, 3) \
+    EH_SLOTS(DTN, DT, 128, 4)
+
 #if !defined(EH_ONLY_DT) || EH_ONLY_DT == 0
 EH_DECODE_HD(f32, DT_F32)
 #endif
 #if !defined(EH_ONLY_DT) || EH_ONLY_DT == 1
 EH_DECODE_HD(f16, DT_F16)
+EH_SLOTS_ALL(f16, DT_F16)
 #endif
 #if !defined(EH_ONLY_DT) || EH_ONLY_DT == 2
 EH_DECODE_HD(bf16, DT_BF16)
+EH_SLOTS_ALL(bf16, DT_BF16)
 #endif
