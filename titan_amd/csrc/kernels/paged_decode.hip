@@ -414,8 +414,11 @@ __device__ __forceinline__ void decode_slots(
     constexpr int NWD = EPL / 2;      // 32-bit words per lane row
     constexpr int NP = EPL / 2;       // packed pairs per lane row
 
-    __shared__ float s_m[NW][SLOT_HMAX], s_l[NW][SLOT_HMAX];
-    __shared__ float s_acc[SLOT_HMAX][HD];
+    // Epilogue staging: one partial state per (wave, token lane tk, head):
+    // TPI * n_wg_heads = 8 * GH per wave.
+    constexpr int NPART = NW * 8 * GH;
+    __shared__ float s_acc[NPART][HD];
+    __shared__ float s_m[NPART], s_l[NPART], s_w[NPART];
 
     const uint32_t split = blockIdx.x;
     const uint32_t hc = blockIdx.y;
@@ -498,8 +501,6 @@ __device__ __forceinline__ void decode_slots(
     }
     const uint32_t t1 = (n - t0 < tps) ? n : t0 + tps;
     const uint32_t nsplit = split_count(n, tps, max_splits);
-
-    for (uint32_t i = threadIdx.x; i < n_wg_heads * HD; i += NW * 64) (&s_acc[0][0])[i] = 0.0f;
 
     float m[GH], l[GH], acc[GH][EPL];
 #pragma unroll
@@ -622,45 +623,28 @@ __device__ __forceinline__ void decode_slots(
         }
     }
 
-    // Merge the TPI token lanes of this wave (lanes r, r + lpt, ...).
-    for (uint32_t off = lpt; off < 64u; off <<= 1) {
-#pragma unroll
-        for (int h = 0; h < GH; ++h) {
-            const float mo = __shfl_xor(m[h], (int)off, 64);
-            const float lo = __shfl_xor(l[h], (int)off, 64);
-            const float M = fmaxf(m[h], mo);
-            const float fa = fast_exp2(m[h] - M), fb = fast_exp2(mo - M);
-            l[h] = l[h] * fa + lo * fb;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float ao = __shfl_xor(acc[h][e], (int)off, 64);
-                acc[h][e] = acc[h][e] * fa + ao * fb;
-            }
-            m[h] = M;
-        }
-    }
-    // Merge the waves in LDS: maxima first, then scaled accumulators.
-    // Workgroup head index hh = (hk * HGR + hg) * GH + h.
+    // Epilogue.  Every lane group (wave, tk) holds a partial softmax state
+    // for its heads; stage them all in LDS, compute one weight per partial,
+    // then combine per output element -- no shuffles, no atomics.
+    // Partial index: (wave * TPI + tk) * n_wg_heads + hh, hh = (hk*HGR+hg)*GH + h.
     const uint32_t hh0 = (hk * hgr + hg) * GH;
-    if (tk == 0 && sub == 0) {
+    const uint32_t pbase = (wave * tpi + tk) * n_wg_heads;
 #pragma unroll
-        for (int h = 0; h < GH; ++h) {
-            s_m[wave][hh0 + h] = m[h];
-            s_l[wave][hh0 + h] = l[h];
-        }
+    for (int h = 0; h < GH; ++h) {
+        float* dst = s_acc[pbase + hh0 + h];
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4)
+            *reinterpret_cast<float4*>(dst + slot_dim<HD>(sub, e)) =
+                make_float4(acc[h][e], acc[h][e + 1], acc[h][e + 2], acc[h][e + 3]);
+        if (sub == 0) { s_m[pbase + hh0 + h] = m[h]; s_l[pbase + hh0 + h] = l[h]; }
     }
     __syncthreads();
-    if (tk == 0) {
-#pragma unroll
-        for (int h = 0; h < GH; ++h) {
-            float M = -1e30f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][hh0 + h]);
-            const float f = fast_exp2(m[h] - M);
-#pragma unroll
-            for (int e = 0; e < EPL; ++e)
-                atomicAdd(&s_acc[hh0 + h][slot_dim<HD>(sub, e)], acc[h][e] * f);
-        }
+    const uint32_t nparts = NW * tpi;  // partials per head
+    for (uint32_t i = threadIdx.x; i < nparts * n_wg_heads; i += NW * 64) {
+        const uint32_t hh = i % n_wg_heads;
+        float M = -1e30f;
+        for (uint32_t pp = 0; pp < nparts; ++pp) M = fmaxf(M, s_m[pp * n_wg_heads + hh]);
+        s_w[i] = fast_exp2(s_m[i] - M);
     }
     __syncthreads();
     for (uint32_t idx = threadIdx.x; idx < n_wg_heads * HD; idx += NW * 64) {
@@ -668,13 +652,13 @@ __device__ __forceinline__ void decode_slots(
         const uint32_t kv = hh / (hgr * GH), w = hh - kv * hgr * GH;
         const uint32_t hin = hc * hgr * GH + w;  // head index within the kv group
         if (hin >= group) continue;
-        float M = -1e30f;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, s_m[ww][hh]);
-        float Ls = 0.0f;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) Ls = fmaf(s_l[ww][hh], fast_exp2(s_m[ww][hh] - M), Ls);
-        const float A = s_acc[hh][d];
+        float M = -1e30f, Ls = 0.0f, A = 0.0f;
+        for (uint32_t pp = 0; pp < nparts; ++pp) {
+            const uint32_t i = pp * n_wg_heads + hh;
+            M = fmaxf(M, s_m[i]);
+            Ls = fmaf(s_l[i], s_w[i], Ls);
+            A = fmaf(s_acc[i][d], s_w[i], A);
+        }
         const uint64_t qrow = (uint64_t)b * n_head + kv * group + hin;
         if (nsplit == 1) {
             out[qrow * HD + d] = Ls > 0.0f ? A / Ls : 0.0f;
