@@ -271,7 +271,7 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
     const hipModule_t mod = c->mod_decode[dt_index(a.kv_dtype)];
     eh_status st;
     if (dk.slots)
-        st = launch(c, mod, name, dim3(a.max_splits, dk.chunks, a.batch), dim3(kDecodeThreads),
+        st = launch(c, mod, name, dim3(a.batch, dk.chunks, a.max_splits), dim3(kDecodeThreads),
                     stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride, a.lens_ptr, a.lens_mode,
                     a.seq_tokens, a.query_pos, a.causal, a.out, a.part_acc, a.part_ml, a.n_head,
                     a.n_head_kv, dk.hgr, a.block_tokens, bt_shift, a.tps, a.max_splits, scale_log2,
@@ -283,7 +283,9 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
                     a.part_acc, a.part_ml, a.n_head, a.n_head_kv, a.block_tokens, bt_shift, a.tps,
                     a.max_splits, scale_log2, a.n_blocks);
     if (st != EH_OK || a.max_splits <= 1) return st;
-    return launch(c, mod, "eh_decode_merge", dim3(a.n_head, a.batch), dim3(128), stream,
+    return launch(c, mod, "eh_decode_merge",
+                  dim3((uint32_t)div_ceil((uint64_t)a.n_head * a.head_dim, 256), a.batch), dim3(256),
+                  stream,
                   (const float*)a.part_acc, (const float*)a.part_ml, a.out, a.lens_ptr, a.lens_mode,
                   a.seq_tokens, a.query_pos, a.causal, a.n_head, a.head_dim, a.tps, a.max_splits);
 }

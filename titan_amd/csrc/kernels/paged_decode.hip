@@ -420,9 +420,11 @@ __device__ __forceinline__ void decode_slots(
     __shared__ float s_acc[NPART][HD];
     __shared__ float s_m[NPART], s_l[NPART], s_w[NPART];
 
-    const uint32_t split = blockIdx.x;
+    // grid (batch, head chunks, splits): dispatch walks split-major, so the
+    // splits past the shorter contexts (empty workgroups) come last.
+    const uint32_t b = blockIdx.x;
     const uint32_t hc = blockIdx.y;
-    const uint32_t b = blockIdx.z;
+    const uint32_t split = blockIdx.z;
     const uint32_t group = n_head / n_head_kv;
     const uint32_t lpt = n_head_kv * hgr * 8;  // lanes per token (power of two <= 64)
     const uint32_t tpi = 64u / lpt;            // tokens per wave step
@@ -670,62 +672,54 @@ __device__ __forceinline__ void decode_slots(
     }
 }
 
-// Splits one merge workgroup combines (LDS-resident weights).
-constexpr uint32_t MERGE_MAX_SPLITS = 256;
-
 }  // namespace
 
 // Log-sum-exp merge of split partials: out = sum_s w_s acc_s / sum_s w_s l_s
-// with w_s = exp2(m_s - max m).  grid (n_head, batch), 128 threads; wave 0
-// reduces over splits (lanes stride the split index), then all threads
-// combine the partial vectors with independent, unrolled loads.
-extern "C" __global__ __launch_bounds__(128) void eh_decode_merge(
+// with w_s = exp2(m_s - max m), splits with l_s == 0 skipped.  One thread
+// per output element (grid (ceil(n_head * head_dim / 256), batch), 256
+// threads); the partials of 8 splits are fetched together before they are
+// folded in (an online max keeps one pass), so a context of S splits costs
+// ceil(S / 8) memory round trips.
+extern "C" __global__ __launch_bounds__(256) void eh_decode_merge(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
     const uint32_t* lens_ptr, uint32_t lens_mode, uint32_t seq_tokens, uint32_t query_pos,
     uint32_t causal, uint32_t n_head, uint32_t head_dim, uint32_t tps, uint32_t max_splits) {
-    __shared__ float s_w[MERGE_MAX_SPLITS];
-    __shared__ float s_inv;
     const len_src L{lens_ptr, lens_mode, seq_tokens, query_pos, causal};
-    const uint32_t qh = blockIdx.x, b = blockIdx.y;
+    const uint32_t b = blockIdx.y;
+    const uint32_t e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= n_head * head_dim) return;
     const uint32_t n = live_tokens(L, b);
-    uint32_t nsplit = split_count(n, tps, max_splits);
-    if (nsplit > MERGE_MAX_SPLITS) nsplit = MERGE_MAX_SPLITS;
+    const uint32_t nsplit = split_count(n, tps, max_splits);
     if (n == 0 || nsplit <= 1) return;  // the split kernel wrote the output
+    const uint32_t qh = e / head_dim, d = e - qh * head_dim;
     const uint64_t qrow = (uint64_t)b * n_head + qh;
-    const float* ml = part_ml + qrow * max_splits * 2;
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        float M = -INFINITY;
-        for (uint32_t s = lane; s < nsplit; s += 64)
-            if (ml[2 * s + 1] > 0.0f) M = fmaxf(M, ml[2 * s]);
+    const float2* ml = reinterpret_cast<const float2*>(part_ml) + qrow * max_splits;
+    const float* pa = part_acc + qrow * max_splits * head_dim + d;
+    float M = -INFINITY, Ls = 0.0f, A = 0.0f;
+    for (uint32_t s0 = 0; s0 < nsplit; s0 += 8) {
+        float2 v[8];
+        float x[8];
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        float Ls = 0.0f;
-        for (uint32_t s = lane; s < nsplit; s += 64) {
-            const float ls = ml[2 * s + 1];
-            const float w = ls > 0.0f ? fast_exp2(ml[2 * s] - M) : 0.0f;
-            s_w[s] = w;
-            Ls = fmaf(ls, w, Ls);
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t sidx = s0 + i < nsplit ? s0 + i : s0;
+            v[i] = ml[sidx];
+            x[i] = pa[(uint64_t)sidx * head_dim];
         }
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) Ls += __shfl_xor(Ls, off, 64);
-        if (lane == 0) s_inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-    }
-    __syncthreads();
-    const float inv = s_inv;
-    for (uint32_t d = threadIdx.x; d < head_dim; d += 128) {
-        const float* pa = part_acc + qrow * max_splits * head_dim + d;
-        float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f;
-        uint32_t s = 0;
-        for (; s + 4 <= nsplit; s += 4) {
-            A0 = fmaf(pa[(uint64_t)s * head_dim], s_w[s], A0);
-            A1 = fmaf(pa[(uint64_t)(s + 1) * head_dim], s_w[s + 1], A1);
-            A2 = fmaf(pa[(uint64_t)(s + 2) * head_dim], s_w[s + 2], A2);
-            A3 = fmaf(pa[(uint64_t)(s + 3) * head_dim], s_w[s + 3], A3);
+        for (int i = 0; i < 8; ++i) {
+            if (s0 + i >= nsplit || !(v[i].y > 0.0f)) continue;
+            if (v[i].x > M) {
+                const float c = fast_exp2(M - v[i].x);  // 0 on the first live split
+                Ls *= c;
+                A *= c;
+                M = v[i].x;
+            }
+            const float w = fast_exp2(v[i].x - M);
+            Ls = fmaf(v[i].y, w, Ls);
+            A = fmaf(x[i], w, A);
         }
-        for (; s < nsplit; ++s) A0 = fmaf(pa[(uint64_t)s * head_dim], s_w[s], A0);
-        out[qrow * head_dim + d] = ((A0 + A1) + (A2 + A3)) * inv;
     }
+    out[qrow * head_dim + d] = Ls > 0.0f ? A / Ls : 0.0f;
 }
 
 #define EH_DECODE(DTN, DT, HD, G)                                                                \
