@@ -154,6 +154,10 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
                          uint32_t head_dim, uint32_t block_tokens, uint32_t max_ctx,
                          uint32_t tokens_per_split_hint, uint32_t* tokens_per_split,
                          uint32_t* max_splits, uint64_t* workspace_bytes);
+/* Name of the split kernel eh_paged_decode_batched launches for a shape
+ * (diagnostics and profiling; no reference counterpart). */
+eh_status eh_decode_kernel_name(uint32_t kv_dtype, uint32_t n_head, uint32_t n_head_kv,
+                                uint32_t head_dim, uint32_t block_tokens, char* buf, uint64_t size);
 /* q/out [batch, n_head, head_dim] f32; block_tables [batch, bt_stride] u32;
  * ctx_lens [batch] u32 = tokens each query attends (its own position + 1),
  * each at most tokens_per_split * max_splits.  workspace, tokens_per_split

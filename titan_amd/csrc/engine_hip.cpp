@@ -293,10 +293,9 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
 // Splits: aim for enough workgroups to fill 256 CUs several times over, with
 // at most kMaxSplits splits and a block-table slice that fits LDS.
 uint64_t auto_tps(uint64_t batch, uint64_t units, uint64_t max_ctx, uint64_t block_tokens,
-                  uint64_t chunk) {
-    const uint64_t target_wgs = 1024;
+                  uint64_t chunk, uint64_t target_wgs = 1024) {
     uint64_t tps = div_ceil(batch * units * (max_ctx ? max_ctx : 1), target_wgs);
-    tps = std::max<uint64_t>(div_ceil(tps, chunk), 1) * chunk;
+    tps = std::max<uint64_t>((tps + chunk / 2) / chunk, 1) * chunk;  // nearest chunk multiple
     while (div_ceil(max_ctx ? max_ctx : 1, tps) > kMaxSplits) tps += chunk;
     return std::min(tps, max_tps(block_tokens, chunk));
 }
@@ -664,7 +663,7 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
     if (pos_ptr) cap = std::max<uint64_t>(cap, (uint64_t)a.bt_stride * block_tokens);
     const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
     const uint64_t chunk = dk.chunk;
-    uint64_t tps = auto_tps(1, dk.units, cap, block_tokens, chunk);
+    uint64_t tps = auto_tps(1, dk.units, cap, block_tokens, chunk, dk.slots ? 512 : 1024);
     if (single_pass && cap <= max_tps(block_tokens, chunk))
         tps = std::max<uint64_t>(div_ceil(cap, chunk), 1) * chunk;
     // Grow the split until the partials fit the context's scratch.
@@ -711,7 +710,8 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
     if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
     const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
     uint64_t tps = hint ? div_ceil(hint, dk.chunk) * dk.chunk
-                        : auto_tps(batch, dk.units, max_ctx, block_tokens, dk.chunk);
+                        : auto_tps(batch, dk.units, max_ctx, block_tokens, dk.chunk,
+                                   dk.slots ? 512 : 1024);
     while (div_ceil(max_ctx ? max_ctx : 1, tps) > kMaxSplits) tps *= 2;
     if (tps > max_tps(block_tokens, dk.chunk))
         return invalid_size(max_tps(block_tokens, dk.chunk), tps, "tokens_per_split");
@@ -719,6 +719,23 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
     if (tokens_per_split) *tokens_per_split = (uint32_t)tps;
     if (max_splits) *max_splits = ms;
     if (workspace_bytes) *workspace_bytes = 4 * decode_ws_floats((uint64_t)batch * n_head, ms, head_dim);
+    return EH_OK;
+}
+
+eh_status eh_decode_kernel_name(uint32_t kv_dtype, uint32_t n_head, uint32_t n_head_kv,
+                                uint32_t head_dim, uint32_t block_tokens, char* buf, uint64_t size) {
+    if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return fail(EH_INVALID_ARGS, "heads");
+    if (block_tokens < 1) return fail(EH_INVALID_ARGS, "block_tokens");
+    const char* dn = dt_name(kv_dtype);
+    if (!dn) return fail(EH_UNSUPPORTED, "kv_dtype");
+    const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
+    char name[64];
+    if (dk.slots)
+        std::snprintf(name, sizeof name, "eh_decode_slots_%s_hd%u_h%u", dn, head_dim, dk.gh);
+    else
+        std::snprintf(name, sizeof name, "eh_decode_split_%s_hd%u_g%u", dn, head_dim, dk.g);
+    if (!buf || size <= std::strlen(name)) return invalid_size(std::strlen(name) + 1, size, "name buffer");
+    std::memcpy(buf, name, std::strlen(name) + 1);
     return EH_OK;
 }
 

@@ -74,6 +74,14 @@ class PagedAttention:
         return tps.value, ms.value, ws.value
 
     @staticmethod
+    def kernel_name(n_head, n_head_kv, head_dim, block_tokens, kv_dtype=KvDataType.F16):
+        """Split kernel decode_batched launches for this shape."""
+        buf_ = C.create_string_buffer(64)
+        check(_lib.load().eh_decode_kernel_name(int(kv_dtype), int(n_head), int(n_head_kv),
+                                                int(head_dim), int(block_tokens), buf_, 64))
+        return buf_.value.decode()
+
+    @staticmethod
     def workspace(plan, device="cuda"):
         """Workspace for the split partials of decode_batched."""
         nbytes = max(plan[2], 4)
