@@ -183,6 +183,35 @@ def test_batched_decode_head_groupings(dev, dtype, shape):
         check_close(out.cpu().numpy(), ref, dtype)
 
 
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
+def test_batched_decode_workspace_reuse(dev, dtype):
+    """One workspace serves repeated calls, a smaller plan after a larger
+    one, and a larger one again: nothing a call leaves in it changes the next
+    call's result."""
+    rng = np.random.default_rng(5)
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    pa = PagedAttention(0)
+    big = PagedAttention.plan(8, n_head, n_kv, hd, bt, 3000, 64, dtype)
+    ws = PagedAttention.workspace(big)
+    for batch, max_ctx, tps in ((8, 3000, 64), (8, 3000, 64), (3, 900, 32), (8, 3000, 128)):
+        lens = rng.integers(0, max_ctx + 1, size=batch).astype(np.int64)
+        lens[0] = max_ctx
+        stride = (max_ctx + bt - 1) // bt
+        nb = batch * stride
+        tab = rng.permutation(nb).astype(np.uint32).reshape(batch, stride)
+        pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, dtype, dev)
+        q = rng.standard_normal((batch, n_head, hd)).astype(np.float32)
+        ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head,
+                                      n_kv, hd)
+        plan = PagedAttention.plan(batch, n_head, n_kv, hd, bt, max_ctx, tps, dtype)
+        assert plan[1] > 1 and plan[2] <= big[2]
+        out = torch.full((batch, n_head, hd), float("nan"), device=dev)
+        pa.decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                          i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, plan, ws)
+        torch.cuda.synchronize()
+        check_close(out.cpu().numpy(), ref, dtype)
+
+
 def test_config1_append_then_decode(dev):
     """Benchmark config 1: f32, B=1, 14/2 heads, hd 64, page 16; 511 cached
     tokens + 1 appended token (512 attended) on the first 32 pages of a seeded
