@@ -42,6 +42,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--roofline-iters", type=int, default=10)
+    p.add_argument("--fuse", type=int, default=1,
+                   help="one fused append+decode launch per layer when the balanced kernel applies")
     return p.parse_args()
 
 
@@ -97,12 +99,18 @@ def main():
     plan = PagedAttention.plan(B, NQ, NKV, HD, BT, max_ctx, args.tps)
     ws = PagedAttention.workspace(plan)
     kname = PagedAttention.kernel_name(NQ, NKV, HD, BT, KvDataType.F16)
+    balanced = plan[0] == 0
+    fused = balanced and bool(args.fuse)
     kv, pa = PagedKvGpu(0), PagedAttention(0)
 
     def layer(i, s=None):
-        kv.append_kv_batched(s, layout, pools[i], newk[i], newv[i], d_tab, cu, start, B)
-        pa.decode_batched(s, qs[i], pools[i], d_tab, lens, outs[i], NQ, NKV, HD, BT,
-                          KvDataType.F16, plan, ws)
+        if fused:  # append + decode in one launch of the balanced kernel
+            pa.append_decode_batched(s, layout, pools[i], newk[i], newv[i], d_tab, start, qs[i],
+                                     outs[i], NQ, HD, plan, ws)
+        else:
+            kv.append_kv_batched(s, layout, pools[i], newk[i], newv[i], d_tab, cu, start, B)
+            pa.decode_batched(s, qs[i], pools[i], d_tab, lens, outs[i], NQ, NKV, HD, BT,
+                              KvDataType.F16, plan, ws)
 
     def step(s=None):
         for i in range(L):
@@ -150,18 +158,23 @@ def main():
     print(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}),"
           f" {value:.1f} GB/s, {tok_s:.0f} tok/s", file=sys.stderr, flush=True)
 
-    # Roofline of the decode launch alone (split kernel + merge): the 28
-    # layers' decode calls are captured in a graph on their own stream and
-    # replayed between two events on that stream, so host enqueue time never
-    # enters the measured interval.
+    # Roofline of the decode launch (split kernel + merge; with --fuse the
+    # same launch also appends the step's rows): the 28 layers' calls are
+    # captured in a graph on their own stream and replayed between two events
+    # on that stream, so host enqueue time never enters the measured interval.
+    # Replays rewrite the same rows at the same positions.
     dstream = torch.cuda.Stream()
     dstream.wait_stream(torch.cuda.current_stream())
     dgraph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(dstream):
         with torch.cuda.graph(dgraph, stream=dstream):
             for i in range(L):
-                pa.decode_batched(dstream, qs[i], pools[i], d_tab, lens, outs[i], NQ, NKV, HD, BT,
-                                  KvDataType.F16, plan, ws)
+                if fused:
+                    pa.append_decode_batched(dstream, layout, pools[i], newk[i], newv[i], d_tab,
+                                             start, qs[i], outs[i], NQ, HD, plan, ws)
+                else:
+                    pa.decode_batched(dstream, qs[i], pools[i], d_tab, lens, outs[i], NQ, NKV, HD,
+                                      BT, KvDataType.F16, plan, ws)
     torch.cuda.synchronize()
     ra, rb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(dstream):  # replay() launches on the current stream
@@ -173,7 +186,9 @@ def main():
     torch.cuda.synchronize()
     avg_ms = ra.elapsed_time(rb) / (args.roofline_iters * L)
     attended = int(lens.sum().item())
-    per_launch_bytes = attended * NKV * HD * 2 * 2
+    # KV rows read once per kv head; a fused launch also reads and writes the
+    # appended rows (B x 2 rows)
+    per_launch_bytes = attended * NKV * HD * 2 * 2 + (2 * B * 2 * rl * 2 if fused else 0)
     achieved = per_launch_bytes / (avg_ms / 1e3) / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_config2_traffic.json")
@@ -184,7 +199,8 @@ def main():
             traffic = tr.get("hbm_bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": kname + " + eh_decode_merge",
+                "kernel": kname + (" + eh_decode_tiles_merge" if balanced else " + eh_decode_merge")
+                + (" (fused append)" if fused else ""),
                 "avg_launch_us": round(avg_ms * 1e3, 2),
                 "algorithmic_bytes_per_launch": per_launch_bytes}
 
@@ -201,7 +217,7 @@ def main():
                                "page 16, f16 KV, ctx U[128,4096], 28 layers (append + decode)",
                    "batch": B, "layers": L, "n_head": NQ, "n_head_kv": NKV, "head_dim": HD,
                    "block_tokens": BT, "ctx_sum": ctx_before, "tokens_per_split": plan[0],
-                   "graph": bool(args.graph)},
+                   "grid": plan[1], "fused_append": fused, "graph": bool(args.graph)},
         "tok_s": round(tok_s, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": roofline, "cpu_baseline": cpu,
     }

@@ -147,9 +147,17 @@ eh_status eh_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype
                             uint64_t query_pos, int causal, const uint32_t* pos_ptr);
 
 /* ---- Batched decode (extension: B sequences in one launch).
- * eh_decode_plan picks tokens_per_split (0 = automatic; at most
- * 1022 * block_tokens) and the split bound (at most 256) for contexts up to
- * max_ctx, and the workspace size the call needs. */
+ * eh_decode_plan picks the kernel and its launch shape for contexts up to
+ * max_ctx, and the workspace size the call needs:
+ *   - hint 0 on a shape the token-balanced kernel serves (16-bit KV,
+ *     head_dim 128, 1/2/4/8 kv heads, at most 8 q heads per kv head,
+ *     power-of-two pages of at least 16 tokens, batch <= 2048):
+ *     tokens_per_split = 0 and max_splits = the grid (workgroups); the device
+ *     cuts the batch's 16-token tiles evenly among them from the live
+ *     lengths, so any context lengths are served (max_ctx is not a bound);
+ *   - otherwise fixed splits: tokens_per_split (hint rounded up to the
+ *     kernel's chunk, or automatic; at most 1022 * block_tokens) and the split
+ *     bound max_splits (at most 256). */
 eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uint32_t n_head_kv,
                          uint32_t head_dim, uint32_t block_tokens, uint32_t max_ctx,
                          uint32_t tokens_per_split_hint, uint32_t* tokens_per_split,
@@ -159,11 +167,11 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
 eh_status eh_decode_kernel_name(uint32_t kv_dtype, uint32_t n_head, uint32_t n_head_kv,
                                 uint32_t head_dim, uint32_t block_tokens, char* buf, uint64_t size);
 /* q/out [batch, n_head, head_dim] f32; block_tables [batch, bt_stride] u32;
- * ctx_lens [batch] u32 = tokens each query attends (its own position + 1),
- * each at most tokens_per_split * max_splits.  workspace, tokens_per_split
- * and max_splits come from eh_decode_plan; calls sharing one workspace must
- * not overlap in time.  Runs one split kernel and, when max_splits > 1, one
- * log-sum-exp merge kernel. */
+ * ctx_lens [batch] u32 = tokens each query attends (its own position + 1;
+ * with fixed splits each at most tokens_per_split * max_splits).  workspace,
+ * tokens_per_split and max_splits come from eh_decode_plan; calls sharing one
+ * workspace must not overlap in time.  Runs one split kernel and one
+ * log-sum-exp merge kernel (fixed splits: only when max_splits > 1). */
 eh_status eh_paged_decode_batched(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
                                   const float* q, uint64_t q_bytes, const void* pool,
                                   uint64_t pool_bytes, const uint32_t* block_tables,
@@ -172,6 +180,29 @@ eh_status eh_paged_decode_batched(eh_context* ctx, eh_stream stream, uint32_t kv
                                   uint32_t n_head_kv, uint32_t head_dim, uint32_t block_tokens,
                                   uint32_t tokens_per_split, uint32_t max_splits, void* workspace,
                                   uint64_t workspace_bytes);
+
+/* ---- Fused decode-step append + attention (extension: the batched
+ * PagedKvGpu::append_kv of paged_kv.rs:200-327 -- in production the decode
+ * append slot of NormRope::launch_fused_qk, norm_rope.cu:280-298 -- followed
+ * by PagedAttention::launch_with_pos_ptr, paged_attention.rs:177-345, for B
+ * sequences in ONE launch of the token-balanced kernel).  Row b of
+ * keys/values [batch, row_len] (pool element type) is written at logical
+ * position start_pos[b] (device u32) through block_tables + b*bt_stride,
+ * then q row b attends tokens 0..start_pos[b] inclusive.  Pool bytes after
+ * the call equal eh_append_kv_batched's; the output equals
+ * eh_paged_decode_batched's with ctx_lens = start_pos + 1.  Shapes: those of
+ * the token-balanced kernel (eh_decode_plan with hint 0 returns
+ * tokens_per_split 0; its max_splits is `grid` and its workspace size
+ * applies); other shapes return EH_UNSUPPORTED.  The appended page must not
+ * be read by another sequence of the same call (copy-on-write first). */
+eh_status eh_append_decode_batched(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                                   void* pool, uint64_t pool_bytes, const void* keys,
+                                   uint64_t keys_bytes, const void* values, uint64_t values_bytes,
+                                   const uint32_t* block_tables, uint64_t bt_bytes,
+                                   uint32_t bt_stride, const uint32_t* start_pos, uint32_t batch,
+                                   const float* q, uint64_t q_bytes, float* out, uint64_t out_bytes,
+                                   uint32_t n_head, uint32_t head_dim, uint32_t grid,
+                                   void* workspace, uint64_t workspace_bytes);
 
 /* ---- FlashAttention2::launch / launch_with_pos_ptr (flash_attention.rs:95-225):
  * causal chunked prefill.  q/out [q_tokens, n_head, head_dim] f32; query i

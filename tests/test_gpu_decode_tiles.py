@@ -1,0 +1,295 @@
+"""GPU parity of the token-balanced decode kernel (eh_decode_tiles_*) and of
+the fused decode-step append + attention (eh_append_decode_batched) against
+the oracle.
+
+Tolerance (the benchmark contract for 16-bit KV with f32 accumulation):
+|gpu - ref| <= 2e-3 + 1e-3*|ref| against sdpa_decode on the exactly widened
+pool; appended pool bytes bit-exact against the oracle's append.  The cases
+drive every piece of the device-side work split: ragged and empty sequences,
+runs that cover several sequences (and more than one LDS round), runs longer
+than a page-id batch (a grid forced small), masked block-table entries,
+pages of 16 and 32 tokens, and graph replay with growing positions.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import orc
+from titan_amd import KvDataType, PagedAttention, PagedKvGpu, PagedKvLayout
+from titan_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TD = {KvDataType.F16: torch.float16, KvDataType.BF16: torch.bfloat16}
+NONE = 0xFFFFFFFF
+
+
+def i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev)
+
+
+def check_close(gpu, ref):
+    gpu, ref = np.asarray(gpu, np.float64), np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(gpu))
+    bad = np.abs(gpu - ref) > 2e-3 + 1e-3 * np.abs(ref)
+    assert not bad.any(), f"max abs err {np.max(np.abs(gpu - ref))} at {np.argwhere(bad)[:4]}"
+
+
+def make_tables(rng, lens, bt, spare=3):
+    lens = np.asarray(lens, np.int64)
+    need = [(int(l) + bt - 1) // bt for l in lens]
+    stride = max(max(need), 1)
+    nb = sum(need) + spare
+    perm = rng.permutation(nb).astype(np.uint32)
+    tab = np.full((len(lens), stride), NONE, np.uint32)
+    pos = 0
+    for b, c in enumerate(need):
+        tab[b, :c] = perm[pos:pos + c]
+        pos += c
+    return tab, nb
+
+
+def make_pool(rng, nb, bt, n_kv, hd, dtype, dev):
+    host = torch.from_numpy(rng.standard_normal(nb * bt * 2 * n_kv * hd).astype(np.float32))
+    t = host.to(TD[dtype])
+    return t.to(dev), t.to(torch.float32).numpy()
+
+
+def run_decode(dev, dtype, lens, shape, seed, grid=None, tab=None, nb=None):
+    n_head, n_kv, hd, bt = shape
+    rng = np.random.default_rng(seed)
+    if tab is None:
+        tab, nb = make_tables(rng, lens, bt)
+    pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, dtype, dev)
+    B = len(lens)
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(max(lens)), 0, dtype)
+    assert plan[0] == 0, "shape should take the token-balanced kernel"
+    if grid is not None:
+        plan = (0, grid, plan[2])
+    ws = PagedAttention.workspace(plan)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                     i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, plan, ws)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), pool_f32, tab, q
+
+
+SHAPES = [(12, 2, 128, 16), (32, 8, 128, 16), (8, 1, 128, 32), (16, 4, 128, 16),
+          (14, 2, 128, 16), (24, 8, 128, 16), (2, 2, 128, 64), (4, 4, 128, 16)]
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_tiles_ragged_matches_sdpa(dev, dtype, shape):
+    lens = np.array([0, 1, 15, 16, 17, 300, 2049, 0, 33, 1000, 7], np.int64)
+    out, pool_f32, tab, q = run_decode(dev, dtype, lens, shape, sum(shape))
+    n_head, n_kv, hd, bt = shape
+    ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
+    check_close(out, ref)
+
+
+@pytest.mark.parametrize("grid", [1, 2, 3, 7, 64])
+def test_tiles_small_grids(dev, grid):
+    """Few workgroups: one run covers several sequences (several LDS
+    rounds) and a wave walks more tiles than one page-id batch holds."""
+    lens = np.array([3000, 1, 2000, 0, 5, 1500, 16, 31, 777], np.int64)
+    shape = (12, 2, 128, 16)
+    out, pool_f32, tab, q = run_decode(dev, KvDataType.F16, lens, shape, 100 + grid, grid=grid)
+    ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), 16, q, 12, 2, 128)
+    check_close(out, ref)
+
+
+def test_tiles_many_short_sequences(dev):
+    rng = np.random.default_rng(77)
+    lens = rng.integers(0, 48, size=700).astype(np.int64)
+    shape = (8, 2, 128, 16)
+    out, pool_f32, tab, q = run_decode(dev, KvDataType.F16, lens, shape, 78)
+    ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), 16, q, 8, 2, 128)
+    check_close(out, ref)
+
+
+def test_tiles_masked_pages(dev):
+    """Block-table entries past the pool mask their 16 tokens: the result
+    equals attention over the remaining tokens."""
+    rng = np.random.default_rng(3)
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    lens = np.array([200, 90, 64], np.int64)
+    tab, nb = make_tables(rng, lens, bt)
+    tab[0, 3] = nb + 5          # past the pool
+    tab[1, 0] = NONE
+    tab[2, 3] = NONE            # the last page
+    pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)
+    q = rng.standard_normal((3, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(3, n_head, n_kv, hd, bt, 200, 0, KvDataType.F16)
+    ws = PagedAttention.workspace(plan)
+    out = torch.full((3, n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                     i32(lens, dev), out, n_head, n_kv, hd, bt, KvDataType.F16,
+                                     plan, ws)
+    torch.cuda.synchronize()
+    # reference: the unmasked pages, in order, as a contiguous sequence
+    pages = pool_f32.reshape(nb, bt * 2 * n_kv * hd)
+    for b in range(3):
+        keep = [int(p) for p in tab[b, :(int(lens[b]) + bt - 1) // bt] if p < nb]
+        n = sum(min(bt, int(lens[b]) - bt * j) for j, p in
+                enumerate(tab[b, :(int(lens[b]) + bt - 1) // bt]) if p < nb)
+        sub = np.concatenate([pages[p] for p in keep]) if keep else np.zeros(1, np.float32)
+        ident = np.arange(len(keep), dtype=np.uint32)
+        ref = orc.sdpa_decode_batched(sub, ident[None], np.array([n], np.uint32), bt,
+                                      q[b:b + 1], n_head, n_kv, hd)
+        check_close(out.cpu().numpy()[b:b + 1], ref)
+
+
+def test_tiles_workspace_reuse(dev):
+    """One workspace serves calls of different batch and lengths in a row."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    big = PagedAttention.plan(40, n_head, n_kv, hd, bt, 4096, 0, KvDataType.F16)
+    ws = PagedAttention.workspace(big)
+    pa = PagedAttention(0)
+    rng = np.random.default_rng(8)
+    for B in (40, 3, 40, 17):
+        lens = rng.integers(0, 4096, size=B).astype(np.int64)
+        tab, nb = make_tables(rng, lens, bt)
+        pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)
+        q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+        plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, 4096, 0, KvDataType.F16)
+        assert plan[2] <= big[2]
+        out = torch.full((B, n_head, hd), float("nan"), device=dev)
+        pa.decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev), i32(lens, dev),
+                          out, n_head, n_kv, hd, bt, KvDataType.F16, plan, ws)
+        torch.cuda.synchronize()
+        ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
+        check_close(out.cpu().numpy(), ref)
+
+
+def fused_case(dev, dtype, starts, shape, seed, grid=None):
+    n_head, n_kv, hd, bt = shape
+    rl = n_kv * hd
+    rng = np.random.default_rng(seed)
+    starts = np.asarray(starts, np.int64)
+    tab, nb = make_tables(rng, starts + 1, bt)
+    pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, dtype, dev)
+    B = len(starts)
+    newk = torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).to(TD[dtype])
+    newv = torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).to(TD[dtype])
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    layout = PagedKvLayout(nb, bt, rl, dtype)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(starts.max()) + 1, 0, dtype)
+    if grid is not None:
+        plan = (0, grid, plan[2])
+    ws = PagedAttention.workspace(plan)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).append_decode_batched(None, layout, pool, newk.to(dev), newv.to(dev),
+                                            i32(tab, dev), i32(starts, dev),
+                                            torch.from_numpy(q).to(dev), out, n_head, hd, plan, ws)
+    torch.cuda.synchronize()
+    # oracle: the same append on the host copy, then sdpa over start+1 tokens
+    p = pool_f32.reshape(nb, bt, 2, rl)
+    for b in range(B):
+        s = int(starts[b])
+        p[tab[b, s // bt], s % bt, 0] = newk[b].float().numpy()
+        p[tab[b, s // bt], s % bt, 1] = newv[b].float().numpy()
+    got = pool.cpu()
+    want = torch.from_numpy(pool_f32).to(TD[dtype])
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), "appended pool differs"
+    ref = orc.sdpa_decode_batched(pool_f32, tab, (starts + 1).astype(np.uint32), bt, q, n_head,
+                                  n_kv, hd)
+    check_close(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
+@pytest.mark.parametrize("shape", [(12, 2, 128, 16), (32, 8, 128, 16), (8, 1, 128, 32)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_fused_append_decode(dev, dtype, shape):
+    starts = [0, 15, 16, 31, 100, 2047, 2048, 5, 639]
+    fused_case(dev, dtype, starts, shape, 11 + sum(shape))
+
+
+@pytest.mark.parametrize("grid", [1, 5])
+def test_fused_append_decode_small_grid(dev, grid):
+    fused_case(dev, KvDataType.F16, [1000, 0, 17, 3000, 63], (12, 2, 128, 16), 50 + grid, grid)
+
+
+def test_fused_config2_one_layer_full_size(dev):
+    """Benchmark config 2 at full size through the fused entry point: 32
+    sequences, ctx U[128,4096] + 1 appended, 12/2 heads, hd 128, f16."""
+    s = synth.config2(0, extra_tokens=1)
+    rng = np.random.default_rng(1)
+    tab = synth.block_tables(s, extra_tokens=1)
+    host = torch.from_numpy(rng.standard_normal(s.n_blocks * 16 * 2 * s.row_len)
+                            .astype(np.float32)).half()
+    pool = host.to(dev)
+    pool_f32 = host.float().numpy()
+    newk = torch.from_numpy(rng.standard_normal((32, s.row_len)).astype(np.float32)).half()
+    newv = torch.from_numpy(rng.standard_normal((32, s.row_len)).astype(np.float32)).half()
+    q = rng.standard_normal((32, 12, 128)).astype(np.float32)
+    layout = PagedKvLayout(s.n_blocks, 16, s.row_len, KvDataType.F16)
+    plan = PagedAttention.plan(32, 12, 2, 128, 16, int(s.ctx_lens.max()) + 1)
+    assert plan[0] == 0
+    ws = PagedAttention.workspace(plan)
+    out = torch.empty((32, 12, 128), device=dev)
+    PagedAttention(0).append_decode_batched(None, layout, pool, newk.to(dev), newv.to(dev),
+                                            i32(tab, dev), i32(s.ctx_lens, dev),
+                                            torch.from_numpy(q).to(dev), out, 12, 128, plan, ws)
+    torch.cuda.synchronize()
+    p = pool_f32.reshape(-1, 16, 2, s.row_len)
+    for b in range(32):
+        L = int(s.ctx_lens[b])
+        p[tab[b, L // 16], L % 16, 0] = newk[b].float().numpy()
+        p[tab[b, L // 16], L % 16, 1] = newv[b].float().numpy()
+    assert np.array_equal(pool.float().cpu().numpy(), pool_f32)
+    ref = orc.sdpa_decode_batched(pool_f32, tab, (s.ctx_lens + 1).astype(np.uint32), 16, q, 12, 2,
+                                  128)
+    check_close(out.cpu().numpy(), ref)
+
+
+def test_fused_graph_replay_growing_positions(dev):
+    """The fused step captured once and replayed as positions grow (the work
+    split follows the device lengths) equals eager append + decode."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl = n_kv * hd
+    B, steps = 6, 5
+    rng = np.random.default_rng(12)
+    start0 = np.array([0, 14, 31, 500, 1023, 77], np.int64)
+    tab, nb = make_tables(rng, start0 + steps + 1, bt)
+    host = torch.from_numpy(rng.standard_normal(nb * bt * 2 * rl).astype(np.float32)).half()
+    pool_g, pool_e = host.to(dev), host.to(dev)
+    layout = PagedKvLayout(nb, bt, rl, KvDataType.F16)
+    dtab = i32(tab, dev)
+    pos = i32(start0, dev)
+    k = torch.empty((B, rl), dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    q = torch.empty((B, n_head, hd), device=dev)
+    out_g = torch.empty((B, n_head, hd), device=dev)
+    out_e = torch.empty_like(out_g)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(start0.max()) + steps + 1)
+    ws_g, ws_e = PagedAttention.workspace(plan), PagedAttention.workspace(plan)
+    pa, kv = PagedAttention(0), PagedKvGpu(0)
+    cu = i32(np.arange(B + 1), dev)
+    pa.append_decode_batched(None, layout, pool_g, k, v, dtab, pos, q, out_g, n_head, hd, plan, ws_g)
+    torch.cuda.synchronize()
+    pool_g.copy_(host.to(dev))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            pa.append_decode_batched(s, layout, pool_g, k, v, dtab, pos, q, out_g, n_head, hd, plan,
+                                     ws_g)
+    torch.cuda.synchronize()
+    for step in range(steps):
+        k.copy_(torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).half())
+        v.copy_(torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).half())
+        q.copy_(torch.from_numpy(rng.standard_normal((B, n_head, hd)).astype(np.float32)))
+        pos.copy_(i32(start0 + step, dev))
+        torch.cuda.synchronize()
+        kv.append_kv_batched(None, layout, pool_e, k, v, dtab, cu, pos, B)
+        lens = pos + 1
+        pa.decode_batched(None, q, pool_e, dtab, lens, out_e, n_head, n_kv, hd, bt,
+                          KvDataType.F16, plan, ws_e)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(pool_g.view(torch.int16), pool_e.view(torch.int16))
+        assert torch.max(torch.abs(out_g - out_e)).item() < 1e-6

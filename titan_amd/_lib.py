@@ -50,6 +50,8 @@ _SIGS = {
     "eh_decode_kernel_name": (i32, [u32, u32, u32, u32, u32, C.c_char_p, u64]),
     "eh_paged_decode_batched": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, u32, vp, u64,
                                       u32, u32, u32, u32, u32, u32, vp, u64]),
+    "eh_append_decode_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp, u64,
+                                       u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp, u64]),
     "eh_flash_attention_prefill": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64,
                                          u64, u64, u64, u64, vp]),
     "eh_prefill_batched": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, vp, u32, u32, u32,

@@ -4,6 +4,8 @@ Outputs (git-ignored, shipped in-tree to the GPU box):
   titan_amd/lib/paged_kv.hsaco      append / gather / page copy / table kernels
   titan_amd/lib/paged_decode_{f32,f16,bf16}.hsaco  split-K decode attention
   titan_amd/lib/paged_prefill.hsaco  MFMA causal chunked prefill
+  titan_amd/lib/paged_decode_tiles_{f16,bf16}.hsaco  token-balanced decode
+      (MFMA q.k, optional fused append)
   titan_amd/lib/libengine_hip.so    hipModuleLoad / hipModuleLaunchKernel C-ABI
 """
 import os
@@ -25,6 +27,8 @@ KERNELS = [
     ("paged_decode_f16", "paged_decode", ["-DEH_ONLY_DT=1"]),
     ("paged_decode_bf16", "paged_decode", ["-DEH_ONLY_DT=2"]),
     ("paged_prefill", "paged_prefill", []),
+    ("paged_decode_tiles_f16", "paged_decode_tiles", ["-DEH_ONLY_DT=1"]),
+    ("paged_decode_tiles_bf16", "paged_decode_tiles", ["-DEH_ONLY_DT=2"]),
 ]
 
 # Packed-FP32 instructions are disabled for all device code on this pool.

@@ -24,6 +24,7 @@ struct eh_context {
     hipModule_t mod_kv = nullptr;
     hipModule_t mod_decode[3] = {nullptr, nullptr, nullptr};  // f32, f16, bf16
     hipModule_t mod_prefill = nullptr;
+    hipModule_t mod_tiles[2] = {nullptr, nullptr};  // token-balanced decode: f16, bf16
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
     // Split-K scratch for eh_flash_decoding, allocated once at creation
@@ -86,16 +87,22 @@ eh_status get_fn(eh_context* c, hipModule_t mod, const char* name, hipFunction_t
 }
 
 template <typename... A>
-eh_status launch(eh_context* c, hipModule_t mod, const char* name, dim3 grid, dim3 block,
-                 eh_stream stream, A... a) {
+eh_status launch_lds(eh_context* c, hipModule_t mod, const char* name, dim3 grid, dim3 block,
+                     uint32_t lds_bytes, eh_stream stream, A... a) {
     hipFunction_t f = nullptr;
     eh_status st = get_fn(c, mod, name, &f);
     if (st != EH_OK) return st;
     void* argv[] = {static_cast<void*>(&a)...};
-    hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
-                                         (hipStream_t)stream, argv, nullptr);
+    hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                         lds_bytes, (hipStream_t)stream, argv, nullptr);
     if (e != hipSuccess) return fail(EH_KERNEL_LAUNCH, "hipModuleLaunchKernel", 0, 0, (int)e);
     return EH_OK;
+}
+
+template <typename... A>
+eh_status launch(eh_context* c, hipModule_t mod, const char* name, dim3 grid, dim3 block,
+                 eh_stream stream, A... a) {
+    return launch_lds(c, mod, name, grid, block, 0, stream, a...);
 }
 
 uint64_t elt_bytes(uint32_t dt) {
@@ -290,6 +297,92 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
                   a.seq_tokens, a.query_pos, a.causal, a.n_head, a.head_dim, a.tps, a.max_splits);
 }
 
+// ---- token-balanced decode (eh_decode_tiles_*, paged_decode_tiles.hip)
+// Serves 16-bit KV with head_dim 128, 1/2/4/8 kv heads, at most 8 q heads per
+// kv head and power-of-two pages of at least 16 tokens.  A workgroup is one
+// wave per kv head; the grid fills every CU at two waves per SIMD; the device
+// cuts the batch's tiles evenly among the workgroups from the live lengths.
+constexpr uint32_t kTilesMaxBatch = 2048;  // lengths + tile prefix staged in LDS
+constexpr uint32_t kTilesQSeg = 2;         // mirrors QSEG in paged_decode_tiles.hip
+constexpr uint32_t kTilesVRow = 288;       // mirrors VROW in paged_decode_tiles.hip
+
+struct tiles_cfg {
+    bool ok = false;
+    uint32_t g = 0, nw = 1;  // compiled head-group width, waves (= kv heads) per workgroup
+};
+
+tiles_cfg pick_tiles(uint32_t kv_dtype, uint64_t head_dim, uint64_t n_head, uint64_t n_head_kv,
+                     uint64_t block_tokens, uint64_t batch) {
+    tiles_cfg t;
+    if (kv_dtype != EH_KV_F16 && kv_dtype != EH_KV_BF16) return t;
+    if (head_dim != 128 || n_head_kv == 0 || n_head % n_head_kv) return t;
+    if (!(n_head_kv == 1 || n_head_kv == 2 || n_head_kv == 4 || n_head_kv == 8)) return t;
+    const uint64_t group = n_head / n_head_kv;
+    if (group < 1 || group > 8) return t;
+    if (block_tokens < 16 || (block_tokens & (block_tokens - 1))) return t;
+    if (batch > kTilesMaxBatch) return t;
+    for (uint32_t g : {1u, 2u, 4u, 6u, 8u})
+        if (g >= group) { t.g = g; break; }
+    t.nw = (uint32_t)n_head_kv;
+    t.ok = true;
+    return t;
+}
+
+uint32_t device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+        return (uint32_t)n;
+    return 256;  // MI355X
+}
+
+// 8 waves per CU (two per SIMD): 8 / n_kv workgroups per CU
+uint32_t tiles_grid(const tiles_cfg& t) { return device_cus() * (8u / t.nw); }
+
+uint64_t tiles_ws_bytes(uint64_t grid, uint64_t batch, uint64_t n_head) {
+    return 4ull * (grid + batch) * n_head * (128 + 2);
+}
+
+struct tiles_args {
+    uint32_t kv_dtype;
+    const float* q;
+    void* pool;
+    uint64_t n_blocks;
+    const uint32_t* bt;
+    uint32_t bt_stride;
+    const uint32_t* lens;
+    uint32_t lens_add;
+    const void* new_k;
+    const void* new_v;
+    uint32_t batch;
+    float* out;
+    uint32_t n_head, n_head_kv, block_tokens, grid;
+    void* ws;
+};
+
+eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const tiles_cfg& t) {
+    char name[64];
+    std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u", dt_name(a.kv_dtype), t.g);
+    const hipModule_t mod = c->mod_tiles[a.kv_dtype == EH_KV_F16 ? 0 : 1];
+    const float scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;  // paged_attention.rs:286
+    // per-wave V tiles (16 rows x kTilesVRow bytes) and staged q rows
+    // (kTilesQSeg sequences x g heads x 128 f32), the tile prefix and token
+    // counts of the batch
+    const uint32_t lds = t.nw * (16 * kTilesVRow + kTilesQSeg * t.g * 128 * 4) + 4u * (2 * a.batch + 1);
+    float* part_acc = (float*)a.ws;
+    float* part_ml = part_acc + (uint64_t)(a.grid + a.batch) * a.n_head * 128;
+    eh_status st = launch_lds(c, mod, name, dim3(a.grid), dim3(t.nw * 64), lds, stream, a.q,
+                              (uint8_t*)a.pool, a.n_blocks, a.bt, a.bt_stride, a.lens, a.lens_add,
+                              (const uint8_t*)a.new_k, (const uint8_t*)a.new_v, a.batch, a.out,
+                              part_acc, part_ml, a.n_head, a.n_head_kv, a.block_tokens,
+                              (uint32_t)log2_exact(a.block_tokens), scale_log2);
+    if (st != EH_OK) return st;
+    return launch(c, mod, "eh_decode_tiles_merge",
+                  dim3((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch), dim3(256), stream,
+                  (const float*)part_acc, (const float*)part_ml, a.out, a.lens, a.lens_add, a.batch,
+                  a.n_head, 128u, a.grid);
+}
+
 // Splits: aim for enough workgroups to fill 256 CUs several times over, with
 // at most kMaxSplits splits and a block-table slice that fits LDS.
 uint64_t auto_tps(uint64_t batch, uint64_t units, uint64_t max_ctx, uint64_t block_tokens,
@@ -451,6 +544,15 @@ eh_status eh_create(int device, const char* code_object_dir, eh_context** out) {
         eh_destroy(c);
         return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_prefill)", 0, 0, (int)e);
     }
+    const char* tile_names[2] = {"/paged_decode_tiles_f16.hsaco", "/paged_decode_tiles_bf16.hsaco"};
+    for (int i = 0; i < 2; ++i) {
+        const std::string path = dir + tile_names[i];
+        e = hipModuleLoad(&c->mod_tiles[i], path.c_str());
+        if (e != hipSuccess) {
+            eh_destroy(c);
+            return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_decode_tiles)", 0, 0, (int)e);
+        }
+    }
     e = hipMalloc((void**)&c->scratch, kScratchFloats * sizeof(float));
     if (e != hipSuccess) {
         eh_destroy(c);
@@ -469,6 +571,8 @@ void eh_destroy(eh_context* c) {
     for (hipModule_t m : c->mod_decode)
         if (m) hipModuleUnload(m);
     if (c->mod_prefill) hipModuleUnload(c->mod_prefill);
+    for (hipModule_t m : c->mod_tiles)
+        if (m) hipModuleUnload(m);
     delete c;
 }
 
@@ -708,6 +812,14 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
     if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return fail(EH_INVALID_ARGS, "heads");
     if (block_tokens < 1) return fail(EH_INVALID_ARGS, "block_tokens");
     if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
+    const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, batch);
+    if (hint == 0 && tc.ok) {  // token-balanced kernel: tokens_per_split 0, max_splits = grid
+        const uint32_t grid = tiles_grid(tc);
+        if (tokens_per_split) *tokens_per_split = 0;
+        if (max_splits) *max_splits = grid;
+        if (workspace_bytes) *workspace_bytes = tiles_ws_bytes(grid, batch, n_head);
+        return EH_OK;
+    }
     const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
     uint64_t tps = hint ? div_ceil(hint, dk.chunk) * dk.chunk
                         : auto_tps(batch, dk.units, max_ctx, block_tokens, dk.chunk,
@@ -729,8 +841,11 @@ eh_status eh_decode_kernel_name(uint32_t kv_dtype, uint32_t n_head, uint32_t n_h
     const char* dn = dt_name(kv_dtype);
     if (!dn) return fail(EH_UNSUPPORTED, "kv_dtype");
     const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
+    const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, 1);
     char name[64];
-    if (dk.slots)
+    if (tc.ok)
+        std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u", dn, tc.g);
+    else if (dk.slots)
         std::snprintf(name, sizeof name, "eh_decode_slots_%s_hd%u_h%u", dn, head_dim, dk.gh);
     else
         std::snprintf(name, sizeof name, "eh_decode_split_%s_hd%u_g%u", dn, head_dim, dk.g);
@@ -754,8 +869,40 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     if (block_tokens < 1) return invalid_size(1, block_tokens);
     if (batch == 0) return EH_OK;
     if (!ctx_lens) return fail(EH_INVALID_ARGS, "ctx_lens is null");
-    if (tps < 1) return invalid_size(1, tps, "tokens_per_split");
     if (max_splits < 1) return invalid_size(1, max_splits, "max_splits");
+    if (tps == 0) {  // token-balanced kernel, max_splits workgroups
+        const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+        if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+        if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+        const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+        if (bt_stride == 0 || bt_bytes < bt_expected)
+            return invalid_size(bt_expected, bt_bytes, "block_tables");
+        const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, batch);
+        if (!tc.ok) return fail(EH_UNSUPPORTED, "tokens_per_split 0: shape outside the balanced kernel");
+        const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * 2;
+        if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
+        const uint64_t ws_need = tiles_ws_bytes(max_splits, batch, n_head);
+        if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
+        eh_status st = bind(c);
+        if (st) return st;
+        tiles_args a{};
+        a.kv_dtype = kv_dtype;
+        a.q = q;
+        a.pool = const_cast<void*>(pool);
+        a.n_blocks = pool_bytes / page_bytes;
+        a.bt = bt;
+        a.bt_stride = bt_stride;
+        a.lens = ctx_lens;
+        a.lens_add = 0;
+        a.batch = batch;
+        a.out = out;
+        a.n_head = n_head;
+        a.n_head_kv = n_head_kv;
+        a.block_tokens = block_tokens;
+        a.grid = max_splits;
+        a.ws = ws;
+        return run_tiles(c, stream, a, tc);
+    }
     const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
@@ -790,6 +937,59 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     a.part_acc = (float*)ws;
     a.part_ml = (float*)ws + (uint64_t)batch * n_head * max_splits * head_dim;
     return run_decode(c, stream, a);
+}
+
+eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                                  void* pool, uint64_t pool_bytes, const void* keys,
+                                  uint64_t keys_bytes, const void* values, uint64_t values_bytes,
+                                  const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                                  const uint32_t* start_pos, uint32_t batch, const float* q,
+                                  uint64_t q_bytes, float* out, uint64_t out_bytes, uint32_t n_head,
+                                  uint32_t head_dim, uint32_t grid, void* ws, uint64_t ws_bytes) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (batch == 0) return EH_OK;
+    if (!start_pos) return fail(EH_INVALID_ARGS, "start_pos is null");
+    if (head_dim < 1 || l->row_len % head_dim) return invalid_size(head_dim, l->row_len % (head_dim ? head_dim : 1));
+    const uint64_t n_head_kv = l->row_len / head_dim;
+    if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return invalid_size(n_head_kv, n_head);
+    const uint64_t elt = elt_bytes(l->data_type);
+    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    if (l->n_blocks < 1 || page_bytes == 0) return fail(EH_INVALID_ARGS, "layout");
+    if (pool_bytes < l->n_blocks * page_bytes) return invalid_size(l->n_blocks * page_bytes, pool_bytes);
+    const uint64_t row_expected = (uint64_t)batch * l->row_len * elt;
+    if (keys_bytes < row_expected) return invalid_size(row_expected, keys_bytes);
+    if (values_bytes < row_expected) return invalid_size(row_expected, values_bytes);
+    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
+    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+    if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+    const tiles_cfg tc = pick_tiles(l->data_type, head_dim, n_head, n_head_kv, l->block_tokens, batch);
+    if (!tc.ok) return fail(EH_UNSUPPORTED, "fused append+decode: shape outside the balanced kernel");
+    if (grid < 1) return invalid_size(1, grid, "grid");
+    const uint64_t ws_need = tiles_ws_bytes(grid, batch, n_head);
+    if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
+    eh_status st = bind(c);
+    if (st) return st;
+    tiles_args a{};
+    a.kv_dtype = l->data_type;
+    a.q = q;
+    a.pool = pool;
+    a.n_blocks = l->n_blocks;
+    a.bt = bt;
+    a.bt_stride = bt_stride;
+    a.lens = start_pos;
+    a.lens_add = 1;
+    a.new_k = keys;
+    a.new_v = values;
+    a.batch = batch;
+    a.out = out;
+    a.n_head = n_head;
+    a.n_head_kv = (uint32_t)n_head_kv;
+    a.block_tokens = (uint32_t)l->block_tokens;
+    a.grid = grid;
+    a.ws = ws;
+    return run_tiles(c, stream, a, tc);
 }
 
 eh_status eh_flash_attention_prefill(eh_context* c, eh_stream stream, uint32_t kv_dtype,

@@ -1,0 +1,671 @@
+// paged_decode_tiles.hip -- token-balanced paged decode for gfx950 (CDNA4, wave64).
+//
+// Semantics: the reference decode attention (engine-cuda/kernels/
+// paged_attention.cu:6-103, split-K form :200-369) and its CPU authority
+// sdpa_decode (engine-core/src/forward_cpu.rs:424-510): q head qh reads kv
+// head qh / (n_head / n_head_kv), attends logical tokens t < n_b with
+// scores q.k / sqrt(head_dim), out = softmax-weighted V (zeros if n_b == 0).
+// With new_k/new_v the launch first appends one token per sequence at
+// position n_b - 1 (the scatter of paged_kv.cu:13-45 / the decode-time append
+// slot of norm_rope.cu:280-298) and attends it in the same pass.
+//
+// Work decomposition (MI355X-first):
+//   * the ragged batch is cut into 16-token tiles; every workgroup of the
+//     grid takes an equal run of consecutive tiles of the flattened
+//     (sequence, tile) order, cut on the device from the live lengths, so
+//     the load is balanced whatever the context mix and a captured graph
+//     stays correct as contexts grow;
+//   * a workgroup has one wave per kv head; the waves walk the same tiles,
+//     so together they stream whole pages (all kv heads of each token slot),
+//     and each wave owns the complete softmax state of its q heads;
+//   * q.k is one MFMA tile per 16 tokens: S[16 tok x 16 heads] =
+//     K[16 x 128] . Q^T with v_mfma_f32_16x16x32 (f16 or bf16), q split into
+//     hi + lo 16-bit halves (two MFMAs per step) so scores keep ~22 bits;
+//   * the score tile leaves lane (g, x) = (lane / 16, lane % 16) with the
+//     scores of tokens 4g..4g+3 for head x; the online softmax runs there in
+//     the log2 domain with a lazy rescale (the running max only moves when a
+//     score exceeds it by 2^8; every weight uses the same stale max, exact);
+//   * P.V is MFMA too: O^T[16 dims x 16 heads] += V^T . P^T with
+//     v_mfma_f32_16x16x16.  P^T is exactly the score tile each lane holds
+//     (f16 P; bf16 P as hi + lo halves); V^T comes from the V tile staged in
+//     LDS through the gfx950 transposed read ds_read_b64_tr_b16;
+//   * every wave keeps DEPTH tiles of K/V loads in flight (16-byte lanes,
+//     K in the MFMA A layout) and fetches its page ids in batches of 64
+//     tiles, read back by v_readlane;
+//   * a wave writes its state when its run leaves a sequence: the final
+//     rows when the whole sequence lies in the workgroup, else one partial
+//     (m, l, acc) that eh_decode_tiles_merge combines.
+// Pages must be a power of two of at least 16 tokens; head_dim 128;
+// at most 8 q heads per kv head; block-table entries past the table or the
+// pool mask their tokens.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+enum { DT_F16 = 1, DT_BF16 = 2 };
+
+constexpr int TILE = 16;         // tokens per tile (MFMA rows)
+constexpr int QSEG = 2;          // sequences per run whose q is staged in LDS up front
+constexpr float RESCALE = 8.0f;  // lazy-rescale threshold, log2 domain
+constexpr float NEG_BIG = -1e30f;
+constexpr int VROW = 288;        // LDS bytes per V token row (256 + 32: conflict-free transposed reads)
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// Transposed LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane
+// 4r + b points at 4 consecutive 16-bit elements of row r (columns 4b..4b+3)
+// of a 4 x 16 block; lane c receives column c of rows 0..3.
+__device__ __forceinline__ uint64_t lds_read_tr(const uint8_t* p) {
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(const_cast<uint8_t*>(p)));
+    return __builtin_bit_cast(uint64_t, v);
+}
+
+template <int DT> struct kvt;
+template <> struct kvt<DT_F16> {
+    typedef f16x8 v8;
+    typedef f16x2 v2;
+    typedef _Float16 s;
+    static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    // 16x16x16 step on raw 4 x 16-bit operands
+    static __device__ __forceinline__ f32x4 mma16(uint64_t a, uint64_t b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                     __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+    }
+};
+template <> struct kvt<DT_BF16> {
+    typedef bf16x8 v8;
+    typedef bf16x2 v2;
+    typedef __bf16 s;
+    static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 mma16(uint64_t a, uint64_t b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a),
+                                                         __builtin_bit_cast(bf16x4, b), c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b),
+                                               c, false);
+    }
+};
+
+template <int N> struct ic { static constexpr int value = N; };
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(ic<I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+// f(ic<I>) for I = 0, 1, ... while it returns true, each call nested inside
+// the previous one's branch: no control-flow merge between the steps, so the
+// compiler's load counters stay exact along the chain.
+template <int I, int N, typename F>
+__device__ __forceinline__ void nested_for(F&& f) {
+    if constexpr (I < N) {
+        if (f(ic<I>{})) nested_for<I + 1, N>(f);
+    }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup barrier ordering LDS only: global loads and stores still in
+// flight (the tile stream, partial writes) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ uint32_t uni(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+// Even cut of T tiles over P workgroups: T = q P + r, workgroup w < r takes
+// q + 1 tiles, the others q (empty workgroups, when T < P, come last).
+struct tile_split {
+    uint32_t q, r;
+    __device__ __forceinline__ uint32_t first(uint32_t w) const { return w * q + (w < r ? w : r); }
+    // workgroup holding tile f
+    __device__ __forceinline__ uint32_t owner(uint32_t f) const {
+        const uint32_t big = r * (q + 1);
+        return f < big ? f / (q + 1) : r + (f - big) / q;
+    }
+};
+__device__ __forceinline__ tile_split make_split(uint32_t T, uint32_t P) {
+    return tile_split{T / P, T % P};
+}
+
+// Two floats as a packed 16-bit pair (RNE), low half first.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    typedef typename kvt<DT>::s S;
+    typedef typename kvt<DT>::v2 V2;
+    const V2 v = {(S)a, (S)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+template <int DT>
+__device__ __forceinline__ float lo_part(float a) {
+    typedef typename kvt<DT>::s S;
+    return a - (float)(S)a;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Split kernel.  Grid: P workgroups (1-D) of n_kv waves; wave kv serves kv
+// head kv on every tile of the workgroup's run.  Dynamic LDS (bytes):
+// n_kv*16*VROW (V tiles) + n_kv*QSEG*G*128*4 (staged q rows) +
+// 4*(2*batch + 1) (tile prefix, token counts).  lens[b] + lens_add = tokens
+// sequence b attends (lens_add = 1 when lens are the positions of a fused
+// append).  Partials: slot w + b for workgroup w and sequence b,
+// part_acc [slots, n_head, 128], part_ml [slots, n_head, 2], slots = P + batch.
+template <int DT, int G, int DEPTH, int CHUNK>
+__device__ __forceinline__ void decode_tiles(
+    const float* __restrict__ q, uint8_t* pool, uint64_t n_blocks,
+    const uint32_t* __restrict__ bt, uint32_t bt_stride, const uint32_t* __restrict__ lens,
+    uint32_t lens_add, const uint8_t* __restrict__ new_k, const uint8_t* __restrict__ new_v,
+    uint32_t batch, float* __restrict__ out, float* __restrict__ part_acc,
+    float* __restrict__ part_ml, uint32_t n_head, uint32_t n_head_kv,
+    uint32_t block_tokens, uint32_t bt_shift, float scale_log2) {
+    constexpr int HD = 128;
+    constexpr int KSTEPS = HD / 32;  // MFMA steps over head_dim
+    typedef kvt<DT> K;
+    typedef typename K::v8 V8;
+    static_assert(G <= 16, "one 16-column score tile per kv head");
+
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const uint32_t NW = blockDim.x >> 6;  // == n_head_kv
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t kv = uni(tid >> 6);    // this wave's kv head
+    const uint32_t group = n_head / n_head_kv;
+    const uint32_t P = gridDim.x;
+    const uint32_t w = blockIdx.x;
+    const uint32_t g = lane >> 4;   // row group: tokens 4g..4g+3 of a tile
+    const uint32_t x = lane & 15;   // head of the score tile / dim slice
+
+    uint8_t* vt = smem + kv * (TILE * VROW);                      // this wave's V tile
+    uint8_t* qst = smem + NW * TILE * VROW + kv * (QSEG * G * HD * 4);  // staged q rows (f32)
+    uint32_t* cum = reinterpret_cast<uint32_t*>(smem + NW * (TILE * VROW + QSEG * G * HD * 4));
+    uint32_t* ntok = cum + batch + 1;
+
+    // ---- tile prefix over the batch (wave 0), from the live lengths
+    if (kv == 0) {
+        uint32_t run = 0;
+        for (uint32_t base = 0; base < batch; base += 64) {
+            const uint32_t j = base + lane;
+            const uint32_t n = j < batch ? lens[j] + lens_add : 0u;
+            uint32_t t = n / TILE + (n % TILE != 0u);
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t y = __shfl_up(t, o, 64);
+                if (lane >= (uint32_t)o) t += y;
+            }
+            if (j < batch) { cum[j + 1] = run + t; ntok[j] = n; }
+            run += __shfl(t, 63, 64);
+        }
+        if (lane == 0) cum[0] = 0;
+    }
+    lds_barrier();
+
+    // T = q P + r: workgroups 0..r-1 take q+1 tiles, the rest q
+    const uint32_t T = cum[batch];
+    const tile_split ts = make_split(T, P);
+    const uint32_t F0 = ts.first(w);
+    const uint32_t F1 = ts.first(w + 1);
+    if (F0 >= F1) return;  // uniform: no tiles for this workgroup
+    const uint32_t n_items = F1 - F0;
+
+    const uint32_t row_bytes = n_head_kv * HD * 2;
+    const uint32_t slot_bytes = 2u * row_bytes;
+    const uint64_t page_bytes = (uint64_t)block_tokens * slot_bytes;
+    const uint32_t kv_off = kv * HD * 2;
+    const uint32_t slot_mask = block_tokens - 1u;
+
+    // first sequence with tiles past f (f < T)
+    auto seq_of = [&](uint32_t f) -> uint32_t {
+        uint32_t lo = 0, hi = batch - 1;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (cum[mid + 1] > f) hi = mid; else lo = mid + 1;
+        }
+        return lo;
+    };
+    const uint32_t b0 = uni(seq_of(F0));  // first sequence of the run
+
+    // page id of item kb + lane (invalid -> ~0): sequence found from b0 up
+    auto load_pages = [&](uint32_t kb) -> uint32_t {
+        const uint32_t k = kb + lane;
+        uint32_t phys = 0xFFFFFFFFu;
+        if (k < n_items) {
+            const uint32_t f = F0 + k;
+            uint32_t b = b0;
+            while (cum[b + 1] <= f) ++b;
+            const uint32_t page = ((f - cum[b]) * TILE) >> bt_shift;
+            if (page < bt_stride) {
+                const uint32_t p = bt[(uint64_t)b * bt_stride + page];
+                phys = (uint64_t)p < n_blocks ? p : 0xFFFFFFFFu;
+            }
+        }
+        return phys;
+    };
+    uint32_t pv = load_pages(0);
+    uint32_t pv_next = n_items > 64 ? load_pages(64) : 0u;
+
+    // ---- q of this lane's head x (dims 32s + 8g .. +7: the MFMA B operand),
+    // scaled into the log2 domain, split into hi + lo 16-bit halves; heads
+    // past the group are zero.  The q rows of the run's first QSEG
+    // sequences (this wave's heads) are fetched together up front and staged
+    // in LDS, so a sequence change inside the run does not wait on global
+    // memory; later sequences (runs over many short sequences) load directly.
+    V8 qa[KSTEPS], qb[KSTEPS];
+    const bool hv = x < group;
+    auto set_q = [&](const float4* a, const float4* c) {
+        typedef typename K::s S;
+        const float sc = hv ? scale_log2 : 0.0f;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st) {
+            const float v[8] = {a[st].x, a[st].y, a[st].z, a[st].w, c[st].x, c[st].y, c[st].z, c[st].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float vv = v[e] * sc;
+                qa[st][e] = (S)vv;
+                qb[st][e] = (S)lo_part<DT>(vv);
+            }
+        }
+    };
+    const uint32_t b_last = uni(seq_of(F1 - 1));
+    const uint32_t n_stage = b_last - b0 + 1 < (uint32_t)QSEG ? b_last - b0 + 1 : (uint32_t)QSEG;
+    {
+        // float4 i of the staged block: sequence i / (G*32), row (i / 32) % G
+        constexpr int NQ4 = QSEG * G * (HD / 4);
+        constexpr int PER = (NQ4 + 63) / 64;
+        float4 v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const uint32_t i = lane + 64 * u;
+            const uint32_t sg = i / (G * (HD / 4)), h = (i / (HD / 4)) % G, d4 = i % (HD / 4);
+            const bool ok = i < (uint32_t)NQ4 && sg < n_stage && h < group;
+            const uint32_t bb = ok ? b0 + sg : b0, hh = ok ? h : 0u;
+            v[u] = *reinterpret_cast<const float4*>(q + ((uint64_t)bb * n_head + kv * group + hh) * HD + 4 * d4);
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const uint32_t i = lane + 64 * u;
+            if (i < (uint32_t)NQ4) reinterpret_cast<float4*>(qst)[i] = v[u];
+        }
+    }
+    // q of sequence b: staged (LDS) or, past the staged ones, fetched now
+    auto load_q = [&](uint32_t b) {
+        float4 a[KSTEPS], c[KSTEPS];
+        const float* src;
+        if (b - b0 < n_stage)
+            src = reinterpret_cast<const float*>(qst) + ((b - b0) * G + (hv ? x : 0u)) * HD + 8 * g;
+        else
+            src = q + ((uint64_t)b * n_head + kv * group + (hv ? x : 0u)) * HD + 8 * g;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st) {
+            a[st] = *reinterpret_cast<const float4*>(src + 32 * st);
+            c[st] = *reinterpret_cast<const float4*>(src + 32 * st + 4);
+        }
+        set_q(a, c);
+    };
+
+    // ---- item k of the run: tile f = F0 + k of sequence seq[k]
+    // (the sequence of each item is tracked incrementally on both streams)
+    u32x4 kr[DEPTH][KSTEPS], vr[DEPTH][4];
+    uint32_t physp[DEPTH];
+    uint32_t iss_b = b0, iss_c0 = uni(cum[b0]), iss_c1 = uni(cum[b0 + 1]);
+    // Loads of item k into ring slot D.  Tokens past the sequence re-read
+    // the tile's first token (masked); with a fused append the appended
+    // token is read from new_k / new_v.
+    auto issue = [&](auto Dc, uint32_t k) {
+        constexpr int D = decltype(Dc)::value;
+        const uint32_t f = F0 + k;
+        while (f >= iss_c1) {  // uniform: next sequence
+            ++iss_b;
+            iss_c0 = iss_c1;
+            iss_c1 = uni(cum[iss_b + 1]);
+        }
+        const uint32_t tok0 = (f - iss_c0) * TILE;
+        const uint32_t phys = uni((uint32_t)__builtin_amdgcn_readlane((int)pv, (int)(k & 63u)));
+        const bool pok = phys != 0xFFFFFFFFu;
+        physp[D] = phys;
+        const uint8_t* base = pool + (uint64_t)(pok ? phys : 0u) * page_bytes +
+                              (uint64_t)(tok0 & slot_mask) * slot_bytes + kv_off;
+        const uint32_t ntk = uni(ntok[iss_b]);
+        const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
+        const bool last = new_k != nullptr && tok0 + TILE >= ntk;  // holds the appended token
+        if (nvalid == (uint32_t)TILE && !last) {
+            static_for<0, KSTEPS>([&](auto Sc) {
+                constexpr int st = decltype(Sc)::value;
+                kr[D][st] = *reinterpret_cast<const u32x4*>(base + x * slot_bytes + 64 * st + 16 * g);
+            });
+            static_for<0, 4>([&](auto Rc) {
+                constexpr int r = decltype(Rc)::value;
+                vr[D][r] = *reinterpret_cast<const u32x4*>(base + row_bytes + (4 * g + r) * slot_bytes +
+                                                           16 * x);
+            });
+        } else {
+            const uint32_t pos = ntk - 1u - tok0;  // appended token within the tile
+            const uint64_t nrow = (uint64_t)iss_b * row_bytes + kv_off;
+            {
+                const bool isnew = last && x == pos;
+                const uint8_t* src = isnew ? new_k + nrow : base + (x < nvalid ? x : 0u) * slot_bytes;
+                static_for<0, KSTEPS>([&](auto Sc) {
+                    constexpr int st = decltype(Sc)::value;
+                    kr[D][st] = *reinterpret_cast<const u32x4*>(src + 64 * st + 16 * g);
+                });
+            }
+            static_for<0, 4>([&](auto Rc) {
+                constexpr int r = decltype(Rc)::value;
+                const uint32_t t = 4 * g + r;
+                const bool isnew = last && t == pos;
+                const uint8_t* src = isnew ? new_v + nrow
+                                           : base + row_bytes + (t < nvalid ? t : 0u) * slot_bytes;
+                vr[D][r] = *reinterpret_cast<const u32x4*>(src + 16 * x);
+            });
+        }
+    };
+
+    // ---- per-lane state of head x (the four lanes of column x of the
+    // score tile share m): m_own, l_own: running max and this lane's weight
+    // sum; acc[db]: O^T rows (dims) 16 db + 4g .. +3, column (head) x.
+    float m_own = NEG_BIG, l_own = 0.0f;
+    f32x4 acc[HD / 16];
+#pragma unroll
+    for (int db = 0; db < HD / 16; ++db) acc[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Write this wave's state for sequence b: the final rows when the whole
+    // sequence lies in this workgroup, else the partial for slot w + b; reset.
+    auto flush = [&](uint32_t b) {
+        float L = l_own;
+        L += __shfl_xor(L, 16, 64);
+        L += __shfl_xor(L, 32, 64);
+        const uint32_t c0 = cum[b], c1 = cum[b + 1];
+        const bool whole = ts.owner(c0) == ts.owner(c1 - 1);
+        if (hv) {
+            const uint32_t qh = kv * group + x;
+            if (whole) {
+                const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+                float* dst = out + ((uint64_t)b * n_head + qh) * HD + 4 * g;
+#pragma unroll
+                for (int db = 0; db < HD / 16; ++db)
+                    *reinterpret_cast<f32x4*>(dst + 16 * db) = acc[db] * inv;
+            } else {
+                const uint64_t slot = (uint64_t)(w + b) * n_head + qh;
+                float* dst = part_acc + slot * HD + 4 * g;
+#pragma unroll
+                for (int db = 0; db < HD / 16; ++db) *reinterpret_cast<f32x4*>(dst + 16 * db) = acc[db];
+                if (g == 0) *reinterpret_cast<float2*>(part_ml + slot * 2) = make_float2(m_own, L);
+            }
+        }
+        m_own = NEG_BIG;
+        l_own = 0.0f;
+#pragma unroll
+        for (int db = 0; db < HD / 16; ++db) acc[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+
+    // transposed-read address of lane (g, r*4+b): token row 4g + r,
+    // dims 4b .. 4b+3 of each 16-dim block
+    const uint32_t tr_off = (4 * g + (x >> 2)) * VROW + (x & 3u) * 8;
+    uint32_t cmp_b = b0, cmp_c0 = uni(cum[b0]), cmp_c1 = uni(cum[b0 + 1]);
+
+    auto compute = [&](auto Dc, uint32_t k) {
+        constexpr int D = decltype(Dc)::value;
+        const uint32_t f = F0 + k;
+        const uint32_t tok0 = (f - cmp_c0) * TILE;
+        const uint32_t ntk = uni(ntok[cmp_b]);
+        const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
+        const uint32_t phys = physp[D];
+        if (phys == 0xFFFFFFFFu) return;  // masked page: its tokens do not count (uniform)
+
+        // V tile rows into LDS (lane (g, x): tokens 4g..4g+3, dims 8x..8x+7)
+        static_for<0, 4>([&](auto Rc) {
+            constexpr int r = decltype(Rc)::value;
+            *reinterpret_cast<u32x4*>(vt + (4 * g + r) * VROW + 16 * x) = vr[D][r];
+        });
+
+        // S = K Q^T: lane (g, x) receives tokens 4g..4g+3 of head x
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st) {
+            const V8 a = __builtin_bit_cast(V8, kr[D][st]);
+            s = K::mma(a, qa[st], s);
+            s = K::mma(a, qb[st], s);
+        }
+        if (nvalid < (uint32_t)TILE) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] = (4 * g + r < nvalid) ? s[r] : -__builtin_inff();
+        }
+        // fused append: store the appended token's K/V slice of this kv
+        // head from the registers that already hold it
+        if (new_k != nullptr && tok0 + TILE >= ntk) {
+            const uint32_t pos = ntk - 1u - tok0;
+            uint8_t* dst = pool + (uint64_t)phys * page_bytes +
+                           (uint64_t)((tok0 & slot_mask) + pos) * slot_bytes + kv_off;
+            if (x == pos) {
+#pragma unroll
+                for (int st = 0; st < KSTEPS; ++st)
+                    *reinterpret_cast<u32x4*>(dst + 64 * st + 16 * g) = kr[D][st];
+            }
+            static_for<0, 4>([&](auto Rc) {
+                constexpr int r = decltype(Rc)::value;
+                if (4 * g + r == pos) *reinterpret_cast<u32x4*>(dst + row_bytes + 16 * x) = vr[D][r];
+            });
+        }
+        // online softmax of head x; the running max moves (for all four row
+        // groups together) only when a score exceeds it by 2^8
+        const float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        if (__builtin_amdgcn_ballot_w64(mt > m_own + RESCALE)) {
+            float mg = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            mg = fmaxf(mg, __shfl_xor(mg, 32, 64));
+            const float mn = fmaxf(m_own, mg);
+            const float corr = fast_exp2(m_own - mn);
+            l_own *= corr;
+#pragma unroll
+            for (int db = 0; db < HD / 16; ++db) acc[db] *= corr;
+            m_own = mn;
+        }
+        const float p0 = fast_exp2(s[0] - m_own), p1 = fast_exp2(s[1] - m_own);
+        const float p2 = fast_exp2(s[2] - m_own), p3 = fast_exp2(s[3] - m_own);
+        l_own += (p0 + p1) + (p2 + p3);
+        // P^T operand (tokens 4g..4g+3 of head x) straight from the scores
+        const uint64_t ph = (uint64_t)pack2<DT>(p0, p1) | ((uint64_t)pack2<DT>(p2, p3) << 32);
+        uint64_t plo = 0;
+        if constexpr (DT == DT_BF16)
+            plo = (uint64_t)pack2<DT>(lo_part<DT>(p0), lo_part<DT>(p1)) |
+                  ((uint64_t)pack2<DT>(lo_part<DT>(p2), lo_part<DT>(p3)) << 32);
+        // O^T += V^T P^T per 16-dim block, V^T by transposed LDS reads
+#pragma unroll
+        for (int db = 0; db < HD / 16; ++db) {
+            const uint64_t va = lds_read_tr(vt + tr_off + 32 * db);
+            acc[db] = K::mma16(va, ph, acc[db]);
+            if constexpr (DT == DT_BF16) acc[db] = K::mma16(va, plo, acc[db]);
+        }
+    };
+
+    // ---- main loop: chunks of CHUNK tiles, each fully unrolled so that no
+    // in-flight load crosses a loop edge (the register allocator would
+    // otherwise copy the ring at the back edge, waiting for it).  Every
+    // chunk issues the same load stream -- DEPTH tiles up front, one refill
+    // per step while the chunk lasts; refills past the chunk's last tile
+    // re-read that tile (a cache hit, never computed) -- and the steps nest,
+    // so each step waits for exactly its own tile.
+    load_q(b0);
+    for (uint32_t c0 = 0; c0 < n_items; c0 += CHUNK) {
+        const uint32_t cn = n_items - c0 < (uint32_t)CHUNK ? n_items - c0 : (uint32_t)CHUNK;
+        if (c0 != 0 && (c0 & 63u) == 0u) {  // next batch of page ids
+            pv = pv_next;
+            if (c0 + 64 < n_items) pv_next = load_pages(c0 + 64);
+        }
+        const uint32_t klast = c0 + cn - 1;
+        static_for<0, DEPTH>([&](auto Dc) {
+            const uint32_t k = c0 + decltype(Dc)::value;
+            issue(Dc, k < klast ? k : klast);
+        });
+        nested_for<0, CHUNK>([&](auto Kc) -> bool {
+            constexpr int kk = decltype(Kc)::value;
+            constexpr int D = kk % DEPTH;
+            if ((uint32_t)kk >= cn) return false;  // uniform
+            const uint32_t k = c0 + kk;
+            if (F0 + k >= cmp_c1) {  // uniform: the run moves to the next sequence
+                flush(cmp_b);
+                do {
+                    ++cmp_b;
+                    cmp_c0 = cmp_c1;
+                    cmp_c1 = uni(cum[cmp_b + 1]);
+                } while (F0 + k >= cmp_c1);
+                load_q(cmp_b);
+            }
+            compute(ic<D>{}, k);
+            // the refill stays below the slot's last use, so its loads reuse
+            // the slot's registers
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kk + DEPTH < CHUNK) {
+                const uint32_t kn = k + DEPTH;
+                issue(ic<D>{}, kn < klast ? kn : klast);
+            }
+            return true;
+        });
+    }
+    flush(cmp_b);
+}
+
+// Log-sum-exp merge of the workgroup partials of every sequence that spans
+// more than one workgroup.  Grid (ceil(n_head*128/64), batch), 256 threads:
+// lane = output element, the 4 waves split the sequence's partials (each
+// wave fetches up to NB of them in one memory round trip) and combine their
+// results through LDS.  Recomputes the split kernel's tile runs from the same
+// lengths (every workgroup between a sequence's first and last holds tiles
+// of it); writes zeros for empty sequences; sequences inside one workgroup
+// were finished by the split kernel.
+extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
+    const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
+    const uint32_t* __restrict__ lens, uint32_t lens_add, uint32_t batch, uint32_t n_head,
+    uint32_t head_dim, uint32_t P) {
+    constexpr int NB = 16;
+    __shared__ float sM[4][64], sL[4][64], sA[4][64];
+    const uint32_t b = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    uint32_t tot = 0, before = 0, mine = 0;
+    for (uint32_t j = lane; j < batch; j += 64) {
+        const uint32_t n = lens[j] + lens_add;
+        const uint32_t t = n / TILE + (n % TILE != 0u);
+        tot += t;
+        before += j < b ? t : 0u;
+        mine += j == b ? t : 0u;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        tot += __shfl_xor(tot, o, 64);
+        before += __shfl_xor(before, o, 64);
+        mine += __shfl_xor(mine, o, 64);
+    }
+    const uint32_t e = blockIdx.x * 64 + lane;
+    const bool live = e < n_head * head_dim;
+    const uint64_t orow = (uint64_t)b * n_head * head_dim + e;
+    if (mine == 0) {  // uniform
+        if (wave == 0 && live) out[orow] = 0.0f;
+        return;
+    }
+    const tile_split ts = make_split(tot, P);
+    const uint32_t w0 = ts.owner(before), w1 = ts.owner(before + mine - 1);
+    if (w0 == w1) return;  // finished by the split kernel
+    const uint32_t ec = live ? e : 0u;
+    const uint32_t qh = ec / head_dim, d = ec - qh * head_dim;
+    const uint32_t ns = w1 - w0 + 1;
+    float M = NEG_BIG, Ls = 0.0f, A = 0.0f;
+    for (uint32_t s0 = wave; s0 < ns; s0 += 4 * NB) {
+        float2 v[NB];
+        float a[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t s = s0 + 4 * i < ns ? s0 + 4 * i : s0;
+            const uint64_t slot = (uint64_t)(w0 + s + b) * n_head + qh;
+            v[i] = reinterpret_cast<const float2*>(part_ml)[slot];
+            a[i] = part_acc[slot * head_dim + d];
+        }
+        float mx = M;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            if (s0 + 4 * i < ns && v[i].y > 0.0f) mx = fmaxf(mx, v[i].x);
+        const float c = fast_exp2(M - mx);  // 0 while nothing was folded in
+        Ls *= c;
+        A *= c;
+        M = mx;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (s0 + 4 * i >= ns || !(v[i].y > 0.0f)) continue;
+            const float fw = fast_exp2(v[i].x - M);
+            Ls = fmaf(v[i].y, fw, Ls);
+            A = fmaf(a[i], fw, A);
+        }
+    }
+    sM[wave][lane] = M;
+    sL[wave][lane] = Ls;
+    sA[wave][lane] = A;
+    __syncthreads();
+    if (wave != 0 || !live) return;
+    float Mx = NEG_BIG;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (sL[u][lane] > 0.0f) Mx = fmaxf(Mx, sM[u][lane]);
+    float L = 0.0f, Acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        if (!(sL[u][lane] > 0.0f)) continue;
+        const float fw = fast_exp2(sM[u][lane] - Mx);
+        L = fmaf(sL[u][lane], fw, L);
+        Acc = fmaf(sA[u][lane], fw, Acc);
+    }
+    out[orow] = L > 0.0f ? Acc / L : 0.0f;
+}
+
+// One wave per kv head; at most 8 waves per workgroup; two waves per SIMD
+// (256 VGPRs, no AGPR copies, which would wait for the loads they copy); 2
+// tiles in flight per wave (measured faster than 4: deeper queues slow the
+// random page reads).
+#define EH_TILES(DTN, DT, G)                                                                        \
+    extern "C" __global__ __launch_bounds__(512, 1) void eh_decode_tiles_##DTN##_hd128_g##G(     \
+        const float* q, uint8_t* pool, uint64_t n_blocks, const uint32_t* bt, uint32_t bt_stride,  \
+        const uint32_t* lens, uint32_t lens_add, const uint8_t* new_k, const uint8_t* new_v,       \
+        uint32_t batch, float* out, float* part_acc, float* part_ml, uint32_t n_head,              \
+        uint32_t n_head_kv, uint32_t block_tokens, uint32_t bt_shift, float scale_log2) {          \
+        decode_tiles<DT, G, 2, 16>(q, pool, n_blocks, bt, bt_stride, lens, lens_add, new_k, new_v, \
+                                   batch, out, part_acc, part_ml, n_head, n_head_kv, block_tokens, \
+                                   bt_shift, scale_log2);                                          \
+    }
+
+#define EH_TILES_ALL(DTN, DT) \
+    EH_TILES(DTN, DT, 1)      \
+    EH_TILES(DTN, DT, 2)      \
+    EH_TILES(DTN, DT, 4)      \
+    EH_TILES(DTN, DT, 6)      \
+    EH_TILES(DTN, DT, 8)
+
+#if !defined(EH_ONLY_DT) || EH_ONLY_DT == 1
+EH_TILES_ALL(f16, DT_F16)
+#endif
+#if !defined(EH_ONLY_DT) || EH_ONLY_DT == 2
+EH_TILES_ALL(bf16, DT_BF16)
+#endif

@@ -101,3 +101,28 @@ class PagedAttention:
             self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
             int(stride), buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv),
             int(head_dim), int(block_tokens), int(plan[0]), int(plan[1]), wp, wb))
+
+    def append_decode_batched(self, stream, layout, pool, keys, values, block_tables, start_pos,
+                              q, out, n_head, head_dim, plan, workspace):
+        """One decode step in one launch: row b of keys/values [B, row_len]
+        lands at logical position start_pos[b] (device u32) through
+        block_tables [B, stride], then q [B, n_head, head_dim] attends tokens
+        0..start_pos[b] (the batched append_kv of paged_kv.rs:200-327 followed
+        by launch_with_pos_ptr, paged_attention.rs:177-345).  `plan` is
+        PagedAttention.plan(...) with tokens_per_split 0 on a shape the
+        token-balanced kernel serves (plan[0] == 0)."""
+        if plan[0] != 0:
+            raise ValueError("append_decode_batched needs a token-balanced plan (tokens_per_split 0)")
+        batch, stride = block_tables.shape
+        pp, pb = buf(pool)
+        kp, kb = buf(keys)
+        vp_, vb = buf(values)
+        bp, bb = buf(block_tables)
+        qp, qb = buf(q)
+        op, ob = buf(out)
+        wp, wb = buf(workspace)
+        lay = layout.c()
+        check(self._L.eh_append_decode_batched(
+            self._ctx.handle, stream_handle(stream), C.byref(lay), pp, pb, kp, kb, vp_, vb, bp, bb,
+            int(stride), buf(start_pos)[0], int(batch), qp, qb, op, ob, int(n_head), int(head_dim),
+            int(plan[1]), wp, wb))
