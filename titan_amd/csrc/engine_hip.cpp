@@ -336,7 +336,8 @@ uint32_t device_cus() {
     return 256;  // MI355X
 }
 
-// 8 waves per CU (two per SIMD): 8 / n_kv workgroups per CU
+// one 8-wave workgroup per CU (two waves per SIMD) holding 8 / n_kv runs;
+// the plan's grid counts runs
 uint32_t tiles_grid(const tiles_cfg& t) { return device_cus() * (8u / t.nw); }
 
 uint64_t tiles_ws_bytes(uint64_t grid, uint64_t batch, uint64_t n_head) {
@@ -368,14 +369,17 @@ eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const 
     // per-wave V tiles (16 rows x kTilesVRow bytes) and staged q rows
     // (kTilesQSeg sequences x g heads x 128 f32), the tile prefix and token
     // counts of the batch
-    const uint32_t lds = t.nw * (16 * kTilesVRow + kTilesQSeg * t.g * 128 * 4) + 4u * (2 * a.batch + 1);
+    const uint32_t runs_per_wg = 8u / t.nw;
+    const uint32_t waves = 8u;
+    const uint32_t lds = waves * (16 * kTilesVRow + kTilesQSeg * t.g * 128 * 4) + 4u * (2 * a.batch + 1);
     float* part_acc = (float*)a.ws;
     float* part_ml = part_acc + (uint64_t)(a.grid + a.batch) * a.n_head * 128;
-    eh_status st = launch_lds(c, mod, name, dim3(a.grid), dim3(t.nw * 64), lds, stream, a.q,
+    eh_status st = launch_lds(c, mod, name, dim3((a.grid + runs_per_wg - 1) / runs_per_wg),
+                              dim3(waves * 64), lds, stream, a.q,
                               (uint8_t*)a.pool, a.n_blocks, a.bt, a.bt_stride, a.lens, a.lens_add,
                               (const uint8_t*)a.new_k, (const uint8_t*)a.new_v, a.batch, a.out,
                               part_acc, part_ml, a.n_head, a.n_head_kv, a.block_tokens,
-                              (uint32_t)log2_exact(a.block_tokens), scale_log2);
+                              (uint32_t)log2_exact(a.block_tokens), scale_log2, a.grid);
     if (st != EH_OK) return st;
     return launch(c, mod, "eh_decode_tiles_merge",
                   dim3((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch), dim3(256), stream,

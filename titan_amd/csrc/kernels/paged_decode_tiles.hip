@@ -15,9 +15,11 @@
 //     (sequence, tile) order, cut on the device from the live lengths, so
 //     the load is balanced whatever the context mix and a captured graph
 //     stays correct as contexts grow;
-//   * a workgroup has one wave per kv head; the waves walk the same tiles,
-//     so together they stream whole pages (all kv heads of each token slot),
-//     and each wave owns the complete softmax state of its q heads;
+//   * a run has one wave per kv head; the waves walk the same tiles, so
+//     together they stream whole pages (all kv heads of each token slot),
+//     and each wave owns the complete softmax state of its q heads; a
+//     workgroup of 8 waves holds 8 / n_kv runs (fewer, larger workgroups
+//     dispatch faster) that share one scan of the lengths;
 //   * q.k is one MFMA tile per 16 tokens: S[16 tok x 16 heads] =
 //     K[16 x 128] . Q^T with v_mfma_f32_16x16x32 (f16 or bf16), q split into
 //     hi + lo 16-bit halves (two MFMAs per step) so scores keep ~22 bits;
@@ -169,9 +171,10 @@ __device__ __forceinline__ float lo_part(float a) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// Split kernel.  Grid: P workgroups (1-D) of n_kv waves; wave kv serves kv
-// head kv on every tile of the workgroup's run.  Dynamic LDS (bytes):
-// n_kv*16*VROW (V tiles) + n_kv*QSEG*G*128*4 (staged q rows) +
+// Split kernel.  Grid: 1-D workgroups of SUB * n_kv waves holding SUB runs
+// each (n_runs in all; the surplus runs of the last workgroup are empty);
+// wave kv of a run serves kv head kv on every tile of the run.  Dynamic LDS
+// (bytes): waves*16*VROW (V tiles) + waves*QSEG*G*128*4 (staged q rows) +
 // 4*(2*batch + 1) (tile prefix, token counts).  lens[b] + lens_add = tokens
 // sequence b attends (lens_add = 1 when lens are the positions of a fused
 // append).  Partials: slot w + b for workgroup w and sequence b,
@@ -183,7 +186,7 @@ __device__ __forceinline__ void decode_tiles(
     uint32_t lens_add, const uint8_t* __restrict__ new_k, const uint8_t* __restrict__ new_v,
     uint32_t batch, float* __restrict__ out, float* __restrict__ part_acc,
     float* __restrict__ part_ml, uint32_t n_head, uint32_t n_head_kv,
-    uint32_t block_tokens, uint32_t bt_shift, float scale_log2) {
+    uint32_t block_tokens, uint32_t bt_shift, float scale_log2, uint32_t n_runs) {
     constexpr int HD = 128;
     constexpr int KSTEPS = HD / 32;  // MFMA steps over head_dim
     typedef kvt<DT> K;
@@ -192,23 +195,28 @@ __device__ __forceinline__ void decode_tiles(
 
     extern __shared__ __align__(16) uint8_t smem[];
 
-    const uint32_t NW = blockDim.x >> 6;  // == n_head_kv
+    // A workgroup holds SUB = waves / n_kv independent runs side by side
+    // (one wave per kv head each), sharing one scan of the lengths; run
+    // w = blockIdx * SUB + sub of P = gridDim * SUB.
+    const uint32_t NW = blockDim.x >> 6;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
-    const uint32_t kv = uni(tid >> 6);    // this wave's kv head
+    const uint32_t wave = uni(tid >> 6);
+    const uint32_t kv = wave % n_head_kv;  // this wave's kv head
+    const uint32_t SUB = NW / n_head_kv;
     const uint32_t group = n_head / n_head_kv;
-    const uint32_t P = gridDim.x;
-    const uint32_t w = blockIdx.x;
+    const uint32_t P = n_runs;
+    const uint32_t w = blockIdx.x * SUB + wave / n_head_kv;  // runs past n_runs have no tiles
     const uint32_t g = lane >> 4;   // row group: tokens 4g..4g+3 of a tile
     const uint32_t x = lane & 15;   // head of the score tile / dim slice
 
-    uint8_t* vt = smem + kv * (TILE * VROW);                      // this wave's V tile
-    uint8_t* qst = smem + NW * TILE * VROW + kv * (QSEG * G * HD * 4);  // staged q rows (f32)
+    uint8_t* vt = smem + wave * (TILE * VROW);                      // this wave's V tile
+    uint8_t* qst = smem + NW * TILE * VROW + wave * (QSEG * G * HD * 4);  // staged q rows (f32)
     uint32_t* cum = reinterpret_cast<uint32_t*>(smem + NW * (TILE * VROW + QSEG * G * HD * 4));
     uint32_t* ntok = cum + batch + 1;
 
     // ---- tile prefix over the batch (wave 0), from the live lengths
-    if (kv == 0) {
+    if (wave == 0) {
         uint32_t run = 0;
         for (uint32_t base = 0; base < batch; base += 64) {
             const uint32_t j = base + lane;
@@ -229,9 +237,9 @@ __device__ __forceinline__ void decode_tiles(
     // T = q P + r: workgroups 0..r-1 take q+1 tiles, the rest q
     const uint32_t T = cum[batch];
     const tile_split ts = make_split(T, P);
-    const uint32_t F0 = ts.first(w);
-    const uint32_t F1 = ts.first(w + 1);
-    if (F0 >= F1) return;  // uniform: no tiles for this workgroup
+    const uint32_t F0 = w < P ? ts.first(w) : T;
+    const uint32_t F1 = w < P ? ts.first(w + 1) : T;
+    if (F0 >= F1) return;  // uniform over the wave: no tiles for this run (no barrier follows)
     const uint32_t n_items = F1 - F0;
 
     const uint32_t row_bytes = n_head_kv * HD * 2;
@@ -650,10 +658,11 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
         const float* q, uint8_t* pool, uint64_t n_blocks, const uint32_t* bt, uint32_t bt_stride,  \
         const uint32_t* lens, uint32_t lens_add, const uint8_t* new_k, const uint8_t* new_v,       \
         uint32_t batch, float* out, float* part_acc, float* part_ml, uint32_t n_head,              \
-        uint32_t n_head_kv, uint32_t block_tokens, uint32_t bt_shift, float scale_log2) {          \
+        uint32_t n_head_kv, uint32_t block_tokens, uint32_t bt_shift, float scale_log2,            \
+        uint32_t n_runs) {                                                                         \
         decode_tiles<DT, G, 2, 16>(q, pool, n_blocks, bt, bt_stride, lens, lens_add, new_k, new_v, \
                                    batch, out, part_acc, part_ml, n_head, n_head_kv, block_tokens, \
-                                   bt_shift, scale_log2);                                          \
+                                   bt_shift, scale_log2, n_runs);                                  \
     }
 
 #define EH_TILES_ALL(DTN, DT) \
