@@ -44,6 +44,11 @@ def parse():
     p.add_argument("--roofline-iters", type=int, default=10)
     p.add_argument("--fuse", type=int, default=1,
                    help="one fused append+decode launch per layer when the balanced kernel applies")
+    p.add_argument("--suite", action="store_true",
+                   help="instead of the headline line, time the other benchmark configurations "
+                        "(1, 3, 4, 5) and append/gather, one JSON line each")
+    p.add_argument("--c5-pool-frac", type=float, default=0.9,
+                   help="config 5 pool size as a fraction of free HBM")
     return p.parse_args()
 
 
@@ -72,6 +77,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.suite:
+        suite(args, dev)
+        return
     L = args.layers
     extra = args.warmup + args.steps + 2 + args.roofline_iters
     shape = synth.config2(0, extra_tokens=extra)
@@ -223,6 +231,180 @@ def main():
     }
     print(json.dumps(line), flush=True)
 
+
+
+def graph_time_us(fn, iters=20, per_graph=20, stream=None):
+    """Capture per_graph back-to-back calls fn(stream) in one graph, replay it
+    iters times between two events on the capture stream; mean microseconds
+    per call (graph launch cost amortised over per_graph calls)."""
+    import torch
+    s = stream or torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    fn(None)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(per_graph):
+                fn(s)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        g.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        for _ in range(iters):
+            g.replay()
+        b.record(s)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / (iters * per_graph)
+
+
+def emit(d):
+    print(json.dumps(d), flush=True)
+
+
+def suite(args, dev):
+    """The benchmark configurations other than the headline (config 2), each
+    on synthetic seeded inputs resident in HBM; timings are HIP events around
+    graph replays (launch cost inside the graph, host enqueue outside)."""
+    import numpy as np
+    import torch
+
+    from titan_amd import (FlashAttention2, KvDataType, PagedAttention, PagedKvGpu,
+                           PagedKvLayout, synth)
+
+    kv, pa, fa = PagedKvGpu(0), PagedAttention(0), FlashAttention2(0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    # ---- config 1: f32, B=1, 14/2 heads, hd 64, page 16, 511 cached + 1 appended
+    s1 = synth.config1(0)
+    rl = s1.row_len
+    lay1 = PagedKvLayout(64, 16, rl, KvDataType.F32)
+    pool1 = torch.randn(lay1.floats_total(), generator=gen, device=dev)
+    tab1 = torch.from_numpy(s1.free_order[:32].astype(np.uint32).view(np.int32)).to(dev)
+    k1 = torch.randn(rl, generator=gen, device=dev)
+    v1 = torch.randn(rl, generator=gen, device=dev)
+    q1 = torch.randn(s1.n_head * s1.head_dim, generator=gen, device=dev)
+    o1 = torch.empty_like(q1)
+
+    def step1(st):
+        kv.append_kv(st, lay1, pool1, k1, v1, tab1, 511, 1)
+        pa.launch_flash_decoding(st, q1, pool1, tab1, o1, s1.n_head, s1.n_head_kv, s1.head_dim,
+                                 16, 512, 511, True)
+    us1 = graph_time_us(step1, 20)
+    emit({"config": 1, "what": "append 1 token + flash-decoding attention, f32, B=1, 14/2 heads, "
+          "hd 64, ctx 512", "latency_us": round(us1, 2),
+          "kv_bytes": 512 * rl * 2 * 4, "GB/s": round(512 * rl * 2 * 4 / us1 / 1e3, 1)})
+
+    # ---- append / gather at config 2's shape (one layer)
+    s2 = synth.config2(0, extra_tokens=1)
+    tab2 = synth.block_tables(s2, extra_tokens=1)
+    lay2 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.F16)
+    pool2 = torch.randn(lay2.floats_total(), generator=gen, device=dev, dtype=torch.float16)
+    dtab2 = torch.from_numpy(tab2.view(np.int32)).to(dev)
+    nk2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
+    nv2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
+    cu2 = torch.arange(33, dtype=torch.int32, device=dev)
+    st2 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
+    us_app = graph_time_us(lambda st: kv.append_kv_batched(st, lay2, pool2, nk2, nv2, dtab2, cu2,
+                                                           st2, 32), 20)
+    app_bytes = 32 * 2 * s2.row_len * 2 * 2
+    emit({"config": 2, "what": "batched append of one token per sequence (32 x 1 KiB rows), f16",
+          "latency_us": round(us_app, 2), "GB/s": round(app_bytes / us_app / 1e3, 2)})
+    L0 = int(s2.ctx_lens[0])
+    gout = torch.empty((L0, s2.row_len), dtype=torch.float16, device=dev)
+    tab_row = dtab2[0].contiguous()
+    us_g = graph_time_us(lambda st: kv.read_keys(st, lay2, pool2, tab_row, gout, 0, L0), 20)
+    g_bytes = L0 * s2.row_len * 2 * 2
+    emit({"config": 2, "what": f"gather of one sequence's K rows ({L0} tokens x 512 B), f16",
+          "latency_us": round(us_g, 2), "GB/s": round(g_bytes / us_g / 1e3, 1)})
+    del pool2
+
+    # ---- config 3: bf16 chunked prefill, B=8, 512 new tokens on 2048 cached, 32/8 heads
+    s3 = synth.config3(0)
+    tab3 = synth.block_tables(s3, extra_tokens=512)
+    lay3 = PagedKvLayout(s3.n_blocks, 16, s3.row_len, KvDataType.BF16)
+    pool3 = torch.randn(lay3.floats_total(), generator=gen, device=dev, dtype=torch.bfloat16)
+    dtab3 = torch.from_numpy(tab3.view(np.int32)).to(dev)
+    T3 = 8 * 512
+    k3 = torch.randn((T3, s3.row_len), generator=gen, device=dev, dtype=torch.bfloat16)
+    v3 = torch.randn((T3, s3.row_len), generator=gen, device=dev, dtype=torch.bfloat16)
+    q3 = torch.randn((T3, 32, 128), generator=gen, device=dev)
+    o3 = torch.empty_like(q3)
+    cu3 = torch.arange(0, T3 + 1, 512, dtype=torch.int32, device=dev)
+    sp3 = torch.full((8,), 2048, dtype=torch.int32, device=dev)
+    us_a3 = graph_time_us(lambda st: kv.append_kv_batched(st, lay3, pool3, k3, v3, dtab3, cu3, sp3,
+                                                          T3), 10)
+    us_p3 = graph_time_us(lambda st: fa.launch_batched(st, q3, pool3, dtab3, cu3, sp3, o3, 32, 8,
+                                                       128, 16, 512, kv_dtype=KvDataType.BF16), 5, 4)
+    flops = 8 * 32 * 4 * 128 * sum(2048 + i + 1 for i in range(512))
+    emit({"config": 3, "what": "chunked prefill (causal, MFMA), bf16 KV, B=8, 512 on 2048, 32/8 "
+          "heads, hd 128", "prefill_us": round(us_p3, 2), "flop": flops,
+          "TFLOP/s": round(flops / us_p3 / 1e6, 1),
+          "mfma_frac_of_2.5PF": round(flops / us_p3 / 1e6 / 2500.0, 4),
+          "append_us": round(us_a3, 2),
+          "append_GB/s": round(T3 * 2 * s3.row_len * 2 * 2 / us_a3 / 1e3, 1)})
+    del pool3, k3, v3, q3, o3
+
+    # ---- config 4: prefix-shared CoW + eviction + compaction (page moves on the GPU)
+    from titan_amd.prefix_share import PrefixShareScenario, run_on_gpu
+    scn = PrefixShareScenario(seed=0)
+    plan4 = scn.plan()
+    pool4, _, _, lay4 = run_on_gpu(scn, plan4)
+    src = torch.from_numpy(np.asarray(plan4.compaction.src, np.uint32).view(np.int32)).to(dev)
+    dst = torch.from_numpy(np.asarray(plan4.compaction.dst, np.uint32).view(np.int32)).to(dev)
+    npairs = int(src.numel())
+    # compaction moves each survivor once; replays re-copy the same bytes
+    us4 = graph_time_us(lambda st: kv.copy_pages(st, lay4, pool4, src, dst), 10) if npairs else 0.0
+    page = lay4.page_bytes()
+    emit({"config": 4, "what": "gather-compaction of surviving pages after prefix-shared "
+          "CoW + 25% LRU eviction (64 seqs, 8 kv heads, hd 128, f16)",
+          "pages_moved": npairs, "cow_copies": plan4.cow_pairs, "compaction_us": round(us4, 2),
+          "GB/s": round(2 * npairs * page / us4 / 1e3, 1) if us4 else None})
+    del pool4
+
+    # ---- config 5: B=4 at 32768 tokens, 32/8 heads, f16, pool ~90% of free HBM
+    torch.cuda.empty_cache()
+    free, _ = torch.cuda.mem_get_info()
+    s5 = synth.config5(0, n_blocks=int(args.c5_pool_frac * free) // (16 * 2 * 1024 * 2))
+    tab5 = synth.block_tables(s5, extra_tokens=1)
+    lay5 = PagedKvLayout(s5.n_blocks, 16, s5.row_len, KvDataType.F16)
+    pool5 = torch.empty(lay5.floats_total(), device=dev, dtype=torch.float16)
+    # fill only the pages the tables use (values do not change the timing)
+    used = torch.from_numpy(tab5[tab5 != 0xFFFFFFFF].astype(np.int64)).to(dev)
+    pg = pool5.view(s5.n_blocks, -1)
+    pg[used] = torch.randn((used.numel(), pg.shape[1]), generator=gen, device=dev,
+                           dtype=torch.float16)
+    dtab5 = torch.from_numpy(tab5.view(np.int32)).to(dev)
+    q5 = torch.randn((4, 32, 128), generator=gen, device=dev)
+    o5 = torch.empty_like(q5)
+    nk5 = torch.randn((4, s5.row_len), generator=gen, device=dev, dtype=torch.float16)
+    nv5 = torch.randn((4, s5.row_len), generator=gen, device=dev, dtype=torch.float16)
+    st5 = torch.from_numpy(s5.ctx_lens.astype(np.int32)).to(dev)
+    plan5 = PagedAttention.plan(4, 32, 8, 128, 16, 32769)
+    ws5 = PagedAttention.workspace(plan5)
+    flush = torch.empty(512 * 1024 * 1024 // 4, device=dev)   # evicts the 256 MB MALL
+    stream = torch.cuda.Stream()
+    times = []
+    with torch.cuda.stream(stream):
+        for it in range(12):
+            flush.fill_(float(it))
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            pa.append_decode_batched(stream, lay5, pool5, nk5, nv5, dtab5, st5, q5, o5, 32, 128,
+                                     plan5, ws5)
+            b.record(stream)
+            torch.cuda.synchronize()
+            if it >= 2:
+                times.append(a.elapsed_time(b) * 1e3)
+    us5 = float(np.median(times))
+    b5 = 4 * 32769 * 8 * 128 * 2 * 2
+    emit({"config": 5, "what": "fused append + decode, B=4 x 32768 ctx, 32/8 heads, hd 128, f16, "
+          f"pool {lay5.bytes_total() / 1e9:.0f} GB ({s5.n_blocks} pages, scattered), MALL "
+          "flushed before each timed call", "latency_us": round(us5, 2), "kv_bytes": b5,
+          "GB/s": round(b5 / us5 / 1e3, 1), "frac_of_8TB/s": round(b5 / us5 / 1e3 / 8000.0, 4),
+          "kernel": PagedAttention.kernel_name(32, 8, 128, 16, KvDataType.F16)})
 
 def cpu_baseline(args, shape, tab, pool0, q0, k0, v0):
     """Oracle append + sdpa_decode (single thread) on whole layer-steps of the
