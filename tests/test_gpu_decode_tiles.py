@@ -89,10 +89,12 @@ def test_tiles_ragged_matches_sdpa(dev, dtype, shape):
     check_close(out, ref)
 
 
-@pytest.mark.parametrize("grid", [1, 2, 3, 7, 64])
+@pytest.mark.parametrize("grid", [1, 2, 3, 7, 64, 101, 1023])
 def test_tiles_small_grids(dev, grid):
-    """Few workgroups: one run covers several sequences (several LDS
-    rounds) and a wave walks more tiles than one page-id batch holds."""
+    """Few runs: one run covers several sequences (several LDS rounds) and a
+    wave walks more tiles than one page-id batch holds.  Grids that are not a
+    multiple of the runs per workgroup, and more runs than tiles, leave
+    empty runs inside the last workgroups."""
     lens = np.array([3000, 1, 2000, 0, 5, 1500, 16, 31, 777], np.int64)
     shape = (12, 2, 128, 16)
     out, pool_f32, tab, q = run_decode(dev, KvDataType.F16, lens, shape, 100 + grid, grid=grid)
@@ -159,7 +161,7 @@ def test_tiles_workspace_reuse(dev):
         pa.decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev), i32(lens, dev),
                           out, n_head, n_kv, hd, bt, KvDataType.F16, plan, ws)
         torch.cuda.synchronize()
-        ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
+            ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
         check_close(out.cpu().numpy(), ref)
 
 
