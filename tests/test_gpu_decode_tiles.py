@@ -161,7 +161,7 @@ def test_tiles_workspace_reuse(dev):
         pa.decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev), i32(lens, dev),
                           out, n_head, n_kv, hd, bt, KvDataType.F16, plan, ws)
         torch.cuda.synchronize()
-            ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
+        ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
         check_close(out.cpu().numpy(), ref)
 
 
