@@ -102,6 +102,34 @@ eh_status eh_append_kv_batched(eh_context* ctx, eh_stream stream, const eh_kv_la
                                const uint32_t* cu_seqlens, const uint32_t* start_pos,
                                uint32_t batch, uint64_t total_tokens);
 
+/* ---- FP8 (E4M3) KV storage (extension: the FP8 KV format of
+ * openspec/archive/2026-08-28-fp8-kv-cache-quantization/design.md:3-6 and
+ * specs/kv-compression/spec.md:8-10, which no reference kernel implements).
+ * Codes are OCP E4M3FN (bias 7, no infinities, S.1111.111 = NaN, max 448);
+ * each kv head has one f32 scale for K and one for V (device arrays
+ * k_scale/v_scale [row_len / head_dim]): element e of a row stores
+ * quantize(x / scale[e / head_dim]) -- round to nearest, ties to even,
+ * |x| >= 448 and infinities saturate to +-448, NaN stays NaN -- and reads back
+ * as decode(code) * scale.  layout->data_type must be EH_KV_FP8; head_dim a
+ * multiple of 4.
+ *
+ * Quantising batched append (PagedKvGpu::append_kv, paged_kv.rs:200-327, for
+ * B sequences as eh_append_kv_batched): keys/values [total_tokens, row_len] f32. */
+eh_status eh_append_kv_e4m3_batched(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                                    void* pool, uint64_t pool_bytes, const float* keys,
+                                    uint64_t keys_bytes, const float* values, uint64_t values_bytes,
+                                    const uint32_t* block_tables, uint64_t bt_bytes,
+                                    uint32_t bt_stride, const uint32_t* cu_seqlens,
+                                    const uint32_t* start_pos, uint32_t batch,
+                                    uint64_t total_tokens, uint32_t head_dim,
+                                    const float* k_scale, const float* v_scale);
+/* Dequantising read (PagedKvGpu::read_keys / read_values, paged_kv.rs:331-470,
+ * of an FP8 pool): out [n_tokens, row_len] f32; `scale` is k_scale or v_scale. */
+eh_status eh_gather_kv_e4m3(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                            const void* pool, uint64_t pool_bytes, const uint32_t* block_table,
+                            uint64_t bt_bytes, float* out, uint64_t out_bytes, uint64_t start_token,
+                            uint64_t n_tokens, int is_value, uint32_t head_dim, const float* scale);
+
 /* ---- Page copies dst_ids[k] <- src_ids[k] (device arrays): copy-on-write
  * of a shared tail page (the copy_block_gpu step sketched for
  * CowBlockTable::perform_tail_cow, engine-kvcache/src/cow.rs:73-81) and
@@ -180,6 +208,20 @@ eh_status eh_paged_decode_batched(eh_context* ctx, eh_stream stream, uint32_t kv
                                   uint32_t n_head_kv, uint32_t head_dim, uint32_t block_tokens,
                                   uint32_t tokens_per_split, uint32_t max_splits, void* workspace,
                                   uint64_t workspace_bytes);
+
+/* ---- Batched decode over an E4M3 pool (extension; format and scales as
+ * eh_append_kv_e4m3_batched): eh_paged_decode_batched's semantics on the
+ * dequantised pool, decode(code) * scale.  Shapes of the token-balanced kernel
+ * only: eh_decode_plan(EH_KV_FP8, ..., hint 0) gives max_splits (the grid) and
+ * the workspace size. */
+eh_status eh_paged_decode_batched_e4m3(eh_context* ctx, eh_stream stream, const float* q,
+                                       uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                                       const uint32_t* block_tables, uint64_t bt_bytes,
+                                       uint32_t bt_stride, const uint32_t* ctx_lens, uint32_t batch,
+                                       float* out, uint64_t out_bytes, uint32_t n_head,
+                                       uint32_t n_head_kv, uint32_t head_dim, uint32_t block_tokens,
+                                       const float* k_scale, const float* v_scale,
+                                       uint32_t max_splits, void* workspace, uint64_t workspace_bytes);
 
 /* ---- Fused decode-step append + attention (extension: the batched
  * PagedKvGpu::append_kv of paged_kv.rs:200-327 -- in production the decode

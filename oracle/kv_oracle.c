@@ -15,6 +15,9 @@
  *     independent numpy float64 softmax-attention on random inputs.
  *   prefill: per-query equality with a numpy causal-attention on a dense copy.
  *   f16/bf16 conversions: every finite f16 pattern against numpy, RNE ties.
+ *   FP8 E4M3: all 256 codes against torch.float8_e4m3fn; quantisation against
+ *     a brute-force nearest-code search (ties to even mantissa) and against
+ *     torch's in-range conversion; saturation and NaN cases explicitly.
  *   CowBlockTable: cow_fork_test.rs:4-44.
  *   RadixTree: radix_cache_test.rs:4-95, plus a brute-force LRU model.
  *     Parity is pinned only under the logical clock (the reference uses
@@ -330,6 +333,47 @@ uint16_t orc_f32_to_bf16_rne(float x) {
 
 void orc_bf16_to_f32_array(const uint16_t* in, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) { uint32_t u = (uint32_t)in[i] << 16; memcpy(&out[i], &u, 4); }
+}
+
+/* FP8 E4M3 (OCP E4M3FN: bias 7, no infinities, S.1111.111 = NaN, max 448),
+ * the format named by the reference's FP8 KV design
+ * (openspec/archive/2026-08-28-fp8-kv-cache-quantization/design.md:3-6),
+ * with one f32 scale per kv head and K/V (spec.md:8-10): stored code =
+ * quantize(x / scale), value = decode(code) * scale.  No reference kernel
+ * implements it, so this is a restatement of the format itself. */
+float orc_e4m3_to_f32(uint8_t code) {
+    const int s = code >> 7, e = (code >> 3) & 15, m = code & 7;
+    if (e == 15 && m == 7) return NAN;
+    const float v = e == 0 ? ldexpf((float)m, -9) : ldexpf((float)(8 + m), e - 10);
+    return s ? -v : v;
+}
+
+/* Round to nearest, ties to even mantissa; |x/scale| >= 448 (and inf)
+ * saturates to +-448; NaN -> S.1111.111. */
+uint8_t orc_f32_to_e4m3(float x, float scale) {
+    const float y = x / scale;
+    uint32_t u; memcpy(&u, &y, 4);
+    const uint8_t s = (uint8_t)((u >> 24) & 0x80u);
+    if (isnan(y)) return (uint8_t)(s | 0x7Fu);
+    const float a = fabsf(y);
+    if (a >= 448.0f) return (uint8_t)(s | 0x7Eu);
+    if (a < 0.015625f) return (uint8_t)(s | (uint8_t)rintf(a * 512.0f)); /* 2^-9 grid; 8 = 2^-6 */
+    int e;
+    frexpf(a, &e);
+    e -= 1;                                          /* a in [2^e, 2^(e+1)), e in -6..8 */
+    float m = rintf(ldexpf(a, -e) * 8.0f) - 8.0f;   /* 0..8 */
+    if (m == 8.0f) { e += 1; m = 0.0f; }
+    int code = ((e + 7) << 3) | (int)m;
+    if (code > 0x7E) code = 0x7E;
+    return (uint8_t)(s | code);
+}
+
+void orc_e4m3_to_f32_array(const uint8_t* in, float* out, size_t n, float scale) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_e4m3_to_f32(in[i]) * scale;
+}
+
+void orc_f32_to_e4m3_array(const float* in, uint8_t* out, size_t n, float scale) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f32_to_e4m3(in[i], scale);
 }
 
 /* ======================= generators ======================= */

@@ -160,6 +160,13 @@ void orc_stream_prune_blocks(const orc_stream* m, const uint32_t* table, size_t 
                              uint32_t* retained, size_t* n_retained, uint32_t* evicted,
                              size_t* n_evicted);
 
+/* FP8 E4M3 (OCP E4M3FN) KV storage with per-head f32 scales: the format of
+ * openspec/archive/2026-08-28-fp8-kv-cache-quantization/design.md:3-6. */
+float orc_e4m3_to_f32(uint8_t code);
+uint8_t orc_f32_to_e4m3(float x, float scale);
+void orc_e4m3_to_f32_array(const uint8_t* in, float* out, size_t n, float scale);
+void orc_f32_to_e4m3_array(const float* in, uint8_t* out, size_t n, float scale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,10 @@ def lib():
             "orc_f32_to_f16_rne": (C.c_uint16, [f32]),
             "orc_f32_to_bf16_rne": (C.c_uint16, [f32]),
             "orc_bf16_to_f32_array": (None, [vp, vp, sz]),
+            "orc_e4m3_to_f32": (f32, [C.c_uint8]),
+            "orc_f32_to_e4m3": (C.c_uint8, [f32, f32]),
+            "orc_e4m3_to_f32_array": (None, [vp, vp, sz, f32]),
+            "orc_f32_to_e4m3_array": (None, [vp, vp, sz, f32]),
             "orc_xorshift_a_f32": (None, [u32, vp, sz]),
             "orc_generate_rows_b": (None, [u32, sz, sz, vp, vp]),
             "orc_fill_pool_paged": (None, [vp, vp, sz, sz, sz, u32, sz]),
@@ -247,6 +251,22 @@ def f32_to_f16_bits(x):
 def f32_to_bf16_bits(x):
     x = np.ascontiguousarray(x, dtype=np.float32).ravel()
     return np.array([lib().orc_f32_to_bf16_rne(float(v)) for v in x], dtype=np.uint16)
+
+
+def e4m3_to_f32(codes, scale=1.0):
+    """decode(code) * scale (f32) for FP8 E4M3 codes."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.zeros(c.shape, dtype=np.float32)
+    lib().orc_e4m3_to_f32_array(_p(c), _p(out), c.size, float(scale))
+    return out
+
+
+def f32_to_e4m3(x, scale=1.0):
+    """E4M3 codes of x / scale (RNE, saturating at 448)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.shape, dtype=np.uint8)
+    lib().orc_f32_to_e4m3_array(_p(x), _p(out), x.size, float(scale))
+    return out
 
 
 def xorshift_a(seed, n):

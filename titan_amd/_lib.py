@@ -39,6 +39,10 @@ _SIGS = {
     "eh_gather_kv": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, u64, u64, i32]),
     "eh_append_kv_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp, u64, u32,
                                    vp, vp, u32, u64]),
+    "eh_append_kv_e4m3_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp,
+                                        u64, u32, vp, vp, u32, u64, u32, vp, vp]),
+    "eh_gather_kv_e4m3": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, u64, u64, i32,
+                                u32, vp]),
     "eh_copy_pages": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, vp, u32]),
     "eh_remap_block_tables": (i32, [vp, vp, vp, u64, vp, u32]),
     "eh_page_refcounts": (i32, [vp, vp, vp, u32, vp, u32, vp, u32]),
@@ -50,6 +54,8 @@ _SIGS = {
     "eh_decode_kernel_name": (i32, [u32, u32, u32, u32, u32, C.c_char_p, u64]),
     "eh_paged_decode_batched": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, u32, vp, u64,
                                       u32, u32, u32, u32, u32, u32, vp, u64]),
+    "eh_paged_decode_batched_e4m3": (i32, [vp, vp, vp, u64, vp, u64, vp, u64, u32, vp, u32, vp, u64,
+                                           u32, u32, u32, u32, vp, vp, u32, vp, u64]),
     "eh_append_decode_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp, u64,
                                        u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp, u64]),
     "eh_flash_attention_prefill": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64,

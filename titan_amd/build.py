@@ -4,7 +4,7 @@ Outputs (git-ignored, shipped in-tree to the GPU box):
   titan_amd/lib/paged_kv.hsaco      append / gather / page copy / table kernels
   titan_amd/lib/paged_decode_{f32,f16,bf16}.hsaco  split-K decode attention
   titan_amd/lib/paged_prefill.hsaco  MFMA causal chunked prefill
-  titan_amd/lib/paged_decode_tiles_{f16,bf16}.hsaco  token-balanced decode
+  titan_amd/lib/paged_decode_tiles_{f16,bf16,fp8}.hsaco  token-balanced decode
       (MFMA q.k, optional fused append)
   titan_amd/lib/libengine_hip.so    hipModuleLoad / hipModuleLaunchKernel C-ABI
 """
@@ -29,6 +29,7 @@ KERNELS = [
     ("paged_prefill", "paged_prefill", []),
     ("paged_decode_tiles_f16", "paged_decode_tiles", ["-DEH_ONLY_DT=1"]),
     ("paged_decode_tiles_bf16", "paged_decode_tiles", ["-DEH_ONLY_DT=2"]),
+    ("paged_decode_tiles_fp8", "paged_decode_tiles", ["-DEH_ONLY_DT=3"]),
 ]
 
 # Packed-FP32 instructions are disabled for all device code on this pool.

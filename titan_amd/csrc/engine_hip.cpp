@@ -24,7 +24,7 @@ struct eh_context {
     hipModule_t mod_kv = nullptr;
     hipModule_t mod_decode[3] = {nullptr, nullptr, nullptr};  // f32, f16, bf16
     hipModule_t mod_prefill = nullptr;
-    hipModule_t mod_tiles[2] = {nullptr, nullptr};  // token-balanced decode: f16, bf16
+    hipModule_t mod_tiles[3] = {nullptr, nullptr, nullptr};  // token-balanced decode: f16, bf16, e4m3
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
     // Split-K scratch for eh_flash_decoding, allocated once at creation
@@ -314,7 +314,7 @@ struct tiles_cfg {
 tiles_cfg pick_tiles(uint32_t kv_dtype, uint64_t head_dim, uint64_t n_head, uint64_t n_head_kv,
                      uint64_t block_tokens, uint64_t batch) {
     tiles_cfg t;
-    if (kv_dtype != EH_KV_F16 && kv_dtype != EH_KV_BF16) return t;
+    if (kv_dtype != EH_KV_F16 && kv_dtype != EH_KV_BF16 && kv_dtype != EH_KV_FP8) return t;
     if (head_dim != 128 || n_head_kv == 0 || n_head % n_head_kv) return t;
     if (!(n_head_kv == 1 || n_head_kv == 2 || n_head_kv == 4 || n_head_kv == 8)) return t;
     const uint64_t group = n_head / n_head_kv;
@@ -359,12 +359,15 @@ struct tiles_args {
     float* out;
     uint32_t n_head, n_head_kv, block_tokens, grid;
     void* ws;
+    const float* k_scale;  // E4M3 pages only
+    const float* v_scale;
 };
 
 eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const tiles_cfg& t) {
     char name[64];
-    std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u", dt_name(a.kv_dtype), t.g);
-    const hipModule_t mod = c->mod_tiles[a.kv_dtype == EH_KV_F16 ? 0 : 1];
+    const bool f8 = a.kv_dtype == EH_KV_FP8;
+    std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u", f8 ? "fp8" : dt_name(a.kv_dtype), t.g);
+    const hipModule_t mod = c->mod_tiles[f8 ? 2 : a.kv_dtype == EH_KV_F16 ? 0 : 1];
     const float scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;  // paged_attention.rs:286
     // per-wave V tiles (16 rows x kTilesVRow bytes) and staged q rows
     // (kTilesQSeg sequences x g heads x 128 f32), the tile prefix and token
@@ -379,7 +382,8 @@ eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const 
                               (uint8_t*)a.pool, a.n_blocks, a.bt, a.bt_stride, a.lens, a.lens_add,
                               (const uint8_t*)a.new_k, (const uint8_t*)a.new_v, a.batch, a.out,
                               part_acc, part_ml, a.n_head, a.n_head_kv, a.block_tokens,
-                              (uint32_t)log2_exact(a.block_tokens), scale_log2, a.grid);
+                              (uint32_t)log2_exact(a.block_tokens), scale_log2, a.grid, a.k_scale,
+                              a.v_scale);
     if (st != EH_OK) return st;
     return launch(c, mod, "eh_decode_tiles_merge",
                   dim3((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch), dim3(256), stream,
@@ -548,8 +552,9 @@ eh_status eh_create(int device, const char* code_object_dir, eh_context** out) {
         eh_destroy(c);
         return fail(EH_KERNEL_LOAD, "hipModuleLoad(paged_prefill)", 0, 0, (int)e);
     }
-    const char* tile_names[2] = {"/paged_decode_tiles_f16.hsaco", "/paged_decode_tiles_bf16.hsaco"};
-    for (int i = 0; i < 2; ++i) {
+    const char* tile_names[3] = {"/paged_decode_tiles_f16.hsaco", "/paged_decode_tiles_bf16.hsaco",
+                                 "/paged_decode_tiles_fp8.hsaco"};
+    for (int i = 0; i < 3; ++i) {
         const std::string path = dir + tile_names[i];
         e = hipModuleLoad(&c->mod_tiles[i], path.c_str());
         if (e != hipSuccess) {
@@ -684,6 +689,78 @@ eh_status eh_append_kv_batched(eh_context* c, eh_stream stream, const eh_kv_layo
                   (uint64_t)l->n_blocks);
 }
 
+// ---- FP8 (E4M3) storage: quantising append and dequantising gather
+// (paged_kv.hip).  Elements move four at a time (f32x4 <-> one u32 of codes).
+static eh_status check_e4m3(const eh_kv_layout* l, uint64_t head_dim, const float* s0,
+                            const float* s1) {
+    if (l->data_type != EH_KV_FP8) return fail(EH_UNSUPPORTED, "data_type must be EH_KV_FP8");
+    if (head_dim == 0 || head_dim % 4 || l->row_len % head_dim)
+        return invalid_size(head_dim, l->row_len, "head_dim (multiple of 4 dividing row_len)");
+    if (!s0 || !s1) return fail(EH_INVALID_ARGS, "scale arrays are null");
+    return EH_OK;
+}
+
+eh_status eh_append_kv_e4m3_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                                    void* pool, uint64_t pool_bytes, const float* keys,
+                                    uint64_t keys_bytes, const float* values, uint64_t values_bytes,
+                                    const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                                    const uint32_t* cu_seqlens, const uint32_t* start_pos,
+                                    uint32_t batch, uint64_t total_tokens, uint32_t head_dim,
+                                    const float* k_scale, const float* v_scale) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    eh_status st = check_e4m3(l, head_dim, k_scale, v_scale);
+    if (st) return st;
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    const uint64_t kv_expected = total_tokens * l->row_len * 4;
+    if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
+    if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
+    if (total_tokens == 0 || batch == 0) return EH_OK;
+    if (!cu_seqlens || !start_pos) return fail(EH_INVALID_ARGS, "cu_seqlens/start_pos are null");
+    if (bt_stride == 0) return invalid_size(1, 0, "bt_stride");
+    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
+    if (((uintptr_t)keys | (uintptr_t)values) % 16 || (uintptr_t)pool % 4)
+        return fail(EH_UNSUPPORTED, "alignment (keys/values 16 B, pool 4 B)");
+    const uint64_t total = total_tokens * 2 * (l->row_len / 4);
+    if (total >= (1ull << 31)) return invalid_size((1ull << 31) - 1, total, "append too large");
+    st = bind(c);
+    if (st) return st;
+    return launch(c, c->mod_kv, "eh_append_kv_e4m3", dim3(grid_for(total, 256)), dim3(256), stream,
+                  keys, values, bt, bt_stride, (uint8_t*)pool, (uint32_t)total_tokens, (uint32_t)0,
+                  (const uint32_t*)nullptr, cu_seqlens, start_pos, batch, (uint32_t)l->row_len,
+                  head_dim, (uint32_t)l->block_tokens, (uint64_t)l->n_blocks, k_scale, v_scale);
+}
+
+eh_status eh_gather_kv_e4m3(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                            const void* pool, uint64_t pool_bytes, const uint32_t* bt,
+                            uint64_t bt_bytes, float* out, uint64_t out_bytes, uint64_t start_token,
+                            uint64_t n_tokens, int is_value, uint32_t head_dim, const float* scale) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    eh_status st = check_e4m3(l, head_dim, scale, scale);
+    if (st) return st;
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    const uint64_t out_expected = n_tokens * l->row_len * 4;
+    if (out_bytes < out_expected) return invalid_size(out_expected, out_bytes);
+    if (bt_bytes == 0) return invalid_size(4, 0);
+    if (n_tokens == 0) return EH_OK;
+    const uint64_t need = div_ceil(start_token + n_tokens, l->block_tokens) * 4;
+    if (bt_bytes < need) return invalid_size(need, bt_bytes, "block_table");
+    if ((uintptr_t)out % 16 || (uintptr_t)pool % 4)
+        return fail(EH_UNSUPPORTED, "alignment (out 16 B, pool 4 B)");
+    const uint64_t total = n_tokens * (l->row_len / 4);
+    if (total >= (1ull << 31) || start_token + n_tokens >= (1ull << 32))
+        return invalid_size((1ull << 31) - 1, total, "gather too large");
+    st = bind(c);
+    if (st) return st;
+    return launch(c, c->mod_kv, "eh_gather_kv_e4m3", dim3(grid_for(total, 256)), dim3(256), stream,
+                  (const uint8_t*)pool, bt, (uint32_t)std::min<uint64_t>(bt_bytes / 4, 0xFFFFFFFFull),
+                  out, (uint32_t)n_tokens, (uint32_t)start_token, (uint32_t)(is_value != 0),
+                  (uint32_t)l->row_len, head_dim, (uint32_t)l->block_tokens, (uint64_t)l->n_blocks,
+                  scale);
+}
+
 eh_status eh_copy_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l, void* pool,
                         uint64_t pool_bytes, const uint32_t* src_ids, const uint32_t* dst_ids,
                         uint32_t n_pairs) {
@@ -815,8 +892,10 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
                          uint64_t* workspace_bytes) {
     if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return fail(EH_INVALID_ARGS, "heads");
     if (block_tokens < 1) return fail(EH_INVALID_ARGS, "block_tokens");
-    if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
     const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, batch);
+    if (kv_dtype == EH_KV_FP8 && !(hint == 0 && tc.ok))
+        return fail(EH_UNSUPPORTED, "E4M3 pages: token-balanced shapes with hint 0 only");
+    if (kv_dtype != EH_KV_FP8 && !dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
     if (hint == 0 && tc.ok) {  // token-balanced kernel: tokens_per_split 0, max_splits = grid
         const uint32_t grid = tiles_grid(tc);
         if (tokens_per_split) *tokens_per_split = 0;
@@ -842,11 +921,12 @@ eh_status eh_decode_kernel_name(uint32_t kv_dtype, uint32_t n_head, uint32_t n_h
                                 uint32_t head_dim, uint32_t block_tokens, char* buf, uint64_t size) {
     if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return fail(EH_INVALID_ARGS, "heads");
     if (block_tokens < 1) return fail(EH_INVALID_ARGS, "block_tokens");
-    const char* dn = dt_name(kv_dtype);
+    const char* dn = kv_dtype == EH_KV_FP8 ? "fp8" : dt_name(kv_dtype);
     if (!dn) return fail(EH_UNSUPPORTED, "kv_dtype");
     const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
     const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, 1);
     char name[64];
+    if (kv_dtype == EH_KV_FP8 && !tc.ok) return fail(EH_UNSUPPORTED, "E4M3 shape");
     if (tc.ok)
         std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u", dn, tc.g);
     else if (dk.slots)
@@ -874,6 +954,7 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     if (batch == 0) return EH_OK;
     if (!ctx_lens) return fail(EH_INVALID_ARGS, "ctx_lens is null");
     if (max_splits < 1) return invalid_size(1, max_splits, "max_splits");
+    if (kv_dtype == EH_KV_FP8) return fail(EH_UNSUPPORTED, "E4M3 pages: eh_paged_decode_batched_e4m3");
     if (tps == 0) {  // token-balanced kernel, max_splits workgroups
         const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
         if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
@@ -943,6 +1024,57 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     return run_decode(c, stream, a);
 }
 
+eh_status eh_paged_decode_batched_e4m3(eh_context* c, eh_stream stream, const float* q,
+                                       uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                                       const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                                       const uint32_t* ctx_lens, uint32_t batch, float* out,
+                                       uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                                       uint32_t head_dim, uint32_t block_tokens,
+                                       const float* k_scale, const float* v_scale,
+                                       uint32_t max_splits, void* ws, uint64_t ws_bytes) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (n_head < 1) return invalid_size(1, n_head);
+    if (n_head_kv < 1) return invalid_size(1, n_head_kv);
+    if (n_head % n_head_kv != 0) return invalid_size(n_head_kv, n_head % n_head_kv);
+    if (block_tokens < 1) return invalid_size(1, block_tokens);
+    if (batch == 0) return EH_OK;
+    if (!ctx_lens) return fail(EH_INVALID_ARGS, "ctx_lens is null");
+    if (!k_scale || !v_scale) return fail(EH_INVALID_ARGS, "scale arrays are null");
+    if (max_splits < 1) return invalid_size(1, max_splits, "max_splits");
+    const tiles_cfg tc = pick_tiles(EH_KV_FP8, head_dim, n_head, n_head_kv, block_tokens, batch);
+    if (!tc.ok) return fail(EH_UNSUPPORTED, "E4M3 decode: shape outside the balanced kernel");
+    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+    if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim;
+    if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
+    const uint64_t ws_need = tiles_ws_bytes(max_splits, batch, n_head);
+    if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
+    eh_status st = bind(c);
+    if (st) return st;
+    tiles_args a{};
+    a.kv_dtype = EH_KV_FP8;
+    a.q = q;
+    a.pool = const_cast<void*>(pool);
+    a.n_blocks = pool_bytes / page_bytes;
+    a.bt = bt;
+    a.bt_stride = bt_stride;
+    a.lens = ctx_lens;
+    a.lens_add = 0;
+    a.batch = batch;
+    a.out = out;
+    a.n_head = n_head;
+    a.n_head_kv = n_head_kv;
+    a.block_tokens = block_tokens;
+    a.grid = max_splits;
+    a.ws = ws;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
+    return run_tiles(c, stream, a, tc);
+}
+
 eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l,
                                   void* pool, uint64_t pool_bytes, const void* keys,
                                   uint64_t keys_bytes, const void* values, uint64_t values_bytes,
@@ -969,7 +1101,8 @@ eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
     const tiles_cfg tc = pick_tiles(l->data_type, head_dim, n_head, n_head_kv, l->block_tokens, batch);
-    if (!tc.ok) return fail(EH_UNSUPPORTED, "fused append+decode: shape outside the balanced kernel");
+    if (!tc.ok || l->data_type == EH_KV_FP8)
+        return fail(EH_UNSUPPORTED, "fused append+decode: shape outside the balanced kernel");
     if (grid < 1) return invalid_size(1, grid, "grid");
     const uint64_t ws_need = tiles_ws_bytes(grid, batch, n_head);
     if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");

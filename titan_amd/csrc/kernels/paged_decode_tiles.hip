@@ -37,6 +37,10 @@
 //   * a wave writes its state when its run leaves a sequence: the final
 //     rows when the whole sequence lies in the workgroup, else one partial
 //     (m, l, acc) that eh_decode_tiles_merge combines.
+// E4M3 pages (OCP E4M3FN codes with one f32 scale per kv head for K and for
+// V) are converted to f16 in registers -- exact, every E4M3 value is an f16 --
+// and take the f16 path: the K scale is folded into q, the V scale into the
+// written rows and partials.
 // Pages must be a power of two of at least 16 tokens; head_dim 128;
 // at most 8 q heads per kv head; block-table entries past the table or the
 // pool mask their tokens.
@@ -46,7 +50,7 @@
 
 namespace {
 
-enum { DT_F16 = 1, DT_BF16 = 2 };
+enum { DT_F16 = 1, DT_BF16 = 2, DT_FP8 = 3 };
 
 constexpr int TILE = 16;         // tokens per tile (MFMA rows)
 constexpr int QSEG = 2;          // sequences per run whose q is staged in LDS up front
@@ -168,6 +172,19 @@ __device__ __forceinline__ float lo_part(float a) {
     return a - (float)(S)a;
 }
 
+// Four E4M3 codes (one dword, lowest byte first) as four f16 (a dword pair,
+// low dword first); exact: every E4M3 value is an f16.
+__device__ __forceinline__ uint64_t e4m3x4_to_f16(uint32_t w) {
+    const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+    const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+// Eight E4M3 codes (two dwords) as one 16-byte f16 operand.
+__device__ __forceinline__ u32x4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
+    const uint64_t a = e4m3x4_to_f16(w0), b = e4m3x4_to_f16(w1);
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -186,10 +203,17 @@ __device__ __forceinline__ void decode_tiles(
     uint32_t lens_add, const uint8_t* __restrict__ new_k, const uint8_t* __restrict__ new_v,
     uint32_t batch, float* __restrict__ out, float* __restrict__ part_acc,
     float* __restrict__ part_ml, uint32_t n_head, uint32_t n_head_kv,
-    uint32_t block_tokens, uint32_t bt_shift, float scale_log2, uint32_t n_runs) {
+    uint32_t block_tokens, uint32_t bt_shift, float scale_log2, uint32_t n_runs,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
     constexpr int HD = 128;
     constexpr int KSTEPS = HD / 32;  // MFMA steps over head_dim
-    typedef kvt<DT> K;
+    // E4M3 pages are converted to f16 in registers (exact) and use the f16 path
+    constexpr bool F8 = DT == DT_FP8;
+    constexpr int CT = F8 ? DT_F16 : DT;  // MFMA operand type
+    constexpr uint32_t ELT = F8 ? 1u : 2u;
+    constexpr int KREG = F8 ? 2 : KSTEPS;  // 16-byte K loads per lane and tile
+    constexpr int VREG = F8 ? 2 : 4;       // 16-byte V loads per lane and tile
+    typedef kvt<CT> K;
     typedef typename K::v8 V8;
     static_assert(G <= 16, "one 16-column score tile per kv head");
 
@@ -242,10 +266,10 @@ __device__ __forceinline__ void decode_tiles(
     if (F0 >= F1) return;  // uniform over the wave: no tiles for this run (no barrier follows)
     const uint32_t n_items = F1 - F0;
 
-    const uint32_t row_bytes = n_head_kv * HD * 2;
+    const uint32_t row_bytes = n_head_kv * HD * ELT;
     const uint32_t slot_bytes = 2u * row_bytes;
     const uint64_t page_bytes = (uint64_t)block_tokens * slot_bytes;
-    const uint32_t kv_off = kv * HD * 2;
+    const uint32_t kv_off = kv * HD * ELT;
     const uint32_t slot_mask = block_tokens - 1u;
 
     // first sequence with tiles past f (f < T)
@@ -288,7 +312,7 @@ __device__ __forceinline__ void decode_tiles(
     const bool hv = x < group;
     auto set_q = [&](const float4* a, const float4* c) {
         typedef typename K::s S;
-        const float sc = hv ? scale_log2 : 0.0f;
+        const float sc = hv ? scale_log2 * (F8 ? k_scale[kv] : 1.0f) : 0.0f;
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st) {
             const float v[8] = {a[st].x, a[st].y, a[st].z, a[st].w, c[st].x, c[st].y, c[st].z, c[st].w};
@@ -296,7 +320,7 @@ __device__ __forceinline__ void decode_tiles(
             for (int e = 0; e < 8; ++e) {
                 const float vv = v[e] * sc;
                 qa[st][e] = (S)vv;
-                qb[st][e] = (S)lo_part<DT>(vv);
+                qb[st][e] = (S)lo_part<CT>(vv);
             }
         }
     };
@@ -321,25 +345,29 @@ __device__ __forceinline__ void decode_tiles(
             if (i < (uint32_t)NQ4) reinterpret_cast<float4*>(qst)[i] = v[u];
         }
     }
-    // q of sequence b: staged (LDS) or, past the staged ones, fetched now
+    // q of sequence b: staged (LDS) or, past the staged ones, fetched now.
+    // Contraction index of MFMA step st, lane (g, x): dims 32 st + 8 g + e for
+    // 16-bit pages; E4M3 lanes hold 32 contiguous dims (32 g ..) of their
+    // token, so step st takes dims 32 g + 8 st + e.
+    const uint32_t qg = F8 ? 32u * g : 8u * g, qs = F8 ? 8u : 32u;
     auto load_q = [&](uint32_t b) {
         float4 a[KSTEPS], c[KSTEPS];
         const float* src;
         if (b - b0 < n_stage)
-            src = reinterpret_cast<const float*>(qst) + ((b - b0) * G + (hv ? x : 0u)) * HD + 8 * g;
+            src = reinterpret_cast<const float*>(qst) + ((b - b0) * G + (hv ? x : 0u)) * HD + qg;
         else
-            src = q + ((uint64_t)b * n_head + kv * group + (hv ? x : 0u)) * HD + 8 * g;
+            src = q + ((uint64_t)b * n_head + kv * group + (hv ? x : 0u)) * HD + qg;
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st) {
-            a[st] = *reinterpret_cast<const float4*>(src + 32 * st);
-            c[st] = *reinterpret_cast<const float4*>(src + 32 * st + 4);
+            a[st] = *reinterpret_cast<const float4*>(src + qs * st);
+            c[st] = *reinterpret_cast<const float4*>(src + qs * st + 4);
         }
         set_q(a, c);
     };
 
     // ---- item k of the run: tile f = F0 + k of sequence seq[k]
     // (the sequence of each item is tracked incrementally on both streams)
-    u32x4 kr[DEPTH][KSTEPS], vr[DEPTH][4];
+    u32x4 kr[DEPTH][KREG], vr[DEPTH][VREG];
     uint32_t physp[DEPTH];
     uint32_t iss_b = b0, iss_c0 = uni(cum[b0]), iss_c1 = uni(cum[b0 + 1]);
     // Loads of item k into ring slot D.  Tokens past the sequence re-read
@@ -362,15 +390,23 @@ __device__ __forceinline__ void decode_tiles(
         const uint32_t ntk = uni(ntok[iss_b]);
         const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
         const bool last = new_k != nullptr && tok0 + TILE >= ntk;  // holds the appended token
+        // K: token x of the tile; 16-bit: dims 32 st + 8 g .. (16 B per step),
+        // E4M3: dims 32 g .. 32 g + 31 (two 16 B loads).  V (row layout):
+        // 16-bit: tokens 4 g + r, dims 8 x ..; E4M3: tokens l / 8 + 8 j, dims
+        // 16 (l % 8) ..
+        auto k_at = [&](const uint8_t* row, int j) -> const u32x4* {
+            return reinterpret_cast<const u32x4*>(row + (F8 ? 32 * g + 16 * j : 64 * j + 16 * g));
+        };
+        auto v_tok = [&](int j) -> uint32_t { return F8 ? (lane >> 3) + 8 * j : 4 * g + j; };
+        const uint32_t v_off = F8 ? 16 * (lane & 7u) : 16 * x;
         if (nvalid == (uint32_t)TILE && !last) {
-            static_for<0, KSTEPS>([&](auto Sc) {
-                constexpr int st = decltype(Sc)::value;
-                kr[D][st] = *reinterpret_cast<const u32x4*>(base + x * slot_bytes + 64 * st + 16 * g);
+            static_for<0, KREG>([&](auto Sc) {
+                constexpr int j = decltype(Sc)::value;
+                kr[D][j] = *k_at(base + x * slot_bytes, j);
             });
-            static_for<0, 4>([&](auto Rc) {
-                constexpr int r = decltype(Rc)::value;
-                vr[D][r] = *reinterpret_cast<const u32x4*>(base + row_bytes + (4 * g + r) * slot_bytes +
-                                                           16 * x);
+            static_for<0, VREG>([&](auto Rc) {
+                constexpr int j = decltype(Rc)::value;
+                vr[D][j] = *reinterpret_cast<const u32x4*>(base + row_bytes + v_tok(j) * slot_bytes + v_off);
             });
         } else {
             const uint32_t pos = ntk - 1u - tok0;  // appended token within the tile
@@ -378,18 +414,18 @@ __device__ __forceinline__ void decode_tiles(
             {
                 const bool isnew = last && x == pos;
                 const uint8_t* src = isnew ? new_k + nrow : base + (x < nvalid ? x : 0u) * slot_bytes;
-                static_for<0, KSTEPS>([&](auto Sc) {
-                    constexpr int st = decltype(Sc)::value;
-                    kr[D][st] = *reinterpret_cast<const u32x4*>(src + 64 * st + 16 * g);
+                static_for<0, KREG>([&](auto Sc) {
+                    constexpr int j = decltype(Sc)::value;
+                    kr[D][j] = *k_at(src, j);
                 });
             }
-            static_for<0, 4>([&](auto Rc) {
-                constexpr int r = decltype(Rc)::value;
-                const uint32_t t = 4 * g + r;
+            static_for<0, VREG>([&](auto Rc) {
+                constexpr int j = decltype(Rc)::value;
+                const uint32_t t = v_tok(j);
                 const bool isnew = last && t == pos;
                 const uint8_t* src = isnew ? new_v + nrow
                                            : base + row_bytes + (t < nvalid ? t : 0u) * slot_bytes;
-                vr[D][r] = *reinterpret_cast<const u32x4*>(src + 16 * x);
+                vr[D][j] = *reinterpret_cast<const u32x4*>(src + v_off);
             });
         }
     };
@@ -404,6 +440,8 @@ __device__ __forceinline__ void decode_tiles(
 
     // Write this wave's state for sequence b: the final rows when the whole
     // sequence lies in this workgroup, else the partial for slot w + b; reset.
+    // E4M3 pages: the V scale of this kv head multiplies the weighted sum
+    const float vsc = F8 ? v_scale[kv] : 1.0f;
     auto flush = [&](uint32_t b) {
         float L = l_own;
         L += __shfl_xor(L, 16, 64);
@@ -413,7 +451,7 @@ __device__ __forceinline__ void decode_tiles(
         if (hv) {
             const uint32_t qh = kv * group + x;
             if (whole) {
-                const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+                const float inv = L > 0.0f ? vsc / L : 0.0f;
                 float* dst = out + ((uint64_t)b * n_head + qh) * HD + 4 * g;
 #pragma unroll
                 for (int db = 0; db < HD / 16; ++db)
@@ -422,7 +460,7 @@ __device__ __forceinline__ void decode_tiles(
                 const uint64_t slot = (uint64_t)(w + b) * n_head + qh;
                 float* dst = part_acc + slot * HD + 4 * g;
 #pragma unroll
-                for (int db = 0; db < HD / 16; ++db) *reinterpret_cast<f32x4*>(dst + 16 * db) = acc[db];
+                for (int db = 0; db < HD / 16; ++db) *reinterpret_cast<f32x4*>(dst + 16 * db) = acc[db] * vsc;
                 if (g == 0) *reinterpret_cast<float2*>(part_ml + slot * 2) = make_float2(m_own, L);
             }
         }
@@ -446,17 +484,35 @@ __device__ __forceinline__ void decode_tiles(
         const uint32_t phys = physp[D];
         if (phys == 0xFFFFFFFFu) return;  // masked page: its tokens do not count (uniform)
 
-        // V tile rows into LDS (lane (g, x): tokens 4g..4g+3, dims 8x..8x+7)
-        static_for<0, 4>([&](auto Rc) {
-            constexpr int r = decltype(Rc)::value;
-            *reinterpret_cast<u32x4*>(vt + (4 * g + r) * VROW + 16 * x) = vr[D][r];
-        });
+        // V tile rows into LDS as f16 (16-bit lane (g, x): tokens 4g..4g+3,
+        // dims 8x..8x+7; E4M3 lane l: tokens l/8 and l/8 + 8, dims 16 (l%8)..)
+        if constexpr (F8) {
+            static_for<0, VREG>([&](auto Rc) {
+                constexpr int j = decltype(Rc)::value;
+                const u32x4 h0 = e4m3x8_to_f16(vr[D][j][0], vr[D][j][1]);
+                const u32x4 h1 = e4m3x8_to_f16(vr[D][j][2], vr[D][j][3]);
+                uint8_t* row = vt + ((lane >> 3) + 8 * j) * VROW + 32 * (lane & 7u);
+                *reinterpret_cast<u32x4*>(row) = h0;
+                *reinterpret_cast<u32x4*>(row + 16) = h1;
+            });
+        } else {
+            static_for<0, 4>([&](auto Rc) {
+                constexpr int r = decltype(Rc)::value;
+                *reinterpret_cast<u32x4*>(vt + (4 * g + r) * VROW + 16 * x) = vr[D][r];
+            });
+        }
 
         // S = K Q^T: lane (g, x) receives tokens 4g..4g+3 of head x
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st) {
-            const V8 a = __builtin_bit_cast(V8, kr[D][st]);
+            V8 a;
+            if constexpr (F8) {  // codes 8 st .. 8 st + 7 of the lane's 32
+                a = __builtin_bit_cast(V8, e4m3x8_to_f16(kr[D][st >> 1][2 * (st & 1)],
+                                                         kr[D][st >> 1][2 * (st & 1) + 1]));
+            } else {
+                a = __builtin_bit_cast(V8, kr[D][st]);
+            }
             s = K::mma(a, qa[st], s);
             s = K::mma(a, qb[st], s);
         }
@@ -466,7 +522,7 @@ __device__ __forceinline__ void decode_tiles(
         }
         // fused append: store the appended token's K/V slice of this kv
         // head from the registers that already hold it
-        if (new_k != nullptr && tok0 + TILE >= ntk) {
+        if constexpr (!F8) if (new_k != nullptr && tok0 + TILE >= ntk) {
             const uint32_t pos = ntk - 1u - tok0;
             uint8_t* dst = pool + (uint64_t)phys * page_bytes +
                            (uint64_t)((tok0 & slot_mask) + pos) * slot_bytes + kv_off;
@@ -497,11 +553,11 @@ __device__ __forceinline__ void decode_tiles(
         const float p2 = fast_exp2(s[2] - m_own), p3 = fast_exp2(s[3] - m_own);
         l_own += (p0 + p1) + (p2 + p3);
         // P^T operand (tokens 4g..4g+3 of head x) straight from the scores
-        const uint64_t ph = (uint64_t)pack2<DT>(p0, p1) | ((uint64_t)pack2<DT>(p2, p3) << 32);
+        const uint64_t ph = (uint64_t)pack2<CT>(p0, p1) | ((uint64_t)pack2<CT>(p2, p3) << 32);
         uint64_t plo = 0;
-        if constexpr (DT == DT_BF16)
-            plo = (uint64_t)pack2<DT>(lo_part<DT>(p0), lo_part<DT>(p1)) |
-                  ((uint64_t)pack2<DT>(lo_part<DT>(p2), lo_part<DT>(p3)) << 32);
+        if constexpr (CT == DT_BF16)
+            plo = (uint64_t)pack2<CT>(lo_part<CT>(p0), lo_part<CT>(p1)) |
+                  ((uint64_t)pack2<CT>(lo_part<CT>(p2), lo_part<CT>(p3)) << 32);
         // O^T += V^T P^T per 16-dim block, V^T by transposed LDS reads
 #pragma unroll
         for (int db = 0; db < HD / 16; ++db) {
@@ -659,10 +715,10 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
         const uint32_t* lens, uint32_t lens_add, const uint8_t* new_k, const uint8_t* new_v,       \
         uint32_t batch, float* out, float* part_acc, float* part_ml, uint32_t n_head,              \
         uint32_t n_head_kv, uint32_t block_tokens, uint32_t bt_shift, float scale_log2,            \
-        uint32_t n_runs) {                                                                         \
+        uint32_t n_runs, const float* k_scale, const float* v_scale) {                             \
         decode_tiles<DT, G, 2, 16>(q, pool, n_blocks, bt, bt_stride, lens, lens_add, new_k, new_v, \
                                    batch, out, part_acc, part_ml, n_head, n_head_kv, block_tokens, \
-                                   bt_shift, scale_log2, n_runs);                                  \
+                                   bt_shift, scale_log2, n_runs, k_scale, v_scale);                \
     }
 
 #define EH_TILES_ALL(DTN, DT) \
@@ -677,4 +733,7 @@ EH_TILES_ALL(f16, DT_F16)
 #endif
 #if !defined(EH_ONLY_DT) || EH_ONLY_DT == 2
 EH_TILES_ALL(bf16, DT_BF16)
+#endif
+#if !defined(EH_ONLY_DT) || EH_ONLY_DT == 3
+EH_TILES_ALL(fp8, DT_FP8)
 #endif

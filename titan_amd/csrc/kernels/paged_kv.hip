@@ -131,7 +131,106 @@ __device__ __forceinline__ void copy_pages_body(uint8_t* __restrict__ pool,
     }
 }
 
+// ---- FP8 E4M3 storage (OCP E4M3FN: bias 7, S.1111.111 = NaN, max 448)
+// with one f32 scale per (kv head, K or V): code = quantize(x / scale),
+// value = decode(code) * scale.  The format is the one named by the
+// reference's FP8 KV design (openspec/archive/2026-08-28-fp8-kv-cache-
+// quantization/design.md:3-6); the reference has no kernel for it.
+
+// Round to nearest, ties to even mantissa; |x| >= 448 (and inf) saturates to
+// +-448; NaN -> S.1111.111.
+__device__ __forceinline__ uint32_t e4m3_code(float y) {
+    const uint32_t u = __float_as_uint(y);
+    const uint32_t s = (u >> 24) & 0x80u;
+    const float a = __builtin_fabsf(y);
+    if (a != a) return s | 0x7Fu;
+    if (a >= 448.0f) return s | 0x7Eu;
+    if (a < 0.015625f) return s | (uint32_t)__builtin_rintf(a * 512.0f);  // 2^-9 grid; 8 = 2^-6
+    int e = (int)((u >> 23) & 0xFFu) - 127;                               // a in [2^e, 2^(e+1))
+    const float mant = __uint_as_float((u & 0x007FFFFFu) | 0x3F800000u);   // a / 2^e in [1, 2)
+    uint32_t m = (uint32_t)__builtin_rintf(mant * 8.0f) - 8u;             // 0..8
+    if (m == 8u) { ++e; m = 0u; }
+    const uint32_t code = ((uint32_t)(e + 7) << 3) | m;
+    return s | (code < 0x7Eu ? code : 0x7Eu);
+}
+
+// Token row `tok` of a ragged batch (or single sequence): its page-row byte
+// offset in the pool, or ~0 when its block-table entry is missing.
+__device__ __forceinline__ uint64_t row_offset(
+    uint32_t tok, const uint32_t* __restrict__ bt, uint32_t bt_stride, uint32_t start,
+    const uint32_t* __restrict__ pos_ptr, const uint32_t* __restrict__ cu,
+    const uint32_t* __restrict__ start_pos, uint32_t batch, uint32_t block_tokens,
+    uint64_t n_blocks, uint64_t page_bytes, uint32_t slot_bytes) {
+    uint32_t pos;
+    const uint32_t* row_bt = bt;
+    if (cu) {
+        const uint32_t b = seq_of(cu, batch, tok);
+        pos = start_pos[b] + (tok - cu[b]);
+        row_bt = bt + (uint64_t)b * bt_stride;
+    } else {
+        pos = (pos_ptr ? *pos_ptr : start) + tok;
+    }
+    const uint32_t page = pos / block_tokens;
+    if (page >= bt_stride) return ~0ull;
+    const uint32_t phys = row_bt[page];
+    if (phys >= n_blocks) return ~0ull;
+    return (uint64_t)phys * page_bytes + (uint64_t)(pos - page * block_tokens) * slot_bytes;
+}
+
 }  // namespace
+
+// Quantising append: f32 keys/values [n_tokens, row_len] -> E4M3 page rows,
+// 4 elements (one u32 of codes) per thread; addressing as eh_append_kv_c*.
+extern "C" __global__ __launch_bounds__(256) void eh_append_kv_e4m3(
+    const float* keys, const float* values, const uint32_t* bt, uint32_t bt_stride, uint8_t* pool,
+    uint32_t n_tokens, uint32_t start, const uint32_t* pos_ptr, const uint32_t* cu,
+    const uint32_t* start_pos, uint32_t batch, uint32_t row_len, uint32_t head_dim,
+    uint32_t block_tokens, uint64_t n_blocks, const float* k_scale, const float* v_scale) {
+    const uint32_t qpr = row_len / 4;   // quads per K (or V) row
+    const uint32_t qpt = 2 * qpr;
+    const uint32_t total = n_tokens * qpt;  // host guarantees < 2^31
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * row_len;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const uint32_t tok = i / qpt;
+        const uint32_t c = i - tok * qpt;
+        const uint64_t off = row_offset(tok, bt, bt_stride, start, pos_ptr, cu, start_pos, batch,
+                                        block_tokens, n_blocks, page_bytes, 2 * row_len);
+        if (off == ~0ull) continue;
+        const bool is_v = c >= qpr;
+        const uint32_t e = 4 * (is_v ? c - qpr : c);  // element within the row
+        const float4 x = *reinterpret_cast<const float4*>((is_v ? values : keys) +
+                                                          (uint64_t)tok * row_len + e);
+        const float sc = (is_v ? v_scale : k_scale)[e / head_dim];
+        const uint32_t w = e4m3_code(x.x / sc) | (e4m3_code(x.y / sc) << 8) |
+                           (e4m3_code(x.z / sc) << 16) | (e4m3_code(x.w / sc) << 24);
+        *reinterpret_cast<uint32_t*>(pool + off + (is_v ? row_len : 0u) + e) = w;
+    }
+}
+
+// Dequantising gather of one sequence's K (is_value = 0) or V rows:
+// out [n_tokens, row_len] f32 = decode(code) * scale of the element's head;
+// rows whose block-table entry is missing are left untouched.
+extern "C" __global__ __launch_bounds__(256) void eh_gather_kv_e4m3(
+    const uint8_t* pool, const uint32_t* bt, uint32_t bt_len, float* out, uint32_t n_tokens,
+    uint32_t start, uint32_t is_value, uint32_t row_len, uint32_t head_dim, uint32_t block_tokens,
+    uint64_t n_blocks, const float* scale) {
+    const uint32_t qpr = row_len / 4;
+    const uint32_t total = n_tokens * qpr;
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * row_len;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const uint32_t tok = i / qpr;
+        const uint32_t e = 4 * (i - tok * qpr);
+        const uint64_t off = row_offset(tok, bt, bt_len, start, nullptr, nullptr, nullptr, 0,
+                                        block_tokens, n_blocks, page_bytes, 2 * row_len);
+        if (off == ~0ull) continue;
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(pool + off + (is_value ? row_len : 0u) + e);
+        const float sc = scale[e / head_dim];
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+        *reinterpret_cast<float4*>(out + (uint64_t)tok * row_len + e) =
+            make_float4(lo[0] * sc, lo[1] * sc, hi[0] * sc, hi[1] * sc);
+    }
+}
 
 #define EH_DEFINE_CHUNK(CH)                                                                      \
     extern "C" __global__ __launch_bounds__(256) void eh_append_kv_c##CH(                        \

@@ -102,6 +102,22 @@ class PagedAttention:
             int(stride), buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv),
             int(head_dim), int(block_tokens), int(plan[0]), int(plan[1]), wp, wb))
 
+    def decode_batched_e4m3(self, stream, q, pool, block_tables, ctx_lens, out, n_head,
+                            n_head_kv, head_dim, block_tokens, k_scale, v_scale, plan, workspace):
+        """decode_batched over an E4M3 pool (per-kv-head f32 scales k_scale /
+        v_scale): attention on decode(code) * scale.  `plan` is
+        PagedAttention.plan(..., kv_dtype=KvDataType.FP8) (token-balanced)."""
+        batch, stride = block_tables.shape
+        qp, qb = buf(q)
+        pp, pb = buf(pool)
+        bp, bb = buf(block_tables)
+        op, ob = buf(out)
+        wp, wb = buf(workspace)
+        check(self._L.eh_paged_decode_batched_e4m3(
+            self._ctx.handle, stream_handle(stream), qp, qb, pp, pb, bp, bb, int(stride),
+            buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv), int(head_dim),
+            int(block_tokens), buf(k_scale)[0], buf(v_scale)[0], int(plan[1]), wp, wb))
+
     def append_decode_batched(self, stream, layout, pool, keys, values, block_tables, start_pos,
                               q, out, n_head, head_dim, plan, workspace):
         """One decode step in one launch: row b of keys/values [B, row_len]

@@ -110,6 +110,33 @@ class PagedKvGpu:
                                            int(stride), buf(cu_seqlens)[0], buf(start_pos)[0],
                                            int(batch), int(total_tokens)))
 
+    # ---- FP8 (E4M3) pools with per-kv-head f32 scales ---------------------
+    def append_kv_e4m3_batched(self, stream, layout, pool, keys, values, block_tables, cu_seqlens,
+                               start_pos, total_tokens, head_dim, k_scale, v_scale):
+        """append_kv_batched into an E4M3 pool: keys/values [T, row_len] f32 are
+        stored as quantize(x / scale[head]) (round to nearest even, saturating
+        at 448); k_scale/v_scale [n_kv] f32 device tensors."""
+        pp, pb = buf(pool)
+        kp, kb = buf(keys)
+        vp, vb = buf(values)
+        bp, bb = buf(block_tables)
+        batch, stride = block_tables.shape
+        check(self._L.eh_append_kv_e4m3_batched(
+            self._ctx.handle, stream_handle(stream), C.byref(layout.c()), pp, pb, kp, kb, vp, vb, bp,
+            bb, int(stride), buf(cu_seqlens)[0], buf(start_pos)[0], int(batch), int(total_tokens),
+            int(head_dim), buf(k_scale)[0], buf(v_scale)[0]))
+
+    def read_e4m3(self, stream, layout, pool, block_table, out, start_token, n_tokens, is_value,
+                  head_dim, scale):
+        """read_keys / read_values of an E4M3 pool, dequantised: out [n, row_len]
+        f32 = decode(code) * scale[head]."""
+        pp, pb = buf(pool)
+        bp, bb = buf(block_table)
+        op, ob = buf(out)
+        check(self._L.eh_gather_kv_e4m3(self._ctx.handle, stream_handle(stream), C.byref(layout.c()),
+                                        pp, pb, bp, bb, op, ob, int(start_token), int(n_tokens),
+                                        int(is_value), int(head_dim), buf(scale)[0]))
+
     def copy_pages(self, stream, layout, pool, src_ids, dst_ids):
         """Whole-page copies dst_ids[k] <- src_ids[k] (copy-on-write, compaction)."""
         pp, pb = buf(pool)
