@@ -321,6 +321,33 @@ def suite(args, dev):
           "latency_us": round(us_g, 2), "GB/s": round(g_bytes / us_g / 1e3, 1)})
     del pool2
 
+    # ---- config 2's decode over E4M3 pages (per-kv-head scales): 16 distinct
+    # pools rotated through the captured calls, so the 256 MB MALL cannot hold them
+    lay8 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.FP8)
+    pools8 = [torch.randint(0, 0x7E, (lay8.floats_total(),), generator=gen, device=dev,
+                            dtype=torch.uint8) for _ in range(16)]
+    q8 = torch.randn((32, 12, 128), generator=gen, device=dev)
+    o8 = torch.empty_like(q8)
+    ks8 = torch.full((2,), 0.01, device=dev)
+    vs8 = torch.full((2,), 0.02, device=dev)
+    lens8 = torch.from_numpy((s2.ctx_lens + 1).astype(np.int32)).to(dev)
+    plan8 = PagedAttention.plan(32, 12, 2, 128, 16, int(s2.ctx_lens.max()) + 1, 0, KvDataType.FP8)
+    ws8 = PagedAttention.workspace(plan8)
+    turn = [0]
+
+    def dec8(st):
+        p = pools8[turn[0] % len(pools8)]
+        turn[0] += 1
+        pa.decode_batched_e4m3(st, q8, p, dtab2, lens8, o8, 12, 2, 128, 16, ks8, vs8, plan8, ws8)
+    us8 = graph_time_us(dec8, 20, 32)
+    b8 = int((s2.ctx_lens + 1).sum()) * 2 * 128 * 2 * 1
+    emit({"config": 2, "what": "decode over E4M3 pages (fp8 KV, per-kv-head scales), B=32, 12/2 "
+          "heads, hd 128, one layer", "latency_us": round(us8, 2), "kv_bytes": b8,
+          "GB/s": round(b8 / us8 / 1e3, 1), "hbm_frac_of_8TB/s": round(b8 / us8 / 1e3 / 8000.0, 4),
+          "kernel": PagedAttention.kernel_name(12, 2, 128, 16, KvDataType.FP8) +
+          " + eh_decode_tiles_merge"})
+    del pools8
+
     # ---- config 3: bf16 chunked prefill, B=8, 512 new tokens on 2048 cached, 32/8 heads
     s3 = synth.config3(0)
     tab3 = synth.block_tables(s3, extra_tokens=512)

@@ -223,6 +223,29 @@ eh_status eh_paged_decode_batched_e4m3(eh_context* ctx, eh_stream stream, const 
                                        const float* k_scale, const float* v_scale,
                                        uint32_t max_splits, void* workspace, uint64_t workspace_bytes);
 
+/* ---- Batched decode over the protected-sinks range (extension: the
+ * attention-sinks + sliding-window rule of openspec/specs/protected-kv-sinks/
+ * spec.md:9-15 and openspec/changes/archive/
+ * 2026-08-28-agent-runtime-optimizations/design.md:211-216, which the
+ * reference's paged_attention.cu does not implement): the query at
+ * pos = ctx_lens[b] - 1 attends tokens [0, sink_tokens) and
+ * [max(sink_tokens, pos - window_tokens), pos]; window_tokens 0 attends all.
+ * Only the tiles holding attended tokens are read and the work split counts
+ * only those.  kv_dtype EH_KV_F16 / EH_KV_BF16 (scales NULL) or EH_KV_FP8
+ * (k_scale / v_scale as eh_append_kv_e4m3_batched); token-balanced shapes,
+ * max_splits and workspace from eh_decode_plan with hint 0. */
+eh_status eh_paged_decode_batched_window(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                                         const float* q, uint64_t q_bytes, const void* pool,
+                                         uint64_t pool_bytes, const uint32_t* block_tables,
+                                         uint64_t bt_bytes, uint32_t bt_stride,
+                                         const uint32_t* ctx_lens, uint32_t batch, float* out,
+                                         uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                                         uint32_t head_dim, uint32_t block_tokens,
+                                         uint32_t sink_tokens, uint32_t window_tokens,
+                                         const float* k_scale, const float* v_scale,
+                                         uint32_t max_splits, void* workspace,
+                                         uint64_t workspace_bytes);
+
 /* ---- Fused decode-step append + attention (extension: the batched
  * PagedKvGpu::append_kv of paged_kv.rs:200-327 -- in production the decode
  * append slot of NormRope::launch_fused_qk, norm_rope.cu:280-298 -- followed

@@ -200,9 +200,13 @@ static double dot_f64(const float* a, const float* b, size_t n) {
     return s;
 }
 
-void orc_sdpa_decode(const float* pool, const uint32_t* block_table, size_t block_tokens,
-                     size_t seq_tokens, const float* query, size_t n_head, size_t n_head_kv,
-                     size_t head_dim, int causal, size_t query_pos, float* out) {
+/* window > 0 additionally keeps only the attention sinks t < sink and the
+ * rolling window t >= max(sink, seq_tokens - 1 - window) (see
+ * orc_sdpa_decode_window_batched); window == 0 is the reference function. */
+static void sdpa_decode_core(const float* pool, const uint32_t* block_table, size_t block_tokens,
+                             size_t seq_tokens, const float* query, size_t n_head, size_t n_head_kv,
+                             size_t head_dim, int causal, size_t query_pos, size_t sink,
+                             size_t window, float* out) {
     /* forward_cpu.rs:436-439 */
     memset(out, 0, n_head * head_dim * sizeof(float));
     if (seq_tokens == 0 || n_head == 0 || head_dim == 0) return;
@@ -224,6 +228,7 @@ void orc_sdpa_decode(const float* pool, const uint32_t* block_table, size_t bloc
         for (size_t t = 0; t < seq_tokens; ++t) {
             scores[t] = -INFINITY;
             if (causal && t > query_pos) continue;
+            if (window && t >= sink && t + 1 + window < seq_tokens) continue; /* t < n - 1 - W */
             size_t phys = block_table[t / block_tokens];
             size_t base = phys * f_blk + (t % block_tokens) * f_tok;
             double s = dot_f64(qv, pool + base + hk * head_dim, head_dim) * scale;
@@ -257,6 +262,30 @@ void orc_sdpa_decode(const float* pool, const uint32_t* block_table, size_t bloc
         for (size_t d = 0; d < head_dim; ++d) out[qh * head_dim + d] = (float)out_h[d];
     }
     free(scores); free(weights); free(out_h);
+}
+
+void orc_sdpa_decode(const float* pool, const uint32_t* block_table, size_t block_tokens,
+                     size_t seq_tokens, const float* query, size_t n_head, size_t n_head_kv,
+                     size_t head_dim, int causal, size_t query_pos, float* out) {
+    sdpa_decode_core(pool, block_table, block_tokens, seq_tokens, query, n_head, n_head_kv,
+                     head_dim, causal, query_pos, 0, 0, out);
+}
+
+/* Decode attention over the protected-sinks range of the reference's design
+ * (openspec/changes/archive/2026-08-28-agent-runtime-optimizations/
+ * design.md:211-216, specs/protected-kv-sinks/spec.md:9-15): the query at
+ * pos = n - 1 attends t in [0, sink) U [max(sink, pos - W), pos]; W == 0
+ * attends all n tokens.  Otherwise sdpa_decode (forward_cpu.rs:424-510). */
+void orc_sdpa_decode_window_batched(const float* pool, const uint32_t* bt, size_t bt_stride,
+                                    const uint32_t* lens, size_t batch, size_t block_tokens,
+                                    const float* q, size_t n_head, size_t n_head_kv,
+                                    size_t head_dim, size_t sink, size_t window, float* out) {
+    const size_t qs = n_head * head_dim;
+    for (size_t b = 0; b < batch; ++b) {
+        size_t n = lens[b];
+        sdpa_decode_core(pool, bt + b * bt_stride, block_tokens, n, q + b * qs, n_head, n_head_kv,
+                         head_dim, 1, n ? n - 1 : 0, sink, window, out + b * qs);
+    }
 }
 
 void orc_sdpa_decode_batched(const float* pool, const uint32_t* bt, size_t bt_stride,

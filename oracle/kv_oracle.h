@@ -160,6 +160,14 @@ void orc_stream_prune_blocks(const orc_stream* m, const uint32_t* table, size_t 
                              uint32_t* retained, size_t* n_retained, uint32_t* evicted,
                              size_t* n_evicted);
 
+/* sdpa_decode over the protected-sinks range [0, sink) U [max(sink, n-1-W), n-1]
+ * (openspec/changes/archive/2026-08-28-agent-runtime-optimizations/design.md:211-216);
+ * window 0 attends every token. */
+void orc_sdpa_decode_window_batched(const float* pool, const uint32_t* bt, size_t bt_stride,
+                                    const uint32_t* lens, size_t batch, size_t block_tokens,
+                                    const float* q, size_t n_head, size_t n_head_kv,
+                                    size_t head_dim, size_t sink, size_t window, float* out);
+
 /* FP8 E4M3 (OCP E4M3FN) KV storage with per-head f32 scales: the format of
  * openspec/archive/2026-08-28-fp8-kv-cache-quantization/design.md:3-6. */
 float orc_e4m3_to_f32(uint8_t code);

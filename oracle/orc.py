@@ -42,6 +42,8 @@ def lib():
             "orc_cache_buffer": (vp, [vp, P(sz)]),
             "orc_sdpa_decode": (None, [vp, vp, sz, sz, vp, sz, sz, sz, i32, sz, vp]),
             "orc_sdpa_decode_batched": (None, [vp, vp, sz, vp, sz, sz, vp, sz, sz, sz, vp]),
+            "orc_sdpa_decode_window_batched": (None, [vp, vp, sz, vp, sz, sz, vp, sz, sz, sz, sz, sz,
+                                                      vp]),
             "orc_prefill_causal": (None, [vp, vp, sz, vp, sz, sz, sz, sz, sz, vp]),
             "orc_f16_to_f32": (f32, [C.c_uint16]),
             "orc_f16_to_f32_array": (None, [vp, vp, sz]),
@@ -215,6 +217,21 @@ def sdpa_decode_batched(pool, bt, lens, block_tokens, q, n_head, n_head_kv, head
     out = np.zeros((B, n_head, head_dim), dtype=np.float32)
     lib().orc_sdpa_decode_batched(_p(pool), _p(bt), bt.shape[1], _p(lens), B, block_tokens,
                                   _p(q), n_head, n_head_kv, head_dim, _p(out))
+    return out
+
+
+def sdpa_decode_window_batched(pool, bt, lens, block_tokens, q, n_head, n_head_kv, head_dim,
+                               sink, window):
+    """sdpa_decode over [0, sink) U [max(sink, n-1-window), n-1]; window 0 = all."""
+    pool = np.ascontiguousarray(pool, dtype=np.float32)
+    bt = np.ascontiguousarray(bt, dtype=np.uint32)
+    lens = np.ascontiguousarray(lens, dtype=np.uint32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    B = len(lens)
+    out = np.zeros((B, n_head, head_dim), dtype=np.float32)
+    lib().orc_sdpa_decode_window_batched(_p(pool), _p(bt), bt.shape[1], _p(lens), B, block_tokens,
+                                         _p(q), n_head, n_head_kv, head_dim, int(sink), int(window),
+                                         _p(out))
     return out
 
 

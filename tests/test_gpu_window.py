@@ -1,0 +1,115 @@
+"""GPU parity of decode over the protected-sinks range (attention sinks +
+rolling window, openspec/specs/protected-kv-sinks/spec.md:9-15) against the
+oracle's windowed sdpa_decode (pinned in tests/test_oracle_window.py).
+
+Tolerance: |gpu - ref| <= 2e-3 + 1e-3*|ref| (16-bit and E4M3 pages).  The
+cases cover sinks that end mid-tile, windows shorter than one tile, windows
+that start mid-tile, gaps of many tiles, sinks covering the whole sequence,
+runs that cross sequences whose walked tiles skip a gap, and window 0 (which
+must equal the plain decode bit for bit).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import orc
+from titan_amd import KvDataType, PagedAttention
+
+pytestmark = pytest.mark.gpu
+
+TD = {KvDataType.F16: torch.float16, KvDataType.BF16: torch.bfloat16}
+
+
+def i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev)
+
+
+def make_tables(rng, lens, bt):
+    need = [(int(l) + bt - 1) // bt for l in lens]
+    stride = max(max(need), 1)
+    nb = sum(need) + 2
+    perm = rng.permutation(nb).astype(np.uint32)
+    tab = np.full((len(lens), stride), 0xFFFFFFFF, np.uint32)
+    p = 0
+    for b, c in enumerate(need):
+        tab[b, :c] = perm[p:p + c]
+        p += c
+    return tab, nb
+
+
+def check_close(gpu, ref):
+    gpu, ref = np.asarray(gpu, np.float64), np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(gpu))
+    bad = np.abs(gpu - ref) > 2e-3 + 1e-3 * np.abs(ref)
+    assert not bad.any(), f"max abs err {np.max(np.abs(gpu - ref))} at {np.argwhere(bad)[:4]}"
+
+
+LENS = np.array([0, 1, 3, 4, 5, 16, 17, 33, 300, 2049, 3000, 100, 7], np.int64)
+
+
+def run(dev, dtype, shape, sink, window, seed, grid=None, lens=LENS):
+    n_head, n_kv, hd, bt = shape
+    rng = np.random.default_rng(seed)
+    tab, nb = make_tables(rng, lens, bt)
+    n = nb * bt * 2 * n_kv * hd
+    q = rng.standard_normal((len(lens), n_head, hd)).astype(np.float32)
+    ks = vs = None
+    if dtype == KvDataType.FP8:
+        codes = rng.integers(0, 256, n).astype(np.uint8)
+        codes[(codes & 0x7F) == 0x7F] = 0x3C
+        ksn = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
+        vsn = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
+        f = orc.e4m3_to_f32(codes).reshape(nb, bt, 2, n_kv, hd)
+        f[:, :, 0] *= ksn[None, None, :, None]
+        f[:, :, 1] *= vsn[None, None, :, None]
+        pool_f32 = f.reshape(-1)
+        pool = torch.from_numpy(codes).to(dev)
+        ks, vs = torch.from_numpy(ksn).to(dev), torch.from_numpy(vsn).to(dev)
+    else:
+        host = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(TD[dtype])
+        pool, pool_f32 = host.to(dev), host.float().numpy()
+    plan = PagedAttention.plan(len(lens), n_head, n_kv, hd, bt, int(max(lens)), 0, dtype)
+    assert plan[0] == 0
+    if grid is not None:
+        plan = (0, grid, plan[2])
+    out = torch.full((len(lens), n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).decode_batched_window(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                            i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, sink,
+                                            window, plan, PagedAttention.workspace(plan), ks, vs)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_decode_window_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head,
+                                         n_kv, hd, sink, window)
+    return out.cpu().numpy(), ref, (q, pool, tab, plan)
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16, KvDataType.FP8],
+                         ids=lambda d: d.name)
+@pytest.mark.parametrize("sink,window", [(4, 1), (4, 15), (4, 16), (4, 100), (0, 40), (20, 1000),
+                                         (40, 3)])
+def test_window_matches_oracle(dev, dtype, sink, window):
+    out, ref, _ = run(dev, dtype, (12, 2, 128, 16), sink, window, 7 + sink + window)
+    check_close(out, ref)
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128, 16), (8, 1, 128, 32), (16, 4, 128, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_window_shapes(dev, shape):
+    out, ref, _ = run(dev, KvDataType.F16, shape, 4, 200, 11 + sum(shape))
+    check_close(out, ref)
+
+
+@pytest.mark.parametrize("grid", [1, 2, 5, 64])
+def test_window_small_grids(dev, grid):
+    """Runs that walk several sequences across their sink/window gaps."""
+    out, ref, _ = run(dev, KvDataType.F16, (12, 2, 128, 16), 4, 50, 20 + grid, grid)
+    check_close(out, ref)
+
+
+def test_window_zero_equals_plain_decode(dev):
+    out, _, (q, pool, tab, plan) = run(dev, KvDataType.F16, (12, 2, 128, 16), 4, 0, 3)
+    plain = torch.full(out.shape, float("nan"), device=dev)
+    PagedAttention(0).decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                     i32(LENS, dev), plain, 12, 2, 128, 16, KvDataType.F16, plan,
+                                     PagedAttention.workspace(plan))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.view(np.uint32), plain.cpu().numpy().view(np.uint32))

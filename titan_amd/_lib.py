@@ -56,6 +56,9 @@ _SIGS = {
                                       u32, u32, u32, u32, u32, u32, vp, u64]),
     "eh_paged_decode_batched_e4m3": (i32, [vp, vp, vp, u64, vp, u64, vp, u64, u32, vp, u32, vp, u64,
                                            u32, u32, u32, u32, vp, vp, u32, vp, u64]),
+    "eh_paged_decode_batched_window": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, u32,
+                                             vp, u64, u32, u32, u32, u32, u32, u32, vp, vp, u32, vp,
+                                             u64]),
     "eh_append_decode_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp, u64,
                                        u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp, u64]),
     "eh_flash_attention_prefill": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64,

@@ -361,6 +361,7 @@ struct tiles_args {
     void* ws;
     const float* k_scale;  // E4M3 pages only
     const float* v_scale;
+    uint32_t sink, window;  // protected-sinks range; window 0 attends every token
 };
 
 eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const tiles_cfg& t) {
@@ -382,13 +383,13 @@ eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const 
                               (uint8_t*)a.pool, a.n_blocks, a.bt, a.bt_stride, a.lens, a.lens_add,
                               (const uint8_t*)a.new_k, (const uint8_t*)a.new_v, a.batch, a.out,
                               part_acc, part_ml, a.n_head, a.n_head_kv, a.block_tokens,
-                              (uint32_t)log2_exact(a.block_tokens), scale_log2, a.grid, a.k_scale,
-                              a.v_scale);
+                              (uint32_t)log2_exact(a.block_tokens), scale_log2, a.grid, a.sink,
+                              a.window, a.k_scale, a.v_scale);
     if (st != EH_OK) return st;
     return launch(c, mod, "eh_decode_tiles_merge",
                   dim3((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch), dim3(256), stream,
                   (const float*)part_acc, (const float*)part_ml, a.out, a.lens, a.lens_add, a.batch,
-                  a.n_head, 128u, a.grid);
+                  a.n_head, 128u, a.grid, a.sink, a.window);
 }
 
 // Splits: aim for enough workgroups to fill 256 CUs several times over, with
@@ -1024,14 +1025,17 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     return run_decode(c, stream, a);
 }
 
-eh_status eh_paged_decode_batched_e4m3(eh_context* c, eh_stream stream, const float* q,
-                                       uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
-                                       const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
-                                       const uint32_t* ctx_lens, uint32_t batch, float* out,
-                                       uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
-                                       uint32_t head_dim, uint32_t block_tokens,
-                                       const float* k_scale, const float* v_scale,
-                                       uint32_t max_splits, void* ws, uint64_t ws_bytes) {
+// Token-balanced batched decode with every option: E4M3 scales and the
+// protected-sinks range.
+static eh_status decode_tiles_entry(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                    const float* q, uint64_t q_bytes, const void* pool,
+                                    uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes,
+                                    uint32_t bt_stride, const uint32_t* ctx_lens, uint32_t batch,
+                                    float* out, uint64_t out_bytes, uint32_t n_head,
+                                    uint32_t n_head_kv, uint32_t head_dim, uint32_t block_tokens,
+                                    uint32_t sink, uint32_t window, const float* k_scale,
+                                    const float* v_scale, uint32_t max_splits, void* ws,
+                                    uint64_t ws_bytes) {
     if (!c) return fail(EH_INVALID_ARGS, "null context");
     if (n_head < 1) return invalid_size(1, n_head);
     if (n_head_kv < 1) return invalid_size(1, n_head_kv);
@@ -1039,23 +1043,24 @@ eh_status eh_paged_decode_batched_e4m3(eh_context* c, eh_stream stream, const fl
     if (block_tokens < 1) return invalid_size(1, block_tokens);
     if (batch == 0) return EH_OK;
     if (!ctx_lens) return fail(EH_INVALID_ARGS, "ctx_lens is null");
-    if (!k_scale || !v_scale) return fail(EH_INVALID_ARGS, "scale arrays are null");
+    const bool f8 = kv_dtype == EH_KV_FP8;
+    if (f8 && (!k_scale || !v_scale)) return fail(EH_INVALID_ARGS, "scale arrays are null");
     if (max_splits < 1) return invalid_size(1, max_splits, "max_splits");
-    const tiles_cfg tc = pick_tiles(EH_KV_FP8, head_dim, n_head, n_head_kv, block_tokens, batch);
-    if (!tc.ok) return fail(EH_UNSUPPORTED, "E4M3 decode: shape outside the balanced kernel");
+    const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, batch);
+    if (!tc.ok) return fail(EH_UNSUPPORTED, "shape outside the token-balanced kernel");
     const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
     const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
-    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim;
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * (f8 ? 1 : 2);
     if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
     const uint64_t ws_need = tiles_ws_bytes(max_splits, batch, n_head);
     if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
     eh_status st = bind(c);
     if (st) return st;
     tiles_args a{};
-    a.kv_dtype = EH_KV_FP8;
+    a.kv_dtype = kv_dtype;
     a.q = q;
     a.pool = const_cast<void*>(pool);
     a.n_blocks = pool_bytes / page_bytes;
@@ -1070,9 +1075,41 @@ eh_status eh_paged_decode_batched_e4m3(eh_context* c, eh_stream stream, const fl
     a.block_tokens = block_tokens;
     a.grid = max_splits;
     a.ws = ws;
-    a.k_scale = k_scale;
-    a.v_scale = v_scale;
+    a.k_scale = f8 ? k_scale : nullptr;
+    a.v_scale = f8 ? v_scale : nullptr;
+    a.sink = sink;
+    a.window = window;
     return run_tiles(c, stream, a, tc);
+}
+
+eh_status eh_paged_decode_batched_e4m3(eh_context* c, eh_stream stream, const float* q,
+                                       uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                                       const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                                       const uint32_t* ctx_lens, uint32_t batch, float* out,
+                                       uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                                       uint32_t head_dim, uint32_t block_tokens,
+                                       const float* k_scale, const float* v_scale,
+                                       uint32_t max_splits, void* ws, uint64_t ws_bytes) {
+    return decode_tiles_entry(c, stream, EH_KV_FP8, q, q_bytes, pool, pool_bytes, bt, bt_bytes,
+                              bt_stride, ctx_lens, batch, out, out_bytes, n_head, n_head_kv,
+                              head_dim, block_tokens, 0, 0, k_scale, v_scale, max_splits, ws,
+                              ws_bytes);
+}
+
+eh_status eh_paged_decode_batched_window(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                         const float* q, uint64_t q_bytes, const void* pool,
+                                         uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes,
+                                         uint32_t bt_stride, const uint32_t* ctx_lens,
+                                         uint32_t batch, float* out, uint64_t out_bytes,
+                                         uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
+                                         uint32_t block_tokens, uint32_t sink_tokens,
+                                         uint32_t window_tokens, const float* k_scale,
+                                         const float* v_scale, uint32_t max_splits, void* ws,
+                                         uint64_t ws_bytes) {
+    return decode_tiles_entry(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes,
+                              bt_stride, ctx_lens, batch, out, out_bytes, n_head, n_head_kv,
+                              head_dim, block_tokens, sink_tokens, window_tokens, k_scale, v_scale,
+                              max_splits, ws, ws_bytes);
 }
 
 eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l,

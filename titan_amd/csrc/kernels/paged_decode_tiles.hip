@@ -158,6 +158,44 @@ __device__ __forceinline__ tile_split make_split(uint32_t T, uint32_t P) {
     return tile_split{T / P, T % P};
 }
 
+// Tokens a decode query attends out of the n of its sequence: all of them,
+// or with a window W > 0 the attention sinks [0, min(sink, n)) and the
+// rolling window [lo, n), lo = max(sink, n - 1 - W) (the valid range of the
+// reference's protected-sinks design, openspec/changes/archive/
+// 2026-08-28-agent-runtime-optimizations/design.md:211-216).  Only tiles
+// holding attended tokens are walked: tiles 0 .. st-1, then the window's
+// from lo / 16 on; walked tile j is tile j < st ? j : j + gap.
+struct span {
+    uint32_t n, lo, sink, st, gap, tiles;
+    __device__ __forceinline__ uint32_t tile(uint32_t j) const { return j < st ? j : j + gap; }
+    __device__ __forceinline__ bool valid(uint32_t t) const { return t < n && (t < sink || t >= lo); }
+    // some token of the tile at tok0 is not attended
+    __device__ __forceinline__ bool partial(uint32_t tok0) const {
+        return tok0 + TILE > n || (lo > sink && tok0 < lo && tok0 + TILE > sink);
+    }
+};
+__device__ __forceinline__ span make_span(uint32_t n, uint32_t sink, uint32_t window) {
+    const uint32_t full = n / TILE + (n % TILE != 0u);
+    span sp{n, 0u, 0u, full, 0u, full};
+    if (window != 0u && n != 0u) {
+        const uint32_t back = n - 1u > window ? n - 1u - window : 0u;
+        sp.lo = back > sink ? back : sink;
+        sp.sink = sink;
+        const uint32_t ns = sink < n ? sink : n;
+        const uint32_t st = ns / TILE + (ns % TILE != 0u);
+        const uint32_t wf = sp.lo / TILE;
+        if (sp.lo >= n) {  // the sinks cover the sequence
+            sp.st = st;
+            sp.tiles = st;
+        } else if (wf > st) {  // a gap between sink and window tiles
+            sp.st = st;
+            sp.gap = wf - st;
+            sp.tiles = st + (full - wf);
+        }
+    }
+    return sp;
+}
+
 // Two floats as a packed 16-bit pair (RNE), low half first.
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
@@ -204,7 +242,8 @@ __device__ __forceinline__ void decode_tiles(
     uint32_t batch, float* __restrict__ out, float* __restrict__ part_acc,
     float* __restrict__ part_ml, uint32_t n_head, uint32_t n_head_kv,
     uint32_t block_tokens, uint32_t bt_shift, float scale_log2, uint32_t n_runs,
-    const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
+    uint32_t sink, uint32_t window, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale) {
     constexpr int HD = 128;
     constexpr int KSTEPS = HD / 32;  // MFMA steps over head_dim
     // E4M3 pages are converted to f16 in registers (exact) and use the f16 path
@@ -245,7 +284,7 @@ __device__ __forceinline__ void decode_tiles(
         for (uint32_t base = 0; base < batch; base += 64) {
             const uint32_t j = base + lane;
             const uint32_t n = j < batch ? lens[j] + lens_add : 0u;
-            uint32_t t = n / TILE + (n % TILE != 0u);
+            uint32_t t = make_span(n, sink, window).tiles;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const uint32_t y = __shfl_up(t, o, 64);
@@ -291,7 +330,7 @@ __device__ __forceinline__ void decode_tiles(
             const uint32_t f = F0 + k;
             uint32_t b = b0;
             while (cum[b + 1] <= f) ++b;
-            const uint32_t page = ((f - cum[b]) * TILE) >> bt_shift;
+            const uint32_t page = (make_span(ntok[b], sink, window).tile(f - cum[b]) * TILE) >> bt_shift;
             if (page < bt_stride) {
                 const uint32_t p = bt[(uint64_t)b * bt_stride + page];
                 phys = (uint64_t)p < n_blocks ? p : 0xFFFFFFFFu;
@@ -381,13 +420,13 @@ __device__ __forceinline__ void decode_tiles(
             iss_c0 = iss_c1;
             iss_c1 = uni(cum[iss_b + 1]);
         }
-        const uint32_t tok0 = (f - iss_c0) * TILE;
+        const uint32_t ntk = uni(ntok[iss_b]);
+        const uint32_t tok0 = (window ? make_span(ntk, sink, window).tile(f - iss_c0) : f - iss_c0) * TILE;
         const uint32_t phys = uni((uint32_t)__builtin_amdgcn_readlane((int)pv, (int)(k & 63u)));
         const bool pok = phys != 0xFFFFFFFFu;
         physp[D] = phys;
         const uint8_t* base = pool + (uint64_t)(pok ? phys : 0u) * page_bytes +
                               (uint64_t)(tok0 & slot_mask) * slot_bytes + kv_off;
-        const uint32_t ntk = uni(ntok[iss_b]);
         const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
         const bool last = new_k != nullptr && tok0 + TILE >= ntk;  // holds the appended token
         // K: token x of the tile; 16-bit: dims 32 st + 8 g .. (16 B per step),
@@ -478,8 +517,9 @@ __device__ __forceinline__ void decode_tiles(
     auto compute = [&](auto Dc, uint32_t k) {
         constexpr int D = decltype(Dc)::value;
         const uint32_t f = F0 + k;
-        const uint32_t tok0 = (f - cmp_c0) * TILE;
         const uint32_t ntk = uni(ntok[cmp_b]);
+        const span sp = make_span(ntk, sink, window);
+        const uint32_t tok0 = (window ? sp.tile(f - cmp_c0) : f - cmp_c0) * TILE;
         const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
         const uint32_t phys = physp[D];
         if (phys == 0xFFFFFFFFu) return;  // masked page: its tokens do not count (uniform)
@@ -516,9 +556,12 @@ __device__ __forceinline__ void decode_tiles(
             s = K::mma(a, qa[st], s);
             s = K::mma(a, qb[st], s);
         }
-        if (nvalid < (uint32_t)TILE) {
+        if (window ? sp.partial(tok0) : nvalid < (uint32_t)TILE) {  // uniform
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[r] = (4 * g + r < nvalid) ? s[r] : -__builtin_inff();
+            for (int r = 0; r < 4; ++r) {
+                const bool ok = window ? sp.valid(tok0 + 4 * g + r) : 4 * g + r < nvalid;
+                s[r] = ok ? s[r] : -__builtin_inff();
+            }
         }
         // fused append: store the appended token's K/V slice of this kv
         // head from the registers that already hold it
@@ -625,7 +668,7 @@ __device__ __forceinline__ void decode_tiles(
 extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
     const uint32_t* __restrict__ lens, uint32_t lens_add, uint32_t batch, uint32_t n_head,
-    uint32_t head_dim, uint32_t P) {
+    uint32_t head_dim, uint32_t P, uint32_t sink, uint32_t window) {
     constexpr int NB = 16;
     __shared__ float sM[4][64], sL[4][64], sA[4][64];
     const uint32_t b = blockIdx.y;
@@ -633,8 +676,7 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
     const uint32_t wave = threadIdx.x >> 6;
     uint32_t tot = 0, before = 0, mine = 0;
     for (uint32_t j = lane; j < batch; j += 64) {
-        const uint32_t n = lens[j] + lens_add;
-        const uint32_t t = n / TILE + (n % TILE != 0u);
+        const uint32_t t = make_span(lens[j] + lens_add, sink, window).tiles;
         tot += t;
         before += j < b ? t : 0u;
         mine += j == b ? t : 0u;
@@ -715,10 +757,11 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
         const uint32_t* lens, uint32_t lens_add, const uint8_t* new_k, const uint8_t* new_v,       \
         uint32_t batch, float* out, float* part_acc, float* part_ml, uint32_t n_head,              \
         uint32_t n_head_kv, uint32_t block_tokens, uint32_t bt_shift, float scale_log2,            \
-        uint32_t n_runs, const float* k_scale, const float* v_scale) {                             \
+        uint32_t n_runs, uint32_t sink, uint32_t window, const float* k_scale,                     \
+        const float* v_scale) {                                                                    \
         decode_tiles<DT, G, 2, 16>(q, pool, n_blocks, bt, bt_stride, lens, lens_add, new_k, new_v, \
                                    batch, out, part_acc, part_ml, n_head, n_head_kv, block_tokens, \
-                                   bt_shift, scale_log2, n_runs, k_scale, v_scale);                \
+                                   bt_shift, scale_log2, n_runs, sink, window, k_scale, v_scale);  \
     }
 
 #define EH_TILES_ALL(DTN, DT) \

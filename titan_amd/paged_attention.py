@@ -118,6 +118,24 @@ class PagedAttention:
             buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv), int(head_dim),
             int(block_tokens), buf(k_scale)[0], buf(v_scale)[0], int(plan[1]), wp, wb))
 
+    def decode_batched_window(self, stream, q, pool, block_tables, ctx_lens, out, n_head,
+                              n_head_kv, head_dim, block_tokens, kv_dtype, sink_tokens,
+                              window_tokens, plan, workspace, k_scale=None, v_scale=None):
+        """decode_batched over the protected-sinks range: the query at
+        pos = ctx_lens[b] - 1 attends [0, sink) and [max(sink, pos - window), pos]
+        (window 0: every token).  E4M3 pools pass k_scale / v_scale."""
+        batch, stride = block_tables.shape
+        qp, qb = buf(q)
+        pp, pb = buf(pool)
+        bp, bb = buf(block_tables)
+        op, ob = buf(out)
+        wp, wb = buf(workspace)
+        check(self._L.eh_paged_decode_batched_window(
+            self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
+            int(stride), buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv),
+            int(head_dim), int(block_tokens), int(sink_tokens), int(window_tokens),
+            buf(k_scale)[0], buf(v_scale)[0], int(plan[1]), wp, wb))
+
     def append_decode_batched(self, stream, layout, pool, keys, values, block_tables, start_pos,
                               q, out, n_head, head_dim, plan, workspace):
         """One decode step in one launch: row b of keys/values [B, row_len]
