@@ -233,7 +233,15 @@ eh_status eh_paged_decode_batched_e4m3(eh_context* ctx, eh_stream stream, const 
  * Only the tiles holding attended tokens are read and the work split counts
  * only those.  kv_dtype EH_KV_F16 / EH_KV_BF16 (scales NULL) or EH_KV_FP8
  * (k_scale / v_scale as eh_append_kv_e4m3_batched); token-balanced shapes,
- * max_splits and workspace from eh_decode_plan with hint 0. */
+ * max_splits and workspace from eh_decode_plan with hint 0.
+ * block_mass (optional, [pool pages] f32, block_mass_bytes >= 4 * pages):
+ * += each page's attention mass, the softmax weights of its attended tokens
+ * summed over the q heads -- the H2O score that
+ * StreamingKvManager::record_attention_mass adds per block
+ * (engine-kvcache/src/streaming.rs:135-141); pages shared by several
+ * sequences get one addition from each, in any order.  It needs
+ * eh_decode_mass_workspace_bytes more workspace (after the plan's) and
+ * block_tokens a multiple of 16, and adds a third launch. */
 eh_status eh_paged_decode_batched_window(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
                                          const float* q, uint64_t q_bytes, const void* pool,
                                          uint64_t pool_bytes, const uint32_t* block_tables,
@@ -243,8 +251,13 @@ eh_status eh_paged_decode_batched_window(eh_context* ctx, eh_stream stream, uint
                                          uint32_t head_dim, uint32_t block_tokens,
                                          uint32_t sink_tokens, uint32_t window_tokens,
                                          const float* k_scale, const float* v_scale,
+                                         float* block_mass, uint64_t block_mass_bytes,
                                          uint32_t max_splits, void* workspace,
                                          uint64_t workspace_bytes);
+/* Extra workspace bytes eh_paged_decode_batched_window needs with block_mass
+ * (no reference counterpart). */
+uint64_t eh_decode_mass_workspace_bytes(uint32_t batch, uint32_t bt_stride, uint32_t block_tokens,
+                                        uint32_t n_head);
 
 /* ---- Fused decode-step append + attention (extension: the batched
  * PagedKvGpu::append_kv of paged_kv.rs:200-327 -- in production the decode

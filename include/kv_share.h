@@ -82,6 +82,12 @@ void eh_stream_destroy(eh_stream_mgr* m);
 void eh_stream_record_attention_mass(eh_stream_mgr* m, uint32_t block_id, float mass); /* :135-141 */
 uint64_t eh_stream_scores_len(const eh_stream_mgr* m);        /* block_scores.len() */
 float eh_stream_score(const eh_stream_mgr* m, uint32_t block_id); /* 0 past the end */
+/* Bulk form: record_attention_mass(i, masses[i]) for each i < n with
+ * masses[i] != 0 -- e.g. the block_mass array a decode launch accumulated
+ * (eh_paged_decode_batched_window), copied to the host.  Zero entries are
+ * skipped, which the reference's lookups (get(..).unwrap_or(0.0),
+ * streaming.rs:106-109) cannot tell from recording them. */
+void eh_stream_record_attention_masses(eh_stream_mgr* m, const float* masses, uint64_t n);
 /* prune_blocks (streaming.rs:87-132): retained (sink, kept middle by
  * descending score, recent) and evicted ids; both outputs need room for n.
  * Equal scores keep block-table order and NaN scores rank last (the

@@ -206,7 +206,7 @@ static double dot_f64(const float* a, const float* b, size_t n) {
 static void sdpa_decode_core(const float* pool, const uint32_t* block_table, size_t block_tokens,
                              size_t seq_tokens, const float* query, size_t n_head, size_t n_head_kv,
                              size_t head_dim, int causal, size_t query_pos, size_t sink,
-                             size_t window, float* out) {
+                             size_t window, float* out, double* mass) {
     /* forward_cpu.rs:436-439 */
     memset(out, 0, n_head * head_dim * sizeof(float));
     if (seq_tokens == 0 || n_head == 0 || head_dim == 0) return;
@@ -249,6 +249,11 @@ static void sdpa_decode_core(const float* pool, const uint32_t* block_table, siz
             if (sum_exp > 0.0)
                 for (size_t t = 0; t < seq_tokens; ++t) weights[t] /= sum_exp;
         }
+        /* attention mass per physical page, summed over heads: the H2O score
+         * StreamingKvManager::record_attention_mass adds (streaming.rs:135-141) */
+        if (mass)
+            for (size_t t = 0; t < seq_tokens; ++t)
+                if (weights[t] != 0.0) mass[block_table[t / block_tokens]] += weights[t];
         /* forward_cpu.rs:492-506: f64 weighted sum of V rows, zero weights skipped. */
         for (size_t d = 0; d < head_dim; ++d) out_h[d] = 0.0;
         for (size_t t = 0; t < seq_tokens; ++t) {
@@ -268,7 +273,7 @@ void orc_sdpa_decode(const float* pool, const uint32_t* block_table, size_t bloc
                      size_t seq_tokens, const float* query, size_t n_head, size_t n_head_kv,
                      size_t head_dim, int causal, size_t query_pos, float* out) {
     sdpa_decode_core(pool, block_table, block_tokens, seq_tokens, query, n_head, n_head_kv,
-                     head_dim, causal, query_pos, 0, 0, out);
+                     head_dim, causal, query_pos, 0, 0, out, NULL);
 }
 
 /* Decode attention over the protected-sinks range of the reference's design
@@ -279,12 +284,13 @@ void orc_sdpa_decode(const float* pool, const uint32_t* block_table, size_t bloc
 void orc_sdpa_decode_window_batched(const float* pool, const uint32_t* bt, size_t bt_stride,
                                     const uint32_t* lens, size_t batch, size_t block_tokens,
                                     const float* q, size_t n_head, size_t n_head_kv,
-                                    size_t head_dim, size_t sink, size_t window, float* out) {
+                                    size_t head_dim, size_t sink, size_t window, float* out,
+                                    double* mass) {
     const size_t qs = n_head * head_dim;
     for (size_t b = 0; b < batch; ++b) {
         size_t n = lens[b];
         sdpa_decode_core(pool, bt + b * bt_stride, block_tokens, n, q + b * qs, n_head, n_head_kv,
-                         head_dim, 1, n ? n - 1 : 0, sink, window, out + b * qs);
+                         head_dim, 1, n ? n - 1 : 0, sink, window, out + b * qs, mass);
     }
 }
 

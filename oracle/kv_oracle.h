@@ -162,11 +162,15 @@ void orc_stream_prune_blocks(const orc_stream* m, const uint32_t* table, size_t 
 
 /* sdpa_decode over the protected-sinks range [0, sink) U [max(sink, n-1-W), n-1]
  * (openspec/changes/archive/2026-08-28-agent-runtime-optimizations/design.md:211-216);
- * window 0 attends every token. */
+ * window 0 attends every token.  mass (optional, indexed by physical page):
+ * += the softmax weights of the page's tokens summed over q heads -- the
+ * attention mass StreamingKvManager::record_attention_mass adds
+ * (streaming.rs:135-141). */
 void orc_sdpa_decode_window_batched(const float* pool, const uint32_t* bt, size_t bt_stride,
                                     const uint32_t* lens, size_t batch, size_t block_tokens,
                                     const float* q, size_t n_head, size_t n_head_kv,
-                                    size_t head_dim, size_t sink, size_t window, float* out);
+                                    size_t head_dim, size_t sink, size_t window, float* out,
+                                    double* mass);
 
 /* FP8 E4M3 (OCP E4M3FN) KV storage with per-head f32 scales: the format of
  * openspec/archive/2026-08-28-fp8-kv-cache-quantization/design.md:3-6. */

@@ -43,7 +43,7 @@ def lib():
             "orc_sdpa_decode": (None, [vp, vp, sz, sz, vp, sz, sz, sz, i32, sz, vp]),
             "orc_sdpa_decode_batched": (None, [vp, vp, sz, vp, sz, sz, vp, sz, sz, sz, vp]),
             "orc_sdpa_decode_window_batched": (None, [vp, vp, sz, vp, sz, sz, vp, sz, sz, sz, sz, sz,
-                                                      vp]),
+                                                      vp, vp]),
             "orc_prefill_causal": (None, [vp, vp, sz, vp, sz, sz, sz, sz, sz, vp]),
             "orc_f16_to_f32": (f32, [C.c_uint16]),
             "orc_f16_to_f32_array": (None, [vp, vp, sz]),
@@ -221,18 +221,20 @@ def sdpa_decode_batched(pool, bt, lens, block_tokens, q, n_head, n_head_kv, head
 
 
 def sdpa_decode_window_batched(pool, bt, lens, block_tokens, q, n_head, n_head_kv, head_dim,
-                               sink, window):
-    """sdpa_decode over [0, sink) U [max(sink, n-1-window), n-1]; window 0 = all."""
+                               sink, window, n_blocks=None):
+    """sdpa_decode over [0, sink) U [max(sink, n-1-window), n-1]; window 0 = all.
+    With n_blocks, also returns the per-page attention mass (f64 [n_blocks])."""
     pool = np.ascontiguousarray(pool, dtype=np.float32)
     bt = np.ascontiguousarray(bt, dtype=np.uint32)
     lens = np.ascontiguousarray(lens, dtype=np.uint32)
     q = np.ascontiguousarray(q, dtype=np.float32)
     B = len(lens)
     out = np.zeros((B, n_head, head_dim), dtype=np.float32)
+    mass = None if n_blocks is None else np.zeros(n_blocks, dtype=np.float64)
     lib().orc_sdpa_decode_window_batched(_p(pool), _p(bt), bt.shape[1], _p(lens), B, block_tokens,
                                          _p(q), n_head, n_head_kv, head_dim, int(sink), int(window),
-                                         _p(out))
-    return out
+                                         _p(out), None if mass is None else _p(mass))
+    return out if mass is None else (out, mass)
 
 
 def prefill_causal(pool, block_table, block_tokens, q, q_tokens, pos_offset, n_head,

@@ -44,11 +44,12 @@ def test_code_objects_contain_launched_kernels():
             for g in (1, 2, 4, 6, 7, 8):
                 assert f"eh_decode_split_{dt}_hd{hd}_g{g}".encode() in dec
         assert b"eh_decode_merge" in dec
-    for dt in ("f16", "bf16"):
+    for dt in ("f16", "bf16", "fp8"):
         tl = open(os.path.join(_lib.LIB_DIR, f"paged_decode_tiles_{dt}.hsaco"), "rb").read()
         for g in (1, 2, 4, 6, 8):
             assert f"eh_decode_tiles_{dt}_hd128_g{g}".encode() in tl
-        assert b"eh_decode_tiles_merge" in tl
+            assert f"eh_decode_tiles_{dt}_hd128_g{g}_ext".encode() in tl
+        assert b"eh_decode_tiles_merge" in tl and b"eh_decode_tiles_mass" in tl
     pf = open(os.path.join(_lib.LIB_DIR, "paged_prefill.hsaco"), "rb").read()
     for dt in ("f32", "f16", "bf16"):
         for hd in (64, 128):

@@ -113,3 +113,103 @@ def test_window_zero_equals_plain_decode(dev):
                                      PagedAttention.workspace(plan))
     torch.cuda.synchronize()
     assert np.array_equal(out.view(np.uint32), plain.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,shape,sink,window,grid", [
+    (KvDataType.F16, (12, 2, 128, 16), 0, 0, None),
+    (KvDataType.F16, (12, 2, 128, 16), 4, 100, None),
+    (KvDataType.F16, (12, 2, 128, 16), 4, 100, 3),
+    (KvDataType.BF16, (8, 1, 128, 32), 4, 40, None),      # two tiles per page
+    (KvDataType.FP8, (32, 8, 128, 16), 0, 0, None),
+    (KvDataType.F16, (16, 4, 128, 64), 20, 500, 7),
+], ids=lambda v: str(v))
+def test_block_mass_matches_oracle(dev, dtype, shape, sink, window, grid):
+    """block_mass[page] += the page's attention mass summed over q heads (the
+    H2O score of record_attention_mass), against the oracle's f64 weights;
+    each sequence's pages receive n_head in total."""
+    n_head, n_kv, hd, bt = shape
+    rng = np.random.default_rng(5 + sink + window)
+    tab, nb = make_tables(rng, LENS, bt)
+    n = nb * bt * 2 * n_kv * hd
+    q = rng.standard_normal((len(LENS), n_head, hd)).astype(np.float32)
+    ks = vs = None
+    if dtype == KvDataType.FP8:
+        codes = rng.integers(0, 256, n).astype(np.uint8)
+        codes[(codes & 0x7F) == 0x7F] = 0x3C
+        f = orc.e4m3_to_f32(codes).reshape(nb, bt, 2, n_kv, hd) * 0.01
+        pool_f32, pool = f.astype(np.float32).reshape(-1), torch.from_numpy(codes).to(dev)
+        ks = vs = torch.full((n_kv,), 0.01, device=dev)
+    else:
+        host = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(TD[dtype])
+        pool, pool_f32 = host.to(dev), host.float().numpy()
+    plan = PagedAttention.plan(len(LENS), n_head, n_kv, hd, bt, int(max(LENS)), 0, dtype)
+    if grid is not None:
+        plan = (0, grid, plan[2])
+    extra = PagedAttention.mass_workspace_bytes(len(LENS), tab.shape[1], bt, n_head)
+    ws = torch.zeros((plan[2] + extra + 3) // 4, device=dev)
+    mass = torch.full((nb,), 0.5, device=dev)
+    out = torch.full((len(LENS), n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).decode_batched_window(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                            i32(LENS, dev), out, n_head, n_kv, hd, bt, dtype, sink,
+                                            window, plan, ws, ks, vs, block_mass=mass)
+    torch.cuda.synchronize()
+    ref, ref_mass = orc.sdpa_decode_window_batched(pool_f32, tab, LENS.astype(np.uint32), bt, q,
+                                                   n_head, n_kv, hd, sink, window, n_blocks=nb)
+    check_close(out.cpu().numpy(), ref)
+    got = mass.cpu().numpy().astype(np.float64) - 0.5
+    bad = np.abs(got - ref_mass) > 2e-4 * n_head + 1e-3 * ref_mass
+    assert not bad.any(), (np.argwhere(bad)[:4], got[bad][:4], ref_mass[bad][:4])
+    for b, L in enumerate(LENS):
+        if L:
+            pages = [int(p) for p in tab[b, :(int(L) + bt - 1) // bt]]
+            assert abs(got[pages].sum() - n_head) < 1e-3 * n_head
+
+
+def test_h2o_scores_drive_prune_like_oracle(dev):
+    """End to end: three decode steps accumulate block_mass on the device; the
+    host StreamingKvManager records it and prunes.  Pages whose keys align with
+    the queries are heavy hitters; the retained and evicted pages equal the
+    oracle manager's fed with the oracle's f64 masses."""
+    from titan_amd.share import StreamingKvConfig, StreamingKvManager
+    n_head, n_kv, hd, bt = 8, 1, 128, 16
+    rng = np.random.default_rng(17)
+    lens = np.array([1000, 900], np.int64)
+    tab, nb = make_tables(rng, lens, bt)
+    pool_f32 = (rng.standard_normal((nb, bt, 2, n_kv, hd)) * 0.3).astype(np.float32)
+    q = rng.standard_normal((2, n_head, hd)).astype(np.float32)
+    heavy = {0: [10, 25, 40], 1: [7, 30, 44]}   # page indices within each sequence
+    for b, pages in heavy.items():
+        for k, j in enumerate(pages):            # distinct strengths: distinct masses
+            pool_f32[tab[b, j], :, 0, 0] = q[b].mean(axis=0) * (0.4 + 0.1 * k)
+    host = torch.from_numpy(pool_f32.reshape(-1)).half()
+    pool, pool_f32 = host.to(dev), host.float().numpy()
+    plan = PagedAttention.plan(2, n_head, n_kv, hd, bt, 1000, 0, KvDataType.F16)
+    ws = torch.zeros((plan[2] + PagedAttention.mass_workspace_bytes(2, tab.shape[1], bt, n_head)
+                      + 3) // 4, device=dev)
+    mass = torch.zeros(nb, device=dev)
+    out = torch.empty((2, n_head, hd), device=dev)
+    ref_mass = np.zeros(nb)
+    for step in range(3):
+        L = lens - 2 + step
+        PagedAttention(0).decode_batched_window(None, torch.from_numpy(q).to(dev), pool,
+                                                i32(tab, dev), i32(L, dev), out, n_head, n_kv, hd,
+                                                bt, KvDataType.F16, 0, 0, plan, ws, block_mass=mass)
+        _, m = orc.sdpa_decode_window_batched(pool_f32, tab, L.astype(np.uint32), bt, q, n_head,
+                                              n_kv, hd, 0, 0, n_blocks=nb)
+        ref_mass += m
+    torch.cuda.synchronize()
+    got = mass.cpu().numpy()
+    assert np.allclose(got, ref_mass, rtol=1e-3, atol=2e-4 * n_head)
+    cfg = StreamingKvConfig(4 * bt, 8 * bt, 15 * bt, bt)   # 4 sink + 8 recent + 3 middle pages
+    mgr, ref = StreamingKvManager(cfg), orc.Streaming(4 * bt, 8 * bt, 15 * bt, bt)
+    mgr.record_attention_masses(got)
+    for i, v in enumerate(ref_mass.astype(np.float32)):
+        if v != 0.0:
+            ref.record_attention_mass(i, float(v))
+    for b in range(2):
+        row = tab[b, :(int(lens[b]) + bt - 1) // bt]
+        kept, evicted = mgr.prune_blocks(row)
+        rkept, revicted = ref.prune_blocks(row)
+        assert kept == rkept                      # sinks, heavy hitters by score, recent
+        assert sorted(evicted) == sorted(revicted)
+        assert sorted(kept[4:7]) == sorted(int(tab[b, j]) for j in heavy[b])

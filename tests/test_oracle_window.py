@@ -85,3 +85,30 @@ def test_gap_tokens_do_not_count():
     p3[tab[0, win_t // bt], win_t % bt, 1, :] = 1e4     # its V row
     moved = orc.sdpa_decode_window_batched(p3.reshape(-1), tab, lens, bt, q, n_head, n_kv, hd, 4, 50)
     assert not np.array_equal(moved, base)
+
+
+def test_attention_mass_invariants():
+    """Per-page attention mass (the H2O score of record_attention_mass,
+    streaming.rs:135-141): each sequence's pages receive n_head in total (each
+    head's weights sum to 1); with q = 0 every attended token weighs 1/|set|,
+    so a page receives n_head * (its attended tokens) / |set|."""
+    rng = np.random.default_rng(4)
+    n_kv, hd, n_head, bt = 2, 64, 6, 16
+    lens = np.array([1, 20, 300, 77], np.uint32)
+    tab, pool, q = setup(rng, lens, bt, n_kv, hd, n_head)
+    nb = int(tab[tab != 0xFFFFFFFF].max()) + 3
+    for sink, window in ((0, 0), (4, 30)):
+        _, mass = orc.sdpa_decode_window_batched(pool, tab, lens, bt, q, n_head, n_kv, hd, sink,
+                                                 window, n_blocks=nb)
+        assert abs(mass.sum() - n_head * len(lens)) < 1e-9
+        for b, n in enumerate(lens):
+            pages = set(int(p) for p in tab[b, :(int(n) + bt - 1) // bt])
+            assert abs(sum(mass[p] for p in pages) - n_head) < 1e-9
+        _, m0 = orc.sdpa_decode_window_batched(pool, tab, lens, bt, np.zeros_like(q), n_head, n_kv,
+                                               hd, sink, window, n_blocks=nb)
+        want = np.zeros(nb)
+        for b, n in enumerate(lens):
+            keep = attended(int(n), sink, window)
+            for t in keep:
+                want[tab[b, t // bt]] += n_head / len(keep)
+        assert np.allclose(m0, want, rtol=1e-12, atol=1e-12)

@@ -219,3 +219,22 @@ def test_streaming_random_matches_oracle(seed):
     for n in (0, 1, 5, 17, 60, 250):
         table = [int(x) for x in rng.permutation(400)[:n]]
         assert prod.prune_blocks(table) == ref.prune_blocks(table)
+
+
+def test_streaming_bulk_record_equals_per_block():
+    """record_attention_masses(array) == record_attention_mass(i, a[i]) for the
+    non-zero entries, as seen through prune_blocks and the scores."""
+    rng = np.random.default_rng(3)
+    cfg = StreamingKvConfig(4, 32, 96, 16)
+    a, b = StreamingKvManager(cfg), StreamingKvManager(cfg)
+    masses = np.where(rng.random(300) < 0.4, rng.random(300), 0.0).astype(np.float32)
+    for _ in range(2):
+        a.record_attention_masses(masses)
+        for i, m in enumerate(masses):
+            if m != 0.0:
+                b.record_attention_mass(i, float(m))
+    sa, sb = a.block_scores, b.block_scores
+    n = max(len(sa), len(sb))
+    assert np.array_equal(np.pad(sa, (0, n - len(sa))), np.pad(sb, (0, n - len(sb))))
+    table = rng.permutation(300)[:40]
+    assert a.prune_blocks(table) == b.prune_blocks(table)

@@ -57,8 +57,9 @@ _SIGS = {
     "eh_paged_decode_batched_e4m3": (i32, [vp, vp, vp, u64, vp, u64, vp, u64, u32, vp, u32, vp, u64,
                                            u32, u32, u32, u32, vp, vp, u32, vp, u64]),
     "eh_paged_decode_batched_window": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, u32,
-                                             vp, u64, u32, u32, u32, u32, u32, u32, vp, vp, u32, vp,
-                                             u64]),
+                                             vp, u64, u32, u32, u32, u32, u32, u32, vp, vp, vp, u64,
+                                             u32, vp, u64]),
+    "eh_decode_mass_workspace_bytes": (u64, [u32, u32, u32, u32]),
     "eh_append_decode_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp, u64,
                                        u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp, u64]),
     "eh_flash_attention_prefill": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64,
@@ -110,6 +111,7 @@ _SIGS = {
     "eh_stream_new": (vp, [eh_stream_cfg]),
     "eh_stream_destroy": (None, [vp]),
     "eh_stream_record_attention_mass": (None, [vp, u32, f32]),
+    "eh_stream_record_attention_masses": (None, [vp, vp, u64]),
     "eh_stream_scores_len": (u64, [vp]),
     "eh_stream_score": (f32, [vp, u32]),
     "eh_stream_prune_blocks": (None, [vp, vp, u64, vp, P(u64), vp, P(u64)]),

@@ -344,6 +344,13 @@ uint64_t tiles_ws_bytes(uint64_t grid, uint64_t batch, uint64_t n_head) {
     return 4ull * (grid + batch) * n_head * (128 + 2);
 }
 
+// Attention-mass scratch: one (weight sum, max) pair per (sequence, 16-token
+// tile the block table can address, q head), then the heads' final (M, L).
+uint64_t mass_rec_row(uint64_t bt_stride, uint64_t block_tokens) { return bt_stride * (block_tokens / 16); }
+uint64_t mass_ws_bytes(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens, uint64_t n_head) {
+    return 8ull * batch * n_head * (mass_rec_row(bt_stride, block_tokens) + 1);
+}
+
 struct tiles_args {
     uint32_t kv_dtype;
     const float* q;
@@ -362,12 +369,16 @@ struct tiles_args {
     const float* k_scale;  // E4M3 pages only
     const float* v_scale;
     uint32_t sink, window;  // protected-sinks range; window 0 attends every token
+    float* block_mass;      // optional H2O scores [n_blocks]: += attention mass per page
+    void* mass_ws;          // tile records + final (M, L), mass_ws_bytes
 };
 
 eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const tiles_cfg& t) {
     char name[64];
     const bool f8 = a.kv_dtype == EH_KV_FP8;
-    std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u", f8 ? "fp8" : dt_name(a.kv_dtype), t.g);
+    const bool ext = a.window != 0 || a.block_mass != nullptr;  // sinks/window or mass records
+    std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u%s", f8 ? "fp8" : dt_name(a.kv_dtype),
+                  t.g, ext ? "_ext" : "");
     const hipModule_t mod = c->mod_tiles[f8 ? 2 : a.kv_dtype == EH_KV_F16 ? 0 : 1];
     const float scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;  // paged_attention.rs:286
     // per-wave V tiles (16 rows x kTilesVRow bytes) and staged q rows
@@ -378,18 +389,27 @@ eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const 
     const uint32_t lds = waves * (16 * kTilesVRow + kTilesQSeg * t.g * 128 * 4) + 4u * (2 * a.batch + 1);
     float* part_acc = (float*)a.ws;
     float* part_ml = part_acc + (uint64_t)(a.grid + a.batch) * a.n_head * 128;
+    const uint32_t rec_row = (uint32_t)mass_rec_row(a.bt_stride, a.block_tokens);
+    float* tile_rec = a.block_mass ? (float*)a.mass_ws : nullptr;
+    float* fin = a.block_mass ? tile_rec + 2ull * a.batch * rec_row * a.n_head : nullptr;
     eh_status st = launch_lds(c, mod, name, dim3((a.grid + runs_per_wg - 1) / runs_per_wg),
                               dim3(waves * 64), lds, stream, a.q,
                               (uint8_t*)a.pool, a.n_blocks, a.bt, a.bt_stride, a.lens, a.lens_add,
                               (const uint8_t*)a.new_k, (const uint8_t*)a.new_v, a.batch, a.out,
                               part_acc, part_ml, a.n_head, a.n_head_kv, a.block_tokens,
                               (uint32_t)log2_exact(a.block_tokens), scale_log2, a.grid, a.sink,
-                              a.window, a.k_scale, a.v_scale);
+                              a.window, tile_rec, fin, rec_row, a.k_scale, a.v_scale);
     if (st != EH_OK) return st;
-    return launch(c, mod, "eh_decode_tiles_merge",
-                  dim3((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch), dim3(256), stream,
+    st = launch(c, mod, "eh_decode_tiles_merge",
+                dim3((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch), dim3(256), stream,
                   (const float*)part_acc, (const float*)part_ml, a.out, a.lens, a.lens_add, a.batch,
-                  a.n_head, 128u, a.grid, a.sink, a.window);
+                  a.n_head, 128u, a.grid, a.sink, a.window, fin);
+    if (st != EH_OK || !a.block_mass) return st;
+    const uint64_t threads = (uint64_t)a.batch * a.bt_stride;
+    return launch(c, mod, "eh_decode_tiles_mass", dim3((uint32_t)div_ceil(threads, 256)), dim3(256),
+                  stream, (const float*)tile_rec, (const float*)fin, a.lens, a.lens_add, a.bt,
+                  a.bt_stride, a.batch, a.n_head, a.block_tokens, a.n_blocks, a.sink, a.window,
+                  rec_row, a.block_mass);
 }
 
 // Splits: aim for enough workgroups to fill 256 CUs several times over, with
@@ -1034,7 +1054,8 @@ static eh_status decode_tiles_entry(eh_context* c, eh_stream stream, uint32_t kv
                                     float* out, uint64_t out_bytes, uint32_t n_head,
                                     uint32_t n_head_kv, uint32_t head_dim, uint32_t block_tokens,
                                     uint32_t sink, uint32_t window, const float* k_scale,
-                                    const float* v_scale, uint32_t max_splits, void* ws,
+                                    const float* v_scale, float* block_mass,
+                                    uint64_t block_mass_bytes, uint32_t max_splits, void* ws,
                                     uint64_t ws_bytes) {
     if (!c) return fail(EH_INVALID_ARGS, "null context");
     if (n_head < 1) return invalid_size(1, n_head);
@@ -1055,8 +1076,13 @@ static eh_status decode_tiles_entry(eh_context* c, eh_stream stream, uint32_t kv
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
     const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * (f8 ? 1 : 2);
     if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
-    const uint64_t ws_need = tiles_ws_bytes(max_splits, batch, n_head);
+    const uint64_t ws_tiles = tiles_ws_bytes(max_splits, batch, n_head);
+    const uint64_t ws_need =
+        ws_tiles + (block_mass ? mass_ws_bytes(batch, bt_stride, block_tokens, n_head) : 0);
     if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
+    if (block_mass && block_mass_bytes < pool_bytes / page_bytes * 4)
+        return invalid_size(pool_bytes / page_bytes * 4, block_mass_bytes, "block_mass");
+    if (block_tokens % 16) return fail(EH_UNSUPPORTED, "block_tokens");
     eh_status st = bind(c);
     if (st) return st;
     tiles_args a{};
@@ -1079,6 +1105,8 @@ static eh_status decode_tiles_entry(eh_context* c, eh_stream stream, uint32_t kv
     a.v_scale = f8 ? v_scale : nullptr;
     a.sink = sink;
     a.window = window;
+    a.block_mass = block_mass;
+    a.mass_ws = block_mass ? (uint8_t*)ws + ws_tiles : nullptr;
     return run_tiles(c, stream, a, tc);
 }
 
@@ -1092,8 +1120,8 @@ eh_status eh_paged_decode_batched_e4m3(eh_context* c, eh_stream stream, const fl
                                        uint32_t max_splits, void* ws, uint64_t ws_bytes) {
     return decode_tiles_entry(c, stream, EH_KV_FP8, q, q_bytes, pool, pool_bytes, bt, bt_bytes,
                               bt_stride, ctx_lens, batch, out, out_bytes, n_head, n_head_kv,
-                              head_dim, block_tokens, 0, 0, k_scale, v_scale, max_splits, ws,
-                              ws_bytes);
+                              head_dim, block_tokens, 0, 0, k_scale, v_scale, nullptr, 0,
+                              max_splits, ws, ws_bytes);
 }
 
 eh_status eh_paged_decode_batched_window(eh_context* c, eh_stream stream, uint32_t kv_dtype,
@@ -1104,12 +1132,18 @@ eh_status eh_paged_decode_batched_window(eh_context* c, eh_stream stream, uint32
                                          uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
                                          uint32_t block_tokens, uint32_t sink_tokens,
                                          uint32_t window_tokens, const float* k_scale,
-                                         const float* v_scale, uint32_t max_splits, void* ws,
+                                         const float* v_scale, float* block_mass,
+                                         uint64_t block_mass_bytes, uint32_t max_splits, void* ws,
                                          uint64_t ws_bytes) {
     return decode_tiles_entry(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes,
                               bt_stride, ctx_lens, batch, out, out_bytes, n_head, n_head_kv,
                               head_dim, block_tokens, sink_tokens, window_tokens, k_scale, v_scale,
-                              max_splits, ws, ws_bytes);
+                              block_mass, block_mass_bytes, max_splits, ws, ws_bytes);
+}
+
+uint64_t eh_decode_mass_workspace_bytes(uint32_t batch, uint32_t bt_stride, uint32_t block_tokens,
+                                        uint32_t n_head) {
+    return mass_ws_bytes(batch, bt_stride, block_tokens, n_head);
 }
 
 eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l,

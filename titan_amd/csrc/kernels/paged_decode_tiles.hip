@@ -234,7 +234,9 @@ __device__ __forceinline__ u32x4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
 // sequence b attends (lens_add = 1 when lens are the positions of a fused
 // append).  Partials: slot w + b for workgroup w and sequence b,
 // part_acc [slots, n_head, 128], part_ml [slots, n_head, 2], slots = P + batch.
-template <int DT, int G, int DEPTH, int CHUNK>
+// EXT: the protected-sinks range and the per-tile attention-mass records are
+// compiled in (the plain instantiation keeps the hot loop free of them).
+template <int DT, int G, int DEPTH, int CHUNK, bool EXT>
 __device__ __forceinline__ void decode_tiles(
     const float* __restrict__ q, uint8_t* pool, uint64_t n_blocks,
     const uint32_t* __restrict__ bt, uint32_t bt_stride, const uint32_t* __restrict__ lens,
@@ -242,8 +244,8 @@ __device__ __forceinline__ void decode_tiles(
     uint32_t batch, float* __restrict__ out, float* __restrict__ part_acc,
     float* __restrict__ part_ml, uint32_t n_head, uint32_t n_head_kv,
     uint32_t block_tokens, uint32_t bt_shift, float scale_log2, uint32_t n_runs,
-    uint32_t sink, uint32_t window, const float* __restrict__ k_scale,
-    const float* __restrict__ v_scale) {
+    uint32_t sink, uint32_t window, float* __restrict__ tile_rec, float* __restrict__ fin,
+    uint32_t rec_row, const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
     constexpr int HD = 128;
     constexpr int KSTEPS = HD / 32;  // MFMA steps over head_dim
     // E4M3 pages are converted to f16 in registers (exact) and use the f16 path
@@ -284,7 +286,7 @@ __device__ __forceinline__ void decode_tiles(
         for (uint32_t base = 0; base < batch; base += 64) {
             const uint32_t j = base + lane;
             const uint32_t n = j < batch ? lens[j] + lens_add : 0u;
-            uint32_t t = make_span(n, sink, window).tiles;
+            uint32_t t = make_span(n, EXT ? sink : 0u, EXT ? window : 0u).tiles;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const uint32_t y = __shfl_up(t, o, 64);
@@ -330,7 +332,8 @@ __device__ __forceinline__ void decode_tiles(
             const uint32_t f = F0 + k;
             uint32_t b = b0;
             while (cum[b + 1] <= f) ++b;
-            const uint32_t page = (make_span(ntok[b], sink, window).tile(f - cum[b]) * TILE) >> bt_shift;
+            const uint32_t j = f - cum[b];
+            const uint32_t page = ((EXT && window ? make_span(ntok[b], sink, window).tile(j) : j) * TILE) >> bt_shift;
             if (page < bt_stride) {
                 const uint32_t p = bt[(uint64_t)b * bt_stride + page];
                 phys = (uint64_t)p < n_blocks ? p : 0xFFFFFFFFu;
@@ -421,7 +424,7 @@ __device__ __forceinline__ void decode_tiles(
             iss_c1 = uni(cum[iss_b + 1]);
         }
         const uint32_t ntk = uni(ntok[iss_b]);
-        const uint32_t tok0 = (window ? make_span(ntk, sink, window).tile(f - iss_c0) : f - iss_c0) * TILE;
+        const uint32_t tok0 = (EXT && window ? make_span(ntk, sink, window).tile(f - iss_c0) : f - iss_c0) * TILE;
         const uint32_t phys = uni((uint32_t)__builtin_amdgcn_readlane((int)pv, (int)(k & 63u)));
         const bool pok = phys != 0xFFFFFFFFu;
         physp[D] = phys;
@@ -491,6 +494,8 @@ __device__ __forceinline__ void decode_tiles(
             const uint32_t qh = kv * group + x;
             if (whole) {
                 const float inv = L > 0.0f ? vsc / L : 0.0f;
+                if (EXT && fin != nullptr && g == 0)
+                    reinterpret_cast<float2*>(fin)[(uint64_t)b * n_head + qh] = make_float2(m_own, L);
                 float* dst = out + ((uint64_t)b * n_head + qh) * HD + 4 * g;
 #pragma unroll
                 for (int db = 0; db < HD / 16; ++db)
@@ -518,8 +523,9 @@ __device__ __forceinline__ void decode_tiles(
         constexpr int D = decltype(Dc)::value;
         const uint32_t f = F0 + k;
         const uint32_t ntk = uni(ntok[cmp_b]);
-        const span sp = make_span(ntk, sink, window);
-        const uint32_t tok0 = (window ? sp.tile(f - cmp_c0) : f - cmp_c0) * TILE;
+        const bool win = EXT && window != 0u;
+        const span sp = make_span(ntk, win ? sink : 0u, win ? window : 0u);
+        const uint32_t tok0 = (win ? sp.tile(f - cmp_c0) : f - cmp_c0) * TILE;
         const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
         const uint32_t phys = physp[D];
         if (phys == 0xFFFFFFFFu) return;  // masked page: its tokens do not count (uniform)
@@ -556,10 +562,10 @@ __device__ __forceinline__ void decode_tiles(
             s = K::mma(a, qa[st], s);
             s = K::mma(a, qb[st], s);
         }
-        if (window ? sp.partial(tok0) : nvalid < (uint32_t)TILE) {  // uniform
+        if (win ? sp.partial(tok0) : nvalid < (uint32_t)TILE) {  // uniform
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const bool ok = window ? sp.valid(tok0 + 4 * g + r) : 4 * g + r < nvalid;
+                const bool ok = win ? sp.valid(tok0 + 4 * g + r) : 4 * g + r < nvalid;
                 s[r] = ok ? s[r] : -__builtin_inff();
             }
         }
@@ -595,6 +601,15 @@ __device__ __forceinline__ void decode_tiles(
         const float p0 = fast_exp2(s[0] - m_own), p1 = fast_exp2(s[1] - m_own);
         const float p2 = fast_exp2(s[2] - m_own), p3 = fast_exp2(s[3] - m_own);
         l_own += (p0 + p1) + (p2 + p3);
+        if (EXT && tile_rec != nullptr) {  // uniform: this tile's weight sum per head, relative to m_own
+            float e = (p0 + p1) + (p2 + p3);
+            e += __shfl_xor(e, 16, 64);
+            e += __shfl_xor(e, 32, 64);
+            const uint32_t a = tok0 / TILE;
+            if (g == 0 && hv && a < rec_row)
+                reinterpret_cast<float2*>(tile_rec)[((uint64_t)cmp_b * rec_row + a) * n_head +
+                                                    kv * group + x] = make_float2(e, m_own);
+        }
         // P^T operand (tokens 4g..4g+3 of head x) straight from the scores
         const uint64_t ph = (uint64_t)pack2<CT>(p0, p1) | ((uint64_t)pack2<CT>(p2, p3) << 32);
         uint64_t plo = 0;
@@ -668,7 +683,7 @@ __device__ __forceinline__ void decode_tiles(
 extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
     const uint32_t* __restrict__ lens, uint32_t lens_add, uint32_t batch, uint32_t n_head,
-    uint32_t head_dim, uint32_t P, uint32_t sink, uint32_t window) {
+    uint32_t head_dim, uint32_t P, uint32_t sink, uint32_t window, float* __restrict__ fin) {
     constexpr int NB = 16;
     __shared__ float sM[4][64], sL[4][64], sA[4][64];
     const uint32_t b = blockIdx.y;
@@ -745,24 +760,64 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
         Acc = fmaf(sA[u][lane], fw, Acc);
     }
     out[orow] = L > 0.0f ? Acc / L : 0.0f;
+    if (fin != nullptr && d == 0) reinterpret_cast<float2*>(fin)[(uint64_t)b * n_head + qh] = make_float2(Mx, L);
+}
+
+// H2O attention mass of one decode call (the score StreamingKvManager::
+// record_attention_mass adds per block, engine-kvcache/src/streaming.rs:
+// 135-141): block_mass[page] += the softmax weights of the page's attended
+// tokens summed over the q heads, from the decode kernel's per-tile records
+// (weight sum e relative to the running max m) and each head's final (M, L):
+// e * 2^(m - M) / L.  One thread per (sequence, block-table entry); pages
+// shared by several sequences receive one atomic add from each.
+extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_mass(
+    const float* __restrict__ tile_rec, const float* __restrict__ fin,
+    const uint32_t* __restrict__ lens, uint32_t lens_add, const uint32_t* __restrict__ bt,
+    uint32_t bt_stride, uint32_t batch, uint32_t n_head, uint32_t block_tokens, uint64_t n_blocks,
+    uint32_t sink, uint32_t window, uint32_t rec_row, float* __restrict__ block_mass) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)batch * bt_stride) return;
+    const uint32_t b = (uint32_t)(i / bt_stride), p = (uint32_t)(i % bt_stride);
+    const uint32_t phys = bt[i];
+    if ((uint64_t)phys >= n_blocks) return;  // masked page: never attended
+    const span sp = make_span(lens[b] + lens_add, sink, window);
+    const uint32_t full = sp.n / TILE + (sp.n % TILE != 0u);
+    const uint32_t tpp = block_tokens / TILE;
+    const float2* rec = reinterpret_cast<const float2*>(tile_rec);
+    const float2* fl = reinterpret_cast<const float2*>(fin) + (uint64_t)b * n_head;
+    float total = 0.0f;
+    for (uint32_t a = p * tpp; a < (p + 1) * tpp && a < full && a < rec_row; ++a) {
+        if (!(a < sp.st || a >= sp.st + sp.gap)) continue;  // tile outside the attended range
+        const float2* r = rec + ((uint64_t)b * rec_row + a) * n_head;
+        for (uint32_t h = 0; h < n_head; ++h) {
+            const float2 f = fl[h];
+            if (f.y > 0.0f) total += r[h].x * exp2f(r[h].y - f.x) / f.y;
+        }
+    }
+    if (total > 0.0f) atomicAdd(block_mass + phys, total);
 }
 
 // One wave per kv head; at most 8 waves per workgroup; two waves per SIMD
 // (256 VGPRs, no AGPR copies, which would wait for the loads they copy); 2
 // tiles in flight per wave (measured faster than 4: deeper queues slow the
 // random page reads).
-#define EH_TILES(DTN, DT, G)                                                                        \
-    extern "C" __global__ __launch_bounds__(512, 1) void eh_decode_tiles_##DTN##_hd128_g##G(     \
+#define EH_TILES_ONE(NAME, DT, G, EXT)                                                              \
+    extern "C" __global__ __launch_bounds__(512, 1) void NAME(                                     \
         const float* q, uint8_t* pool, uint64_t n_blocks, const uint32_t* bt, uint32_t bt_stride,  \
         const uint32_t* lens, uint32_t lens_add, const uint8_t* new_k, const uint8_t* new_v,       \
         uint32_t batch, float* out, float* part_acc, float* part_ml, uint32_t n_head,              \
         uint32_t n_head_kv, uint32_t block_tokens, uint32_t bt_shift, float scale_log2,            \
-        uint32_t n_runs, uint32_t sink, uint32_t window, const float* k_scale,                     \
-        const float* v_scale) {                                                                    \
-        decode_tiles<DT, G, 2, 16>(q, pool, n_blocks, bt, bt_stride, lens, lens_add, new_k, new_v, \
-                                   batch, out, part_acc, part_ml, n_head, n_head_kv, block_tokens, \
-                                   bt_shift, scale_log2, n_runs, sink, window, k_scale, v_scale);  \
+        uint32_t n_runs, uint32_t sink, uint32_t window, float* tile_rec, float* fin,              \
+        uint32_t rec_row, const float* k_scale, const float* v_scale) {                            \
+        decode_tiles<DT, G, 2, 16, EXT>(q, pool, n_blocks, bt, bt_stride, lens, lens_add, new_k,   \
+                                        new_v, batch, out, part_acc, part_ml, n_head, n_head_kv,   \
+                                        block_tokens, bt_shift, scale_log2, n_runs, sink, window,  \
+                                        tile_rec, fin, rec_row, k_scale, v_scale);                 \
     }
+// _ext: with the protected-sinks range and attention-mass records
+#define EH_TILES(DTN, DT, G)                                                       \
+    EH_TILES_ONE(eh_decode_tiles_##DTN##_hd128_g##G, DT, G, false)                \
+    EH_TILES_ONE(eh_decode_tiles_##DTN##_hd128_g##G##_ext, DT, G, true)
 
 #define EH_TILES_ALL(DTN, DT) \
     EH_TILES(DTN, DT, 1)      \

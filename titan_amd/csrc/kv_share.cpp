@@ -368,6 +368,14 @@ void eh_stream_record_attention_mass(eh_stream_mgr* m, uint32_t block, float mas
     m->scores[block] += mass;
 }
 
+// record_attention_mass(i, masses[i]) for every i < n with a non-zero mass:
+// the per-page masses a decode launch accumulated (eh_paged_decode_batched_window's
+// block_mass, copied to the host) in one call.
+void eh_stream_record_attention_masses(eh_stream_mgr* m, const float* masses, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i)
+        if (masses[i] != 0.0f) eh_stream_record_attention_mass(m, (uint32_t)i, masses[i]);
+}
+
 uint64_t eh_stream_scores_len(const eh_stream_mgr* m) { return m->scores.size(); }
 
 float eh_stream_score(const eh_stream_mgr* m, uint32_t block) {

@@ -118,12 +118,22 @@ class PagedAttention:
             buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv), int(head_dim),
             int(block_tokens), buf(k_scale)[0], buf(v_scale)[0], int(plan[1]), wp, wb))
 
+    @staticmethod
+    def mass_workspace_bytes(batch, bt_stride, block_tokens, n_head):
+        """Extra workspace decode_batched_window needs when it accumulates block_mass."""
+        return int(_lib.load().eh_decode_mass_workspace_bytes(int(batch), int(bt_stride),
+                                                               int(block_tokens), int(n_head)))
+
     def decode_batched_window(self, stream, q, pool, block_tables, ctx_lens, out, n_head,
                               n_head_kv, head_dim, block_tokens, kv_dtype, sink_tokens,
-                              window_tokens, plan, workspace, k_scale=None, v_scale=None):
+                              window_tokens, plan, workspace, k_scale=None, v_scale=None,
+                              block_mass=None):
         """decode_batched over the protected-sinks range: the query at
         pos = ctx_lens[b] - 1 attends [0, sink) and [max(sink, pos - window), pos]
-        (window 0: every token).  E4M3 pools pass k_scale / v_scale."""
+        (window 0: every token).  E4M3 pools pass k_scale / v_scale.  With
+        block_mass ([pages] f32) each page's attention mass summed over q heads
+        is added to it (the H2O score of record_attention_mass); the workspace
+        then needs plan[2] + mass_workspace_bytes(...) bytes."""
         batch, stride = block_tables.shape
         qp, qb = buf(q)
         pp, pb = buf(pool)
@@ -134,7 +144,7 @@ class PagedAttention:
             self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
             int(stride), buf(ctx_lens)[0], int(batch), op, ob, int(n_head), int(n_head_kv),
             int(head_dim), int(block_tokens), int(sink_tokens), int(window_tokens),
-            buf(k_scale)[0], buf(v_scale)[0], int(plan[1]), wp, wb))
+            buf(k_scale)[0], buf(v_scale)[0], *buf(block_mass), int(plan[1]), wp, wb))
 
     def append_decode_batched(self, stream, layout, pool, keys, values, block_tables, start_pos,
                               q, out, n_head, head_dim, plan, workspace):

@@ -182,6 +182,12 @@ class StreamingKvManager:
     def record_attention_mass(self, block_id, mass):
         self._L.eh_stream_record_attention_mass(self._h, int(block_id), float(mass))
 
+    def record_attention_masses(self, masses):
+        """record_attention_mass(i, masses[i]) for every non-zero entry: the
+        per-page masses a decode launch accumulated (block_mass), on the host."""
+        m = np.ascontiguousarray(masses, dtype=np.float32)
+        self._L.eh_stream_record_attention_masses(self._h, _p(m), m.size)
+
     @property
     def block_scores(self):
         n = self._L.eh_stream_scores_len(self._h)
