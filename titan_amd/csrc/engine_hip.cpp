@@ -466,18 +466,19 @@ struct prefill_args {
     uint32_t n_head, n_head_kv, head_dim, block_tokens;
 };
 
-// One launch: grid (128-row tiles, kv heads, sequences) of 256 threads.
+constexpr uint32_t kPrefillRows = 256;  // query rows per workgroup (8 waves x 32), mirrors ROWS
+// One launch: grid (256-row tiles, kv heads, sequences) of 512 threads.
 eh_status run_prefill(eh_context* c, eh_stream stream, const prefill_args& a) {
     char name[48];
     std::snprintf(name, sizeof name, "eh_prefill_%s_hd%u", dt_name(a.kv_dtype), a.head_dim);
     const uint32_t group = a.n_head / a.n_head_kv;
-    const uint64_t tiles = div_ceil((uint64_t)a.max_q * group, 128);
+    const uint64_t tiles = div_ceil((uint64_t)a.max_q * group, kPrefillRows);
     if (tiles > 0x7FFFFFFFull) return invalid_size(0x7FFFFFFFull, tiles, "row tiles");
     const float scale = 1.0f / std::sqrt((float)a.head_dim);  // flash_attention.rs:166
     const float scale_log2 = scale * 1.4426950408889634f;
     const uint32_t row_bytes = a.n_head_kv * a.head_dim * (uint32_t)elt_bytes(a.kv_dtype);
     return launch(c, c->mod_prefill, name, dim3((uint32_t)tiles, a.n_head_kv, a.batch),
-                  dim3(256), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
+                  dim3(2 * kPrefillRows), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
                   a.bt_entries, a.cu_q, a.start_pos, a.pos_ptr, a.q_tokens, a.pos_offset, a.out,
                   a.n_head, a.n_head_kv, a.block_tokens, log2_exact(a.block_tokens), row_bytes,
                   scale_log2, a.n_blocks);

@@ -10,7 +10,7 @@
 //
 // Work decomposition (MI355X-first; the reference runs one warp per
 // (q head, query) and re-reads K/V for each):
-//   * one workgroup of 4 waves per (128-row tile, kv head, sequence); the
+//   * one workgroup of 8 waves per (256-row tile, kv head, sequence); the
 //     rows of a tile are (query token, q head of the GQA group) pairs, so one
 //     K/V tile in LDS serves every q head of the group;
 //   * K/V tiles of N keys are gathered through the block table into LDS,
@@ -39,7 +39,9 @@ namespace {
 
 enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 
-constexpr int NT = 256;           // threads per workgroup (4 waves)
+constexpr int NT = 512;           // threads per workgroup (8 waves)
+constexpr int NL = 256;           // threads (waves 0-3) that stage the K/V tiles
+constexpr uint32_t ROWS = NT / 2;  // query rows per workgroup: 32 per wave
 constexpr uint32_t SLICE = 1024;  // block-table entries staged in LDS at once
 constexpr float RESCALE_LOG2 = 8.0f;
 
@@ -98,13 +100,13 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint3
 }
 
 // Geometry per (type, head_dim): one load item = 4 consecutive keys x 16
-// bytes of a head row; N keys per tile so that the 256 threads own one item.
+// bytes of a head row; N keys per tile so that the NL staging threads own one item each.
 template <int DT, int HD>
 struct geo {
     static constexpr int ELT = op_t<DT>::ELT;
     static constexpr int EPC = 16 / ELT;          // elements per 16-byte chunk
     static constexpr int PARTS = HD / EPC;        // chunks per head row
-    static constexpr int N = 4 * NT / PARTS;      // keys per tile
+    static constexpr int N = 4 * NL / PARTS;      // keys per tile
     static constexpr int SUB = N / 32;            // 32-key sub-blocks per tile
     static constexpr int KPITCH = HD * ELT + 16;  // bytes per K row in LDS
     static constexpr int VPITCH = N * ELT + (ELT == 4 ? 16 : 8);  // bytes per V^T row
@@ -163,7 +165,7 @@ __device__ __forceinline__ void prefill(
     }
     const uint32_t group = n_head / n_head_kv;
     const uint32_t rows = n_q * group;
-    const uint32_t row0 = tile * 128u;
+    const uint32_t row0 = tile * ROWS;
     if (row0 >= rows) return;  // uniform over the workgroup
 
     const int tid = threadIdx.x;
@@ -192,14 +194,14 @@ __device__ __forceinline__ void prefill(
     const uint32_t wr1 = min(row0 + wave * 32u + 31u, rows - 1u);
     const uint32_t wave_min = clamp_pos(wr0 / group);
     const uint32_t wave_max = clamp_pos(wr1 / group);
-    const uint32_t kmax = clamp_pos(min(row0 + 127u, rows - 1u) / group);  // workgroup bound
+    const uint32_t kmax = clamp_pos(min(row0 + ROWS - 1u, rows - 1u) / group);  // workgroup bound
     const uint32_t n_tiles = kmax / N + 1u;
 
     // ---- LDS carve-up
     lds_hdr* hdr = reinterpret_cast<lds_hdr*>(smem);
     uint32_t* slice = reinterpret_cast<uint32_t*>(smem + 64);
     uint8_t* kflag = smem + 64 + SLICE * 4;                 // [2][N] key valid bytes
-    uint8_t* stage = smem + 64 + SLICE * 4 + 2 * 128;       // [2][STAGE]
+    uint8_t* stage = smem + 64 + SLICE * 4 + 2 * N;         // [2][STAGE]
 
     auto entry_of = [&](uint32_t key) -> uint32_t {
         return bt_shift >= 0 ? (key >> bt_shift) : key / block_tokens;
@@ -316,7 +318,7 @@ __device__ __forceinline__ void prefill(
             uint32_t f = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) f |= ((okbits >> j) & 1u) << (8 * j);
-            *reinterpret_cast<uint32_t*>(kflag + buf * 128 + 4 * kg) = f;
+            *reinterpret_cast<uint32_t*>(kflag + buf * N + 4 * kg) = f;
         }
         if (okbits >> 4) hdr->tile_bad[buf] = t;
     };
@@ -359,11 +361,12 @@ __device__ __forceinline__ void prefill(
     if (tid == 0) { hdr->tile_bad[0] = 0xFFFFFFFFu; hdr->tile_bad[1] = 0xFFFFFFFFu; }
     stage_slice(0);
     __syncthreads();
-    issue(0);
+    const bool loader = tid < NL;  // uniform per wave
+    if (loader) issue(0);
 
     for (uint32_t j = 0; j < n_tiles; ++j) {
         const int buf = j & 1;
-        commit(j, buf);
+        if (loader) commit(j, buf);
         if (j + 1 < n_tiles) {
             const uint32_t e_last = entry_of((j + 1) * N + N - 1);
             if (e_last >= hdr->slice_base + SLICE) {  // uniform
@@ -372,7 +375,7 @@ __device__ __forceinline__ void prefill(
             }
         }
         __syncthreads();
-        if (j + 1 < n_tiles) issue(j + 1);
+        if (loader && j + 1 < n_tiles) issue(j + 1);
 
         const uint8_t* ks = stage + buf * Gm::STAGE;
         const uint8_t* vs = ks + Gm::KBYTES;
@@ -403,7 +406,7 @@ __device__ __forceinline__ void prefill(
             }
             // causal / page mask; key of register r: kb + 8(r/4) + 4h + r%4
             if (bad || kb + 31u > wave_min) {
-                const uint8_t* fl = kflag + buf * 128 + sb * 32;
+                const uint8_t* fl = kflag + buf * N + sb * 32;
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
                     const int ko = 8 * g4 + 4 * h;
@@ -497,13 +500,13 @@ __device__ __forceinline__ void prefill(
 }  // namespace
 
 #define EH_PREFILL(DTN, DT, HD)                                                                   \
-    extern "C" __global__ __launch_bounds__(NT, 2) void eh_prefill_##DTN##_hd##HD(              \
+    extern "C" __global__ __launch_bounds__(NT, 1) void eh_prefill_##DTN##_hd##HD(              \
         const float* q, const uint8_t* pool, const uint32_t* bt, uint32_t bt_stride,             \
         uint32_t bt_entries, const uint32_t* cu_q, const uint32_t* start_pos,                    \
         const uint32_t* pos_ptr, uint32_t q_tokens, uint32_t pos_offset, float* out,             \
         uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens, int bt_shift,                \
         uint32_t row_bytes, float scale_log2, uint64_t n_blocks) {                               \
-        constexpr int BYTES = 64 + SLICE * 4 + 2 * 128 + 2 * geo<DT, HD>::STAGE;                 \
+        constexpr int BYTES = 64 + SLICE * 4 + 2 * geo<DT, HD>::N + 2 * geo<DT, HD>::STAGE;      \
         __shared__ __attribute__((aligned(16))) uint8_t smem[BYTES];                             \
         prefill<DT, HD>(q, pool, bt, bt_stride, bt_entries, cu_q, start_pos, pos_ptr, q_tokens,  \
                         pos_offset, out, n_head, n_head_kv, block_tokens, bt_shift, row_bytes,   \
