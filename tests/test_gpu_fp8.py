@@ -211,3 +211,36 @@ def test_e4m3_entry_rejects_other_paths(dev):
         PagedAttention.plan(4, 12, 2, 128, 16, 100, 64, KvDataType.FP8)   # fixed splits
     with pytest.raises(HipError):
         PagedAttention.plan(4, 12, 2, 64, 16, 100, 0, KvDataType.FP8)     # head_dim 64
+
+
+def test_e4m3_entry_errors(dev):
+    """Null scales, short buffers and non-FP8 layouts are rejected before any launch."""
+    from titan_amd import HipError, KvCacheError
+    n_kv, hd, bt, nb = 2, 128, 16, 4
+    rl = n_kv * hd
+    pool = torch.zeros(nb * bt * 2 * rl, dtype=torch.uint8, device=dev)
+    lay = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
+    keys = torch.zeros((3, rl), device=dev)
+    tab = torch.zeros((1, nb), dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 3], dtype=torch.int32, device=dev)
+    st = torch.zeros(1, dtype=torch.int32, device=dev)
+    sc = torch.ones(n_kv, device=dev)
+    pk = PagedKvGpu(0)
+    with pytest.raises(HipError):       # keys shorter than total_tokens rows
+        pk.append_kv_e4m3_batched(None, lay, pool, keys, keys, tab, cu, st, 4, hd, sc, sc)
+    with pytest.raises(HipError):       # a 16-bit layout
+        pk.append_kv_e4m3_batched(None, PagedKvLayout(nb, bt, rl, KvDataType.F16), pool, keys,
+                                  keys, tab, cu, st, 3, hd, sc, sc)
+    with pytest.raises((HipError, KvCacheError)):   # null scale arrays
+        pk.append_kv_e4m3_batched(None, lay, pool, keys, keys, tab, cu, st, 3, hd, None, None)
+    plan = PagedAttention.plan(1, 12, n_kv, hd, bt, 64, 0, KvDataType.FP8)
+    q = torch.zeros((1, 12, hd), device=dev)
+    out = torch.empty_like(q)
+    lens = torch.tensor([20], dtype=torch.int32, device=dev)
+    ws = PagedAttention.workspace(plan)
+    with pytest.raises((HipError, KvCacheError)):
+        PagedAttention(0).decode_batched_e4m3(None, q, pool, tab, lens, out, 12, n_kv, hd, bt,
+                                              None, None, plan, ws)
+    with pytest.raises(HipError):       # E4M3 pools only through the scale-aware entries
+        PagedAttention(0).decode_batched(None, q, pool, tab, lens, out, 12, n_kv, hd, bt,
+                                         KvDataType.FP8, plan, ws)

@@ -213,3 +213,29 @@ def test_h2o_scores_drive_prune_like_oracle(dev):
         assert kept == rkept                      # sinks, heavy hitters by score, recent
         assert sorted(evicted) == sorted(revicted)
         assert sorted(kept[4:7]) == sorted(int(tab[b, j]) for j in heavy[b])
+
+
+def test_window_mass_buffer_checks(dev):
+    """block_mass shorter than the pool's pages, or a workspace without the
+    mass scratch, is rejected; without block_mass the plan's workspace suffices."""
+    from titan_amd import HipError
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rng = np.random.default_rng(1)
+    lens = np.array([40, 7], np.int64)
+    tab, nb = make_tables(rng, lens, bt)
+    pool = torch.zeros(nb * bt * 2 * n_kv * hd, dtype=torch.float16, device=dev)
+    q = torch.zeros((2, n_head, hd), device=dev)
+    out = torch.empty_like(q)
+    plan = PagedAttention.plan(2, n_head, n_kv, hd, bt, 64, 0, KvDataType.F16)
+    pa = PagedAttention(0)
+    args = (None, q, pool, i32(tab, dev), i32(lens, dev), out, n_head, n_kv, hd, bt,
+            KvDataType.F16, 4, 16, plan)
+    with pytest.raises(HipError):
+        pa.decode_batched_window(*args, PagedAttention.workspace(plan),
+                                 block_mass=torch.zeros(nb - 1, device=dev))
+    with pytest.raises(HipError):
+        pa.decode_batched_window(*args, PagedAttention.workspace(plan),
+                                 block_mass=torch.zeros(nb, device=dev))
+    pa.decode_batched_window(*args, PagedAttention.workspace(plan))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
