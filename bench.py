@@ -372,7 +372,18 @@ def suite(args, dev):
           "mfma_frac_of_2.5PF": round(flops / us_p3 / 1e6 / 2500.0, 4),
           "append_us": round(us_a3, 2),
           "append_GB/s": round(T3 * 2 * s3.row_len * 2 * 2 / us_a3 / 1e3, 1)})
-    del pool3, k3, v3, q3, o3
+    # config 3's prefill over E4M3 pages (per-kv-head scales)
+    lay3e = PagedKvLayout(s3.n_blocks, 16, s3.row_len, KvDataType.FP8)
+    pool3e = torch.randint(0, 0x7E, (lay3e.floats_total(),), generator=gen, device=dev,
+                           dtype=torch.uint8)
+    sc3 = torch.full((8,), 0.01, device=dev)
+    us_p3e = graph_time_us(lambda st: fa.launch_batched_e4m3(st, q3, pool3e, dtab3, cu3, sp3, o3,
+                                                             32, 8, 128, 16, 512, sc3, sc3), 5, 4)
+    emit({"config": 3, "what": "chunked prefill (causal, MFMA) over E4M3 pages (fp8 KV, per-kv-head "
+          "scales), B=8, 512 on 2048, 32/8 heads, hd 128", "prefill_us": round(us_p3e, 2),
+          "flop": flops, "TFLOP/s": round(flops / us_p3e / 1e6, 1),
+          "mfma_frac_of_2.5PF": round(flops / us_p3e / 1e6 / 2500.0, 4)})
+    del pool3, pool3e, k3, v3, q3, o3
 
     # ---- config 4: prefix-shared CoW + eviction + compaction (page moves on the GPU)
     from titan_amd.prefix_share import PrefixShareScenario, run_on_gpu

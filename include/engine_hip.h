@@ -314,6 +314,20 @@ eh_status eh_prefill_batched(eh_context* ctx, eh_stream stream, uint32_t kv_dtyp
                              float* out, uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
                              uint32_t head_dim, uint32_t block_tokens);
 
+/* ---- Batched chunked prefill over an E4M3 pool (extension; format and
+ * scales as eh_append_kv_e4m3_batched): eh_prefill_batched's semantics on the
+ * dequantised pool, decode(code) * scale.  Codes are widened to f16 (exact)
+ * as the tiles are staged and take the f16 MFMA path; head_dim 64 or 128. */
+eh_status eh_prefill_batched_e4m3(eh_context* ctx, eh_stream stream, const float* q,
+                                  uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                                  const uint32_t* block_tables, uint64_t bt_bytes,
+                                  uint32_t bt_stride, const uint32_t* cu_q,
+                                  const uint32_t* start_pos, uint32_t batch, uint32_t max_q_tokens,
+                                  uint32_t total_q_tokens, float* out, uint64_t out_bytes,
+                                  uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
+                                  uint32_t block_tokens, const float* k_scale,
+                                  const float* v_scale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -251,3 +251,58 @@ def test_validation_errors(dev):
     assert e.value.kind == "Unsupported"
     # zero tokens is a no-op success
     fa.launch(None, q, pool, table, out, 8, 2, 128, 16, 0, 0)
+
+
+@pytest.mark.parametrize("hd,nh,nkv", [(128, 16, 4), (64, 8, 8), (128, 32, 8)])
+def test_batched_ragged_chunks_e4m3(dev, hd, nh, nkv):
+    """Chunked prefill over an E4M3 pool (per-kv-head scales) against the
+    oracle's causal attention on the dequantised pool, decode(code) * scale."""
+    bt = 16
+    rng = np.random.default_rng(23 + hd + nh)
+    starts = [0, 5, 130, 1000]
+    lens = [33, 1, 200, 64]
+    stride = max(-(-(s + n) // bt) for s, n in zip(starts, lens)) + 2
+    n_pages = sum(-(-(s + n) // bt) for s, n in zip(starts, lens)) + 3
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    tables = np.full((len(starts), stride), 0xFFFFFFFF, np.uint32)
+    o = 0
+    for b, (s, n) in enumerate(zip(starts, lens)):
+        k = -(-(s + n) // bt)
+        tables[b, :k] = perm[o:o + k]
+        o += k
+    codes = rng.integers(0, 256, n_pages * bt * 2 * nkv * hd).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C
+    ks = rng.uniform(0.002, 0.05, nkv).astype(np.float32)
+    vs = rng.uniform(0.002, 0.05, nkv).astype(np.float32)
+    f = orc.e4m3_to_f32(codes).reshape(n_pages, bt, 2, nkv, hd)
+    f[:, :, 0] *= ks[None, None, :, None]
+    f[:, :, 1] *= vs[None, None, :, None]
+    hpool = f.reshape(-1)
+    total = sum(lens)
+    q = rng.standard_normal((total, nh, hd)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    out = torch.full((total, nh, hd), float("nan"), device=dev)
+    FlashAttention2(0).launch_batched_e4m3(None, torch.from_numpy(q).to(dev),
+                                           torch.from_numpy(codes).to(dev), i32(tables, dev),
+                                           i32(cu, dev), i32(np.array(starts, np.uint32), dev), out,
+                                           nh, nkv, hd, bt, max(lens), torch.from_numpy(ks).to(dev),
+                                           torch.from_numpy(vs).to(dev))
+    torch.cuda.synchronize()
+    g = out.cpu().numpy()
+    for b, (s, n) in enumerate(zip(starts, lens)):
+        k = -(-(s + n) // bt)
+        ref = orc.prefill_causal(hpool, tables[b, :k], bt, q[cu[b]:cu[b + 1]], n, s, nh, nkv, hd)
+        check_close(g[cu[b]:cu[b + 1]], ref, KvDataType.F16, f"seq {b}")
+
+
+def test_e4m3_prefill_rejects_other_entries(dev):
+    """An E4M3 pool goes through the scale-aware prefill only."""
+    pool = torch.zeros(4 * 16 * 2 * 256, dtype=torch.uint8, device=dev)
+    q = torch.zeros((4, 8, 128), device=dev)
+    out = torch.empty_like(q)
+    tab = torch.zeros((1, 4), dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 4], dtype=torch.int32, device=dev)
+    st = torch.zeros(1, dtype=torch.int32, device=dev)
+    with pytest.raises(HipError):
+        FlashAttention2(0).launch_batched(None, q, pool, tab, cu, st, out, 8, 2, 128, 16, 4,
+                                          kv_dtype=KvDataType.FP8)

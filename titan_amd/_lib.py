@@ -64,6 +64,8 @@ _SIGS = {
                                        u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp, u64]),
     "eh_flash_attention_prefill": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64,
                                          u64, u64, u64, u64, vp]),
+    "eh_prefill_batched_e4m3": (i32, [vp, vp, vp, u64, vp, u64, vp, u64, u32, vp, vp, u32, u32, u32,
+                                      vp, u64, u32, u32, u32, u32, vp, vp]),
     "eh_prefill_batched": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, vp, u32, u32, u32,
                                  vp, u64, u32, u32, u32, u32]),
     # host bookkeeping (kv_host.h)

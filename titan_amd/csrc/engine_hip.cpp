@@ -464,13 +464,16 @@ struct prefill_args {
     uint32_t q_tokens, pos_offset, batch, max_q;
     float* out;
     uint32_t n_head, n_head_kv, head_dim, block_tokens;
+    const float* k_scale;  // E4M3 pages only
+    const float* v_scale;
 };
 
 constexpr uint32_t kPrefillRows = 256;  // query rows per workgroup (8 waves x 32), mirrors ROWS
 // One launch: grid (256-row tiles, kv heads, sequences) of 512 threads.
 eh_status run_prefill(eh_context* c, eh_stream stream, const prefill_args& a) {
     char name[48];
-    std::snprintf(name, sizeof name, "eh_prefill_%s_hd%u", dt_name(a.kv_dtype), a.head_dim);
+    std::snprintf(name, sizeof name, "eh_prefill_%s_hd%u",
+                  a.kv_dtype == EH_KV_FP8 ? "fp8" : dt_name(a.kv_dtype), a.head_dim);
     const uint32_t group = a.n_head / a.n_head_kv;
     const uint64_t tiles = div_ceil((uint64_t)a.max_q * group, kPrefillRows);
     if (tiles > 0x7FFFFFFFull) return invalid_size(0x7FFFFFFFull, tiles, "row tiles");
@@ -481,14 +484,15 @@ eh_status run_prefill(eh_context* c, eh_stream stream, const prefill_args& a) {
                   dim3(2 * kPrefillRows), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
                   a.bt_entries, a.cu_q, a.start_pos, a.pos_ptr, a.q_tokens, a.pos_offset, a.out,
                   a.n_head, a.n_head_kv, a.block_tokens, log2_exact(a.block_tokens), row_bytes,
-                  scale_log2, a.n_blocks);
+                  scale_log2, a.n_blocks, a.k_scale, a.v_scale);
 }
 
 // Shape checks shared by the prefill entry points (beyond the reference's
 // size checks, which come first): the kernel set and a pool of >= 1 page.
 eh_status validate_prefill_shape(uint32_t kv_dtype, uint64_t n_head, uint64_t n_head_kv,
-                                 uint64_t head_dim, uint64_t block_tokens, uint64_t pool_bytes) {
-    if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
+                                 uint64_t head_dim, uint64_t block_tokens, uint64_t pool_bytes,
+                                 bool e4m3 = false) {
+    if (e4m3 ? kv_dtype != EH_KV_FP8 : !dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
     if (!prefill_hd(head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 128, head_dim);
     const uint64_t page_bytes = block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
     if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
@@ -1250,13 +1254,16 @@ eh_status eh_flash_attention_prefill(eh_context* c, eh_stream stream, uint32_t k
     return run_prefill(c, stream, a);
 }
 
-eh_status eh_prefill_batched(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
-                             uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
-                             const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
-                             const uint32_t* cu_q, const uint32_t* start_pos, uint32_t batch,
-                             uint32_t max_q_tokens, uint32_t total_q_tokens, float* out,
-                             uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
-                             uint32_t head_dim, uint32_t block_tokens) {
+static eh_status prefill_batched_body(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                      const float* q, uint64_t q_bytes, const void* pool,
+                                      uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes,
+                                      uint32_t bt_stride, const uint32_t* cu_q,
+                                      const uint32_t* start_pos, uint32_t batch,
+                                      uint32_t max_q_tokens, uint32_t total_q_tokens, float* out,
+                                      uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                                      uint32_t head_dim, uint32_t block_tokens,
+                                      const float* k_scale, const float* v_scale) {
+    const bool e4m3 = k_scale != nullptr;
     if (!c) return fail(EH_INVALID_ARGS, "null context");
     if (n_head < 1) return invalid_size(1, n_head);
     if (n_head_kv < 1) return invalid_size(1, n_head_kv);
@@ -1269,7 +1276,7 @@ eh_status eh_prefill_batched(eh_context* c, eh_stream stream, uint32_t kv_dtype,
     const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
     eh_status st = validate_prefill_shape(kv_dtype, n_head, n_head_kv, head_dim, block_tokens,
-                                          pool_bytes);
+                                          pool_bytes, e4m3);
     if (st) return st;
     if (batch == 0 || total_q_tokens == 0 || max_q_tokens == 0) return EH_OK;
     if (!cu_q || !start_pos) return fail(EH_INVALID_ARGS, "cu_q / start_pos is null");
@@ -1293,7 +1300,37 @@ eh_status eh_prefill_batched(eh_context* c, eh_stream stream, uint32_t kv_dtype,
     a.n_head_kv = n_head_kv;
     a.head_dim = head_dim;
     a.block_tokens = block_tokens;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
     return run_prefill(c, stream, a);
+}
+
+eh_status eh_prefill_batched(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
+                             uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                             const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                             const uint32_t* cu_q, const uint32_t* start_pos, uint32_t batch,
+                             uint32_t max_q_tokens, uint32_t total_q_tokens, float* out,
+                             uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                             uint32_t head_dim, uint32_t block_tokens) {
+    return prefill_batched_body(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes,
+                                bt_stride, cu_q, start_pos, batch, max_q_tokens, total_q_tokens,
+                                out, out_bytes, n_head, n_head_kv, head_dim, block_tokens, nullptr,
+                                nullptr);
+}
+
+eh_status eh_prefill_batched_e4m3(eh_context* c, eh_stream stream, const float* q,
+                                  uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                                  const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                                  const uint32_t* cu_q, const uint32_t* start_pos, uint32_t batch,
+                                  uint32_t max_q_tokens, uint32_t total_q_tokens, float* out,
+                                  uint64_t out_bytes, uint32_t n_head, uint32_t n_head_kv,
+                                  uint32_t head_dim, uint32_t block_tokens, const float* k_scale,
+                                  const float* v_scale) {
+    if (!k_scale || !v_scale) return fail(EH_INVALID_ARGS, "scale arrays are null");
+    return prefill_batched_body(c, stream, EH_KV_FP8, q, q_bytes, pool, pool_bytes, bt, bt_bytes,
+                                bt_stride, cu_q, start_pos, batch, max_q_tokens, total_q_tokens,
+                                out, out_bytes, n_head, n_head_kv, head_dim, block_tokens, k_scale,
+                                v_scale);
 }
 
 }  // extern "C"

@@ -37,7 +37,7 @@
 
 namespace {
 
-enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_FP8 = 3 };
 
 constexpr int NT = 512;           // threads per workgroup (8 waves)
 constexpr int NL = 256;           // threads (waves 0-3) that stage the K/V tiles
@@ -78,13 +78,24 @@ template <> struct op_t<DT_F32> {
     }
 };
 
+// E4M3 pages are staged into LDS as f16 (exact) and use the f16 operands,
+// with q split into hi + lo f16 halves for S (E4M3 keys span 448 / 2^-9, so
+// scores need more than q's 11 bits); P stays single f16 as in decode.
+template <> struct op_t<DT_FP8> : op_t<DT_F16> {
+    static constexpr bool SPLIT = true;
+};
+
 // 8 f32 -> MFMA operand (hi part, and lo = x - hi for split types).
 template <int DT>
 __device__ __forceinline__ void pack8(const float* x, typename op_t<DT>::v& hi,
                                       typename op_t<DT>::v& lo) {
     if constexpr (DT == DT_F16) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hi[e] = (_Float16)x[e];
+        for (int e = 0; e < 8; ++e) {
+            const _Float16 h = (_Float16)x[e];
+            hi[e] = h;
+            lo[e] = (_Float16)(x[e] - (float)h);
+        }
     } else if constexpr (DT == DT_BF16) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -121,6 +132,19 @@ struct geo {
     static_assert(HD % 32 == 0, "head_dim must be a multiple of 32");
 };
 
+template <int HD>
+struct geo<DT_FP8, HD> : geo<DT_F16, HD> {};
+
+// Eight E4M3 codes (two dwords, lowest byte first) as eight f16 (four dwords);
+// exact: every E4M3 value is an f16.
+__device__ __forceinline__ uint4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
+    return make_uint4(
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true)));
+}
+
 struct lds_hdr {
     uint32_t tile_bad[2];  // tile index whose keys include an invalid page
     uint32_t slice_base;
@@ -133,7 +157,8 @@ __device__ __forceinline__ void prefill(
     const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ start_pos,
     const uint32_t* __restrict__ pos_ptr, uint32_t q_tokens, uint32_t pos_offset,
     float* __restrict__ out, uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens,
-    int bt_shift, uint32_t row_bytes, float scale_log2, uint64_t n_blocks, uint8_t* smem) {
+    int bt_shift, uint32_t row_bytes, float scale_log2, uint64_t n_blocks, uint8_t* smem,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
     typedef op_t<DT> O;
     typedef typename O::v opv;
     typedef geo<DT, HD> Gm;
@@ -223,7 +248,11 @@ __device__ __forceinline__ void prefill(
     const int part = tid % Gm::PARTS;
     const int kg = tid / Gm::PARTS;
     const uint64_t page_bytes = (uint64_t)block_tokens * 2u * row_bytes;
-    const uint32_t head_off = hk * HD * Gm::ELT + part * 16;
+    // E4M3 pages: one byte per element, a load item is 8 codes per key
+    constexpr bool F8 = DT == DT_FP8;
+    constexpr int CT = F8 ? DT_F16 : DT;  // MFMA operand type
+    constexpr uint32_t SE = F8 ? 1u : (uint32_t)Gm::ELT;  // stored element bytes
+    const uint32_t head_off = hk * HD * SE + part * (16 / Gm::ELT) * SE;
     uint4 kr[4], vr[4];
     uint32_t okbits = 0;  // bit j: key 4*kg+j loadable; bit 4+j: key <= kmax with a bad page
 
@@ -246,8 +275,15 @@ __device__ __forceinline__ void prefill(
                 const bool live = key0 + j <= kmax;
                 okbits |= (live && pv ? 1u : 0u) << j;
                 okbits |= (live && !pv ? 1u : 0u) << (4 + j);
-                kr[j] = *reinterpret_cast<const uint4*>(p + j * step);
-                vr[j] = *reinterpret_cast<const uint4*>(p + j * step + (pv ? row_bytes : 0u));
+                if constexpr (F8) {
+                    const uint2 a = *reinterpret_cast<const uint2*>(p + j * step);
+                    const uint2 b = *reinterpret_cast<const uint2*>(p + j * step + (pv ? row_bytes : 0u));
+                    kr[j] = make_uint4(a.x, a.y, 0u, 0u);
+                    vr[j] = make_uint4(b.x, b.y, 0u, 0u);
+                } else {
+                    kr[j] = *reinterpret_cast<const uint4*>(p + j * step);
+                    vr[j] = *reinterpret_cast<const uint4*>(p + j * step + (pv ? row_bytes : 0u));
+                }
             }
         } else {
             uint32_t phys[4];
@@ -263,8 +299,15 @@ __device__ __forceinline__ void prefill(
                 okbits |= (live && !pv ? 1u : 0u) << (4 + j);
                 const uint8_t* p = pool + (uint64_t)(pv ? phys[j] : 0u) * page_bytes +
                                    (uint64_t)(pv ? slot * slot_bytes + head_off : 0u);
-                kr[j] = *reinterpret_cast<const uint4*>(p);
-                vr[j] = *reinterpret_cast<const uint4*>(p + (pv ? row_bytes : 0u));
+                if constexpr (F8) {
+                    const uint2 a = *reinterpret_cast<const uint2*>(p);
+                    const uint2 b = *reinterpret_cast<const uint2*>(p + (pv ? row_bytes : 0u));
+                    kr[j] = make_uint4(a.x, a.y, 0u, 0u);
+                    vr[j] = make_uint4(b.x, b.y, 0u, 0u);
+                } else {
+                    kr[j] = *reinterpret_cast<const uint4*>(p);
+                    vr[j] = *reinterpret_cast<const uint4*>(p + (pv ? row_bytes : 0u));
+                }
             }
         }
     };
@@ -272,6 +315,13 @@ __device__ __forceinline__ void prefill(
     auto commit = [&](uint32_t t, int buf) {
         uint8_t* ks = stage + buf * Gm::STAGE;
         uint8_t* vs = ks + Gm::KBYTES;
+        if constexpr (F8) {  // codes -> f16, then the f16 staging below
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                kr[j] = e4m3x8_to_f16(kr[j].x, kr[j].y);
+                vr[j] = e4m3x8_to_f16(vr[j].x, vr[j].y);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             if (okbits != 0xFu) {  // rare: keys past the window or on a bad page
@@ -327,6 +377,7 @@ __device__ __forceinline__ void prefill(
     //   16-bit: step t, half h -> dims 16t + 8h + e (e < 8)
     //   f32:    step t = 4u + e, half h -> dim 8u + 4h + e
     constexpr int QSTEPS = HD / O::KS;
+    const float qscale = scale_log2 * (F8 ? k_scale[hk] : 1.0f);  // E4M3: the K scale folds into q
     opv qa[QSTEPS], qb[O::SPLIT ? QSTEPS : 1];
     {
         const float* qrow = q + ((uint64_t)(qoff + tok) * n_head + head) * HD;
@@ -335,19 +386,19 @@ __device__ __forceinline__ void prefill(
             for (int t = 0; t < QSTEPS; ++t) {
                 const float4 a = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h);
                 const float4 c = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h + 4);
-                const float x[8] = {a.x * scale_log2, a.y * scale_log2, a.z * scale_log2,
-                                    a.w * scale_log2, c.x * scale_log2, c.y * scale_log2,
-                                    c.z * scale_log2, c.w * scale_log2};
-                pack8<DT>(x, qa[t], qb[O::SPLIT ? t : 0]);
+                const float x[8] = {a.x * qscale, a.y * qscale, a.z * qscale,
+                                    a.w * qscale, c.x * qscale, c.y * qscale,
+                                    c.z * qscale, c.w * qscale};
+                pack8<CT>(x, qa[t], qb[O::SPLIT ? t : 0]);
             }
         } else {
 #pragma unroll
             for (int u = 0; u < HD / 8; ++u) {
                 const float4 a = *reinterpret_cast<const float4*>(qrow + 8 * u + 4 * h);
-                qa[4 * u + 0] = a.x * scale_log2;
-                qa[4 * u + 1] = a.y * scale_log2;
-                qa[4 * u + 2] = a.z * scale_log2;
-                qa[4 * u + 3] = a.w * scale_log2;
+                qa[4 * u + 0] = a.x * qscale;
+                qa[4 * u + 1] = a.y * qscale;
+                qa[4 * u + 2] = a.z * qscale;
+                qa[4 * u + 3] = a.w * qscale;
             }
         }
     }
@@ -441,8 +492,8 @@ __device__ __forceinline__ void prefill(
             // O^T (HD x 32 rows) += V^T P^T
             if constexpr (Gm::ELT == 2) {
                 opv pa[2], pb[2];
-                pack8<DT>(p, pa[0], pb[0]);
-                pack8<DT>(p + 8, pa[1], pb[1]);
+                pack8<CT>(p, pa[0], pb[0]);
+                pack8<CT>(p + 8, pa[1], pb[1]);
 #pragma unroll
                 for (int db = 0; db < HD / 32; ++db) {
                     const int d = db * 32 + l32;
@@ -456,7 +507,7 @@ __device__ __forceinline__ void prefill(
                         const uint4 w = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
                         const opv a = __builtin_bit_cast(opv, w);
                         acc[db] = O::mma(a, pa[st], acc[db]);
-                        if constexpr (O::SPLIT) acc[db] = O::mma(a, pb[st], acc[db]);
+                        if constexpr (O::SPLIT && !F8) acc[db] = O::mma(a, pb[st], acc[db]);
                     }
                 }
             } else {
@@ -481,7 +532,7 @@ __device__ __forceinline__ void prefill(
 
     // ---- epilogue: combine the two halves' sums, normalise, store
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    const float inv = l_tot > 0.f ? (F8 ? v_scale[hk] : 1.0f) / l_tot : 0.f;
     if (row_ok) {
         float* orow = out + ((uint64_t)(qoff + tok) * n_head + head) * HD;
 #pragma unroll
@@ -505,12 +556,13 @@ __device__ __forceinline__ void prefill(
         uint32_t bt_entries, const uint32_t* cu_q, const uint32_t* start_pos,                    \
         const uint32_t* pos_ptr, uint32_t q_tokens, uint32_t pos_offset, float* out,             \
         uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens, int bt_shift,                \
-        uint32_t row_bytes, float scale_log2, uint64_t n_blocks) {                               \
+        uint32_t row_bytes, float scale_log2, uint64_t n_blocks, const float* k_scale,           \
+        const float* v_scale) {                                                                  \
         constexpr int BYTES = 64 + SLICE * 4 + 2 * geo<DT, HD>::N + 2 * geo<DT, HD>::STAGE;      \
         __shared__ __attribute__((aligned(16))) uint8_t smem[BYTES];                             \
         prefill<DT, HD>(q, pool, bt, bt_stride, bt_entries, cu_q, start_pos, pos_ptr, q_tokens,  \
                         pos_offset, out, n_head, n_head_kv, block_tokens, bt_shift, row_bytes,   \
-                        scale_log2, n_blocks, smem);                                             \
+                        scale_log2, n_blocks, smem, k_scale, v_scale);                           \
     }
 
 EH_PREFILL(f16, DT_F16, 64)
@@ -519,3 +571,5 @@ EH_PREFILL(bf16, DT_BF16, 64)
 EH_PREFILL(bf16, DT_BF16, 128)
 EH_PREFILL(f32, DT_F32, 64)
 EH_PREFILL(f32, DT_F32, 128)
+EH_PREFILL(fp8, DT_FP8, 64)
+EH_PREFILL(fp8, DT_FP8, 128)

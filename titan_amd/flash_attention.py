@@ -56,3 +56,20 @@ class FlashAttention2:
             self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
             int(stride), buf(cu_q)[0], buf(start_pos)[0], int(batch), int(max_q_tokens),
             int(total), op, ob, int(n_head), int(n_head_kv), int(head_dim), int(block_tokens)))
+
+    def launch_batched_e4m3(self, stream, q, pool, block_tables, cu_q, start_pos, out, n_head,
+                            n_head_kv, head_dim, block_tokens, max_q_tokens, k_scale, v_scale):
+        """launch_batched over an E4M3 pool with per-kv-head f32 scales
+        (k_scale / v_scale [n_head_kv] device tensors): attention on
+        decode(code) * scale."""
+        batch, stride = block_tables.shape
+        total = q.shape[0]
+        qp, qb = buf(q)
+        pp, pb = buf(pool)
+        bp, bb = buf(block_tables)
+        op, ob = buf(out)
+        check(self._L.eh_prefill_batched_e4m3(
+            self._ctx.handle, stream_handle(stream), qp, qb, pp, pb, bp, bb, int(stride),
+            buf(cu_q)[0], buf(start_pos)[0], int(batch), int(max_q_tokens), int(total), op, ob,
+            int(n_head), int(n_head_kv), int(head_dim), int(block_tokens), buf(k_scale)[0],
+            buf(v_scale)[0]))
