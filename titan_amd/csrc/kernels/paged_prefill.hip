@@ -106,6 +106,17 @@ __device__ __forceinline__ void pack8(const float* x, typename op_t<DT>::v& hi,
     }
 }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// Transposed LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane
+// 4r + b points at 4 consecutive 16-bit elements of row r (columns 4b..4b+3)
+// of a 4 x 16 block; lane c receives column c of rows 0..3.
+__device__ __forceinline__ uint64_t lds_read_tr(const uint8_t* p) {
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(const_cast<uint8_t*>(p)));
+    return __builtin_bit_cast(uint64_t, v);
+}
+
 __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
     return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
@@ -126,7 +137,11 @@ struct geo {
     static constexpr int GMASK = N / 4 - 1;
     static constexpr int GBYTES = 4 * ELT;
     static constexpr int KBYTES = N * KPITCH;
-    static constexpr int VBYTES = HD * VPITCH;
+    // 16-bit operands: V row-major (keys x dims, rows padded by 128 bytes) and
+    // read back transposed by ds_read_b64_tr_b16; f32: V^T rows
+    static constexpr bool VROWM = ELT == 2;
+    static constexpr int VRPITCH = HD * 2 + 128;  // padding measured best for the transposed reads
+    static constexpr int VBYTES = VROWM ? N * VRPITCH : HD * VPITCH;
     static constexpr int STAGE = KBYTES + VBYTES;
     static_assert(N % 32 == 0 && N >= 32, "tile must hold whole 32-key sub-blocks");
     static_assert(HD % 32 == 0, "head_dim must be a multiple of 32");
@@ -198,6 +213,9 @@ __device__ __forceinline__ void prefill(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int h = lane >> 5;
+    // transposed V reads: this lane's byte offset in a row-major V tile
+    const uint32_t vtr_off = (4 * h + ((lane & 15) >> 2)) * Gm::VRPITCH +
+                             (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
 
     // ---- this lane's query row (column of S^T / O^T)
     const uint32_t row_raw = row0 + wave * 32 + l32;
@@ -333,24 +351,10 @@ __device__ __forceinline__ void prefill(
             }
             *reinterpret_cast<uint4*>(ks + (4 * kg + j) * Gm::KPITCH + part * 16) = kr[j];
         }
-        if constexpr (Gm::ELT == 2) {
-            // V^T rows: element d of the chunk, 4 keys -> 8 bytes
-            const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
-            const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
-            const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
-            const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
+        if constexpr (Gm::VROWM) {  // V rows like K rows
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint2 ev, od;
-                ev.x = perm(w1[i], w0[i], 0x05040100u);
-                ev.y = perm(w3[i], w2[i], 0x05040100u);
-                od.x = perm(w1[i], w0[i], 0x07060302u);
-                od.y = perm(w3[i], w2[i], 0x07060302u);
-                const int d = part * 8 + 2 * i;
-                const int col = (kg ^ (part & Gm::GMASK)) * Gm::GBYTES;  // d >> 3 == part
-                *reinterpret_cast<uint2*>(vs + d * Gm::VPITCH + col) = ev;
-                *reinterpret_cast<uint2*>(vs + (d + 1) * Gm::VPITCH + col) = od;
-            }
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<uint4*>(vs + (4 * kg + j) * Gm::VRPITCH + part * 16) = vr[j];
         } else {
             const uint32_t w[4][4] = {{vr[0].x, vr[0].y, vr[0].z, vr[0].w},
                                       {vr[1].x, vr[1].y, vr[1].z, vr[1].w},
@@ -494,17 +498,21 @@ __device__ __forceinline__ void prefill(
                 opv pa[2], pb[2];
                 pack8<CT>(p, pa[0], pb[0]);
                 pack8<CT>(p + 8, pa[1], pb[1]);
+                const uint8_t* vtr = vs + vtr_off;
+                // A = V^T[dims db*32 + l32][keys]: lane (l32, h) takes keys
+                // 16st + 4h + 0..3 and 16st + 8 + 4h + 0..3 (the order P^T holds
+                // them in), two transposed reads of 4 keys each; within a
+                // 16-lane group c = lane % 16 points at key row 4h + c/4 (+ the
+                // step's base) and dims 16 ((lane/16) % 2) + 4 (c % 4) ..
 #pragma unroll
                 for (int db = 0; db < HD / 32; ++db) {
-                    const int d = db * 32 + l32;
-                    const uint8_t* vrow = vs + d * Gm::VPITCH;
-                    const int sw = (d >> 3) & Gm::GMASK;
 #pragma unroll
                     for (int st = 0; st < 2; ++st) {
-                        const int g = sb * 8 + 4 * st + h;  // keys 16st+4h.. and 16st+8+4h..
-                        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + (g ^ sw) * Gm::GBYTES);
-                        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + ((g + 2) ^ sw) * Gm::GBYTES);
-                        const uint4 w = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+                        const uint8_t* vp = vtr + (sb * 32 + 16 * st) * Gm::VRPITCH + db * 64;
+                        const uint64_t r0 = lds_read_tr(vp);
+                        const uint64_t r1 = lds_read_tr(vp + 8 * Gm::VRPITCH);
+                        const uint4 w = make_uint4((uint32_t)r0, (uint32_t)(r0 >> 32), (uint32_t)r1,
+                                                   (uint32_t)(r1 >> 32));
                         const opv a = __builtin_bit_cast(opv, w);
                         acc[db] = O::mma(a, pa[st], acc[db]);
                         if constexpr (O::SPLIT && !F8) acc[db] = O::mma(a, pb[st], acc[db]);
