@@ -182,15 +182,16 @@ uint64_t max_tps(uint64_t block_tokens, uint64_t chunk = 1) {
     return std::max<uint64_t>((kBtSlice - 2) * block_tokens / chunk, 1) * chunk;
 }
 
-// Tokens one decode workgroup walks per unrolled chunk (mirrors the kernel:
-// 16-byte lane vectors, 4 waves, 16 wave steps capped at 512 tokens).
+// Split granularity of the fixed-split kernel: one round of its 4 waves, TPW
+// tokens each (mirrors the kernel: 16-byte lane vectors, a head row over
+// head_dim / (16 / elt) lanes).  The waves take turns by TPW tokens, so any
+// multiple of a round keeps every wave busy.
 uint64_t chunk_tokens(uint32_t kv_dtype, uint64_t head_dim) {
     const uint64_t elt = elt_bytes(kv_dtype) ? elt_bytes(kv_dtype) : 4;
     const uint64_t epl = std::min<uint64_t>(16 / elt, head_dim);
     const uint64_t tpw = 64 / std::max<uint64_t>(head_dim / epl, 1);
     const uint64_t nw = kDecodeThreads / 64;
-    const uint64_t steps = std::max<uint64_t>(1, std::min<uint64_t>(16, 512 / (nw * tpw)));
-    return nw * tpw * steps;
+    return nw * tpw;
 }
 
 // Which split kernel serves a decode shape, and its work granularity.

@@ -138,8 +138,8 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // touches.  The host keeps tokens_per_split <= (BT_SLICE - 2) * block_tokens.
 constexpr uint32_t BT_SLICE = 1024;
 // Wave steps per chunk: 16, fewer for narrow heads so that a chunk stays at
-// most 512 tokens.  tokens_per_split should be a multiple of the chunk
-// NW * TPW * chunk_steps(TPW) (the host derives the same value).
+// most 512 tokens.  tokens_per_split is a multiple of one round of the
+// waves, NW * TPW tokens (the host derives the same value).
 __host__ __device__ constexpr int chunk_steps(int tpw) {
     return (512 / (NW * tpw)) < 1 ? 1 : ((512 / (NW * tpw)) > 16 ? 16 : 512 / (NW * tpw));
 }
@@ -242,22 +242,23 @@ __device__ __forceinline__ void decode_split(
     __syncthreads();
 
     // The split is walked in chunks of NW * TPW * STEPS tokens.  Inside a
-    // chunk each wave streams STEPS consecutive wave steps (TPW neighbouring
-    // tokens each, one per lane group) through a DEPTH-deep register
-    // pipeline.  The steps are fully unrolled, so slot indices are compile
-    // time constants and no in-flight load crosses a loop back edge.
+    // chunk the waves take turns by TPW neighbouring tokens (one per lane
+    // group): wave step k of wave w covers tokens c0 + (k NW + w) TPW ..,
+    // so a split shorter than a chunk still spreads over every wave.  Each
+    // wave streams its steps through a DEPTH-deep register pipeline; the
+    // steps are fully unrolled, so slot indices are compile time constants
+    // and no in-flight load crosses a loop back edge.
     for (uint32_t c0 = t0; c0 < t1; c0 += CHUNK) {
-        const uint32_t w0 = c0 + (uint32_t)wave * TPW * STEPS;
-        const uint32_t w1 = (w0 + TPW * STEPS < t1) ? w0 + TPW * STEPS : t1;
-        if (w0 >= w1) continue;  // wave-uniform: nothing left for this wave
+        const uint32_t w0 = c0 + (uint32_t)wave * TPW;  // this wave's first token
+        if (w0 >= t1) continue;                         // wave-uniform: nothing left
         raw_t<NWORDS> kr[DEPTH], vr[DEPTH];
         bool ok[DEPTH];
         // Loads of wave step k into slot k % DEPTH.  Steps past the end of
         // the range re-read the wave's first row (masked), staying in bounds.
         auto issue = [&](int k) {
             const int j = k % DEPTH;
-            const uint32_t t = w0 + (uint32_t)(k * TPW) + grp;
-            const bool valid = t < w1;
+            const uint32_t t = w0 + (uint32_t)(k * NW * TPW) + grp;
+            const bool valid = t < t1;
             const uint32_t tc = valid ? t : w0;
             const uint32_t pg = page_of(tc);
             const uint32_t rel = pg - pg0;
@@ -274,7 +275,7 @@ __device__ __forceinline__ void decode_split(
 #pragma unroll
         for (int k = 0; k < STEPS; ++k) {
             const int j = k % DEPTH;
-            if (w0 + (uint32_t)(k * TPW) >= w1) break;  // wave-uniform tail exit
+            if (w0 + (uint32_t)(k * NW * TPW) >= t1) break;  // wave-uniform tail exit
             float s[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) {
