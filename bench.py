@@ -67,7 +67,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus above 1 is not supported "
-                          "(see DESIGN.md for how the path shards)", "n_gpus": args.gpus}))
+                          "(the path shards by sequence or by kv head with no exchange inside it; one "
+                          "GPU's share is what is measured)", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import numpy as np
