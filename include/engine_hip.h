@@ -281,6 +281,23 @@ eh_status eh_append_decode_batched(eh_context* ctx, eh_stream stream, const eh_k
                                    const float* q, uint64_t q_bytes, float* out, uint64_t out_bytes,
                                    uint32_t n_head, uint32_t head_dim, uint32_t grid,
                                    void* workspace, uint64_t workspace_bytes);
+/* The same fused decode step over E4M3 pages (extension: the quantising
+ * append of eh_append_kv_e4m3_batched, then eh_paged_decode_batched_e4m3, in
+ * one launch): keys/values [batch, row_len] f32 are quantised in the launch
+ * (code = quantize(x / scale) with k_scale / v_scale [n_head_kv], as the
+ * append); pool bytes after the call equal eh_append_kv_e4m3_batched's and
+ * the output equals eh_paged_decode_batched_e4m3's with ctx_lens =
+ * start_pos + 1.  layout->data_type must be EH_KV_FP8. */
+eh_status eh_append_decode_batched_e4m3(eh_context* ctx, eh_stream stream,
+                                        const eh_kv_layout* layout, void* pool, uint64_t pool_bytes,
+                                        const float* keys, uint64_t keys_bytes, const float* values,
+                                        uint64_t values_bytes, const uint32_t* block_tables,
+                                        uint64_t bt_bytes, uint32_t bt_stride,
+                                        const uint32_t* start_pos, uint32_t batch, const float* q,
+                                        uint64_t q_bytes, float* out, uint64_t out_bytes,
+                                        uint32_t n_head, uint32_t head_dim, uint32_t grid,
+                                        void* workspace, uint64_t workspace_bytes,
+                                        const float* k_scale, const float* v_scale);
 
 /* ---- FlashAttention2::launch / launch_with_pos_ptr (flash_attention.rs:95-225):
  * causal chunked prefill.  q/out [q_tokens, n_head, head_dim] f32; query i

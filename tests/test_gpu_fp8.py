@@ -244,3 +244,56 @@ def test_e4m3_entry_errors(dev):
     with pytest.raises(HipError):       # E4M3 pools only through the scale-aware entries
         PagedAttention(0).decode_batched(None, q, pool, tab, lens, out, 12, n_kv, hd, bt,
                                          KvDataType.FP8, plan, ws)
+
+
+@pytest.mark.parametrize("shape,grid", [((12, 2, 128, 16), None), ((32, 8, 128, 16), None),
+                                        ((12, 2, 128, 16), 5)])
+def test_e4m3_fused_step_matches_separate(dev, shape, grid):
+    """eh_append_decode_batched_e4m3 (quantising append + decode in one launch)
+    leaves the pool bit-identical to eh_append_kv_e4m3_batched and its output
+    bit-identical to eh_paged_decode_batched_e4m3 after that append (lens =
+    start_pos + 1), and within tolerance of sdpa_decode on the dequantised
+    pool.  The appended rows include values that saturate (|x/scale| >= 448),
+    and contexts that end on every slot of a page."""
+    n_head, n_kv, hd, bt = shape
+    rng = np.random.default_rng(77 + n_kv)
+    pos = np.concatenate([[0, 1, 15, 16, 17, 31, 32, 255], rng.integers(1, 700, 8)]).astype(np.uint32)
+    B, rl = len(pos), n_kv * hd
+    tab, nb = make_tables(rng, pos + 1, bt)
+    codes = rng.integers(0, 256, nb * bt * 2 * rl).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C
+    ks = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
+    vs = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
+    newk = rng.standard_normal((B, rl)).astype(np.float32)
+    newv = rng.standard_normal((B, rl)).astype(np.float32)
+    newk[0, :4] = [30.0, -30.0, 1e-7, 0.0]               # saturating, subnormal, zero
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, KvDataType.FP8)
+    assert plan[0] == 0
+    if grid is not None:
+        plan = (0, grid, plan[2])
+    lay = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    dks, dvs, dq, dtab = t(ks), t(vs), t(q), i32(tab, dev)
+    pa = PagedAttention(0)
+    # separate: quantising append, then decode over lens = pos + 1
+    pool_a = t(codes.copy())
+    PagedKvGpu(0).append_kv_e4m3_batched(None, lay, pool_a, t(newk), t(newv), dtab,
+                                         i32(np.arange(B + 1), dev), i32(pos, dev), B, hd, dks, dvs)
+    out_a = torch.full((B, n_head, hd), float("nan"), device=dev)
+    pa.decode_batched_e4m3(None, dq, pool_a, dtab, i32(pos + 1, dev), out_a, n_head, n_kv, hd, bt,
+                           dks, dvs, plan, PagedAttention.workspace(plan))
+    # fused
+    pool_b = t(codes.copy())
+    out_b = torch.full((B, n_head, hd), float("nan"), device=dev)
+    pa.append_decode_batched_e4m3(None, lay, pool_b, t(newk), t(newv), dtab, i32(pos, dev), dq,
+                                  out_b, n_head, hd, plan, PagedAttention.workspace(plan), dks, dvs)
+    torch.cuda.synchronize()
+    pa_np, pb_np = pool_a.cpu().numpy(), pool_b.cpu().numpy()
+    bad = np.argwhere(pa_np != pb_np)
+    assert bad.size == 0, (bad[:4], pa_np[bad[0]], pb_np[bad[0]])
+    oa, ob = out_a.cpu().numpy(), out_b.cpu().numpy()
+    assert np.array_equal(oa.view(np.uint32), ob.view(np.uint32)), np.max(np.abs(oa - ob))
+    ref = orc.sdpa_decode_batched(dequant_pool(pb_np, nb, bt, n_kv, hd, ks, vs), tab, pos + 1, bt,
+                                  q, n_head, n_kv, hd)
+    check_close(ob, ref)

@@ -62,6 +62,9 @@ _SIGS = {
     "eh_decode_mass_workspace_bytes": (u64, [u32, u32, u32, u32]),
     "eh_append_decode_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp, u64,
                                        u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp, u64]),
+    "eh_append_decode_batched_e4m3": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp,
+                                            u64, u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp,
+                                            u64, vp, vp]),
     "eh_flash_attention_prefill": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64,
                                          u64, u64, u64, u64, vp]),
     "eh_prefill_batched_e4m3": (i32, [vp, vp, vp, u64, vp, u64, vp, u64, u32, vp, vp, u32, u32, u32,

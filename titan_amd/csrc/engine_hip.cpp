@@ -1152,13 +1152,16 @@ uint64_t eh_decode_mass_workspace_bytes(uint32_t batch, uint32_t bt_stride, uint
     return mass_ws_bytes(batch, bt_stride, block_tokens, n_head);
 }
 
-eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l,
-                                  void* pool, uint64_t pool_bytes, const void* keys,
-                                  uint64_t keys_bytes, const void* values, uint64_t values_bytes,
-                                  const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
-                                  const uint32_t* start_pos, uint32_t batch, const float* q,
-                                  uint64_t q_bytes, float* out, uint64_t out_bytes, uint32_t n_head,
-                                  uint32_t head_dim, uint32_t grid, void* ws, uint64_t ws_bytes) {
+static eh_status append_decode_body(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                                    void* pool, uint64_t pool_bytes, const void* keys,
+                                    uint64_t keys_bytes, const void* values, uint64_t values_bytes,
+                                    const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                                    const uint32_t* start_pos, uint32_t batch, const float* q,
+                                    uint64_t q_bytes, float* out, uint64_t out_bytes,
+                                    uint32_t n_head, uint32_t head_dim, uint32_t grid, void* ws,
+                                    uint64_t ws_bytes, const float* k_scale,
+                                    const float* v_scale) {
+    const bool e4m3 = k_scale != nullptr;
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
     if (batch == 0) return EH_OK;
     if (!start_pos) return fail(EH_INVALID_ARGS, "start_pos is null");
@@ -1169,7 +1172,12 @@ eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_
     const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
     if (l->n_blocks < 1 || page_bytes == 0) return fail(EH_INVALID_ARGS, "layout");
     if (pool_bytes < l->n_blocks * page_bytes) return invalid_size(l->n_blocks * page_bytes, pool_bytes);
-    const uint64_t row_expected = (uint64_t)batch * l->row_len * elt;
+    if (e4m3 && (l->data_type != EH_KV_FP8 || !v_scale))
+        return fail(EH_INVALID_ARGS, "E4M3 fused append+decode: FP8 layout and both scales");
+    if (!e4m3 && l->data_type == EH_KV_FP8)
+        return fail(EH_UNSUPPORTED, "FP8 pages: use eh_append_decode_batched_e4m3");
+    // E4M3: the appended rows arrive as f32 and are quantised in the launch
+    const uint64_t row_expected = (uint64_t)batch * l->row_len * (e4m3 ? 4 : elt);
     if (keys_bytes < row_expected) return invalid_size(row_expected, keys_bytes);
     if (values_bytes < row_expected) return invalid_size(row_expected, values_bytes);
     const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
@@ -1178,8 +1186,7 @@ eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
     const tiles_cfg tc = pick_tiles(l->data_type, head_dim, n_head, n_head_kv, l->block_tokens, batch);
-    if (!tc.ok || l->data_type == EH_KV_FP8)
-        return fail(EH_UNSUPPORTED, "fused append+decode: shape outside the balanced kernel");
+    if (!tc.ok) return fail(EH_UNSUPPORTED, "fused append+decode: shape outside the balanced kernel");
     if (grid < 1) return invalid_size(1, grid, "grid");
     const uint64_t ws_need = tiles_ws_bytes(grid, batch, n_head);
     if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
@@ -1203,7 +1210,38 @@ eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_
     a.block_tokens = (uint32_t)l->block_tokens;
     a.grid = grid;
     a.ws = ws;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
     return run_tiles(c, stream, a, tc);
+}
+
+eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                                  void* pool, uint64_t pool_bytes, const void* keys,
+                                  uint64_t keys_bytes, const void* values, uint64_t values_bytes,
+                                  const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                                  const uint32_t* start_pos, uint32_t batch, const float* q,
+                                  uint64_t q_bytes, float* out, uint64_t out_bytes, uint32_t n_head,
+                                  uint32_t head_dim, uint32_t grid, void* ws, uint64_t ws_bytes) {
+    return append_decode_body(c, stream, l, pool, pool_bytes, keys, keys_bytes, values,
+                              values_bytes, bt, bt_bytes, bt_stride, start_pos, batch, q, q_bytes,
+                              out, out_bytes, n_head, head_dim, grid, ws, ws_bytes, nullptr,
+                              nullptr);
+}
+
+eh_status eh_append_decode_batched_e4m3(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                                       void* pool, uint64_t pool_bytes, const float* keys,
+                                       uint64_t keys_bytes, const float* values,
+                                       uint64_t values_bytes, const uint32_t* bt, uint64_t bt_bytes,
+                                       uint32_t bt_stride, const uint32_t* start_pos, uint32_t batch,
+                                       const float* q, uint64_t q_bytes, float* out,
+                                       uint64_t out_bytes, uint32_t n_head, uint32_t head_dim,
+                                       uint32_t grid, void* ws, uint64_t ws_bytes,
+                                       const float* k_scale, const float* v_scale) {
+    if (!k_scale) return fail(EH_INVALID_ARGS, "k_scale is null");
+    return append_decode_body(c, stream, l, pool, pool_bytes, keys, keys_bytes, values,
+                              values_bytes, bt, bt_bytes, bt_stride, start_pos, batch, q, q_bytes,
+                              out, out_bytes, n_head, head_dim, grid, ws, ws_bytes, k_scale,
+                              v_scale);
 }
 
 eh_status eh_flash_attention_prefill(eh_context* c, eh_stream stream, uint32_t kv_dtype,

@@ -48,6 +48,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "e4m3.h"
+
 namespace {
 
 enum { DT_F16 = 1, DT_BF16 = 2, DT_FP8 = 3 };
@@ -450,6 +452,52 @@ __device__ __forceinline__ void decode_tiles(
                 constexpr int j = decltype(Rc)::value;
                 vr[D][j] = *reinterpret_cast<const u32x4*>(base + row_bytes + v_tok(j) * slot_bytes + v_off);
             });
+        } else if constexpr (F8) {
+            // partial tile; with a fused append the appended token's codes
+            // replace its (not yet written) pool row in the registers
+            static_for<0, KREG>([&](auto Sc) {
+                constexpr int j = decltype(Sc)::value;
+                kr[D][j] = *k_at(base + (x < nvalid ? x : 0u) * slot_bytes, j);
+            });
+            static_for<0, VREG>([&](auto Rc) {
+                constexpr int j = decltype(Rc)::value;
+                const uint32_t t = v_tok(j);
+                vr[D][j] = *reinterpret_cast<const u32x4*>(base + row_bytes +
+                                                           (t < nvalid ? t : 0u) * slot_bytes + v_off);
+            });
+            if (last) {  // uniform
+                // The appended f32 row of this kv head, quantised by the whole
+                // wave: lane l < 32 codes K dims 4l .. 4l + 3, lane 32 + l V
+                // dims 4l .. 4l + 3 (x / scale, as eh_append_kv_e4m3); the
+                // codes then move to the lanes of the tile layout by
+                // ds_bpermute -- K: lane (g, pos) takes dims 32 g + 16 j + 4 w
+                // from lane 8 g + 4 j + w; V: a lane holding token pos takes
+                // dims 16 (lane % 8) + 4 w from lane 32 + 4 (lane % 8) + w.
+                const uint32_t pos = ntk - 1u - tok0;
+                const bool kh = lane < 32u;
+                const float* nrow = reinterpret_cast<const float*>(kh ? new_k : new_v) +
+                                    (uint64_t)iss_b * n_head_kv * HD + kv * HD + 4u * (lane & 31u);
+                const float4 nv = *reinterpret_cast<const float4*>(nrow);
+                const float sc = kh ? k_scale[kv] : v_scale[kv];
+                const uint32_t c4 = e4m3_code(nv.x / sc) | (e4m3_code(nv.y / sc) << 8) |
+                                    (e4m3_code(nv.z / sc) << 16) | (e4m3_code(nv.w / sc) << 24);
+                static_for<0, KREG>([&](auto Sc) {
+                    constexpr int j = decltype(Sc)::value;
+                    u32x4 c;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w)
+                        c[w] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((8u * g + 4u * j + w) * 4u), (int)c4);
+                    if (x == pos) kr[D][j] = c;
+                });
+                u32x4 cv;
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    cv[w] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((32u + 4u * (lane & 7u) + w) * 4u), (int)c4);
+                static_for<0, VREG>([&](auto Rc) {
+                    constexpr int j = decltype(Rc)::value;
+                    if (v_tok(j) == pos) vr[D][j] = cv;
+                });
+            }
         } else {
             const uint32_t pos = ntk - 1u - tok0;  // appended token within the tile
             const uint64_t nrow = (uint64_t)iss_b * row_bytes + kv_off;
@@ -570,7 +618,25 @@ __device__ __forceinline__ void decode_tiles(
             }
         }
         // fused append: store the appended token's K/V slice of this kv
-        // head from the registers that already hold it
+        // head from the registers that already hold it (E4M3: its codes;
+        // K lane (g, pos): dims 32 g .. 32 g + 31, V: the lanes holding
+        // token pos, dims 16 (lane % 8) ..)
+        if constexpr (F8) if (new_k != nullptr && tok0 + TILE >= ntk) {
+            const uint32_t pos = ntk - 1u - tok0;
+            uint8_t* dst = pool + (uint64_t)phys * page_bytes +
+                           (uint64_t)((tok0 & slot_mask) + pos) * slot_bytes + kv_off;
+            if (x == pos) {
+                static_for<0, KREG>([&](auto Sc) {
+                    constexpr int j = decltype(Sc)::value;
+                    *reinterpret_cast<u32x4*>(dst + 32 * g + 16 * j) = kr[D][j];
+                });
+            }
+            static_for<0, VREG>([&](auto Rc) {
+                constexpr int j = decltype(Rc)::value;
+                if ((lane >> 3) + 8u * j == pos)
+                    *reinterpret_cast<u32x4*>(dst + row_bytes + 16 * (lane & 7u)) = vr[D][j];
+            });
+        }
         if constexpr (!F8) if (new_k != nullptr && tok0 + TILE >= ntk) {
             const uint32_t pos = ntk - 1u - tok0;
             uint8_t* dst = pool + (uint64_t)phys * page_bytes +

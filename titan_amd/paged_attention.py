@@ -170,3 +170,27 @@ class PagedAttention:
             self._ctx.handle, stream_handle(stream), C.byref(lay), pp, pb, kp, kb, vp_, vb, bp, bb,
             int(stride), buf(start_pos)[0], int(batch), qp, qb, op, ob, int(n_head), int(head_dim),
             int(plan[1]), wp, wb))
+
+    def append_decode_batched_e4m3(self, stream, layout, pool, keys, values, block_tables,
+                                   start_pos, q, out, n_head, head_dim, plan, workspace, k_scale,
+                                   v_scale):
+        """append_decode_batched over E4M3 pages: keys/values [B, row_len] f32
+        are quantised in the launch with k_scale / v_scale [n_head_kv] (as
+        PagedKvGpu.append_kv_e4m3_batched), then attended as
+        decode_batched_e4m3."""
+        if plan[0] != 0:
+            raise ValueError("append_decode_batched_e4m3 needs a token-balanced plan "
+                             "(tokens_per_split 0)")
+        batch, stride = block_tables.shape
+        pp, pb = buf(pool)
+        kp, kb = buf(keys)
+        vp_, vb = buf(values)
+        bp, bb = buf(block_tables)
+        qp, qb = buf(q)
+        op, ob = buf(out)
+        wp, wb = buf(workspace)
+        lay = layout.c()
+        check(self._L.eh_append_decode_batched_e4m3(
+            self._ctx.handle, stream_handle(stream), C.byref(lay), pp, pb, kp, kb, vp_, vb, bp, bb,
+            int(stride), buf(start_pos)[0], int(batch), qp, qb, op, ob, int(n_head), int(head_dim),
+            int(plan[1]), wp, wb, buf(k_scale)[0], buf(v_scale)[0]))
