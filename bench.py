@@ -347,6 +347,23 @@ def suite(args, dev):
           "GB/s": round(b8 / us8 / 1e3, 1), "hbm_frac_of_8TB/s": round(b8 / us8 / 1e3 / 8000.0, 4),
           "kernel": PagedAttention.kernel_name(12, 2, 128, 16, KvDataType.FP8) +
           " + eh_decode_tiles_merge"})
+
+    # the same step with the appended f32 rows quantised inside the decode launch
+    pos8 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
+    nk8 = torch.randn((32, s2.row_len), generator=gen, device=dev)
+    nv8 = torch.randn((32, s2.row_len), generator=gen, device=dev)
+
+    def step8(st):
+        p = pools8[turn[0] % len(pools8)]
+        turn[0] += 1
+        pa.append_decode_batched_e4m3(st, lay8, p, nk8, nv8, dtab2, pos8, q8, o8, 12, 128, plan8,
+                                      ws8, ks8, vs8)
+    us8f = graph_time_us(step8, 20, 32)
+    emit({"config": 2, "what": "fused E4M3 decode step (quantising append of the 32 new f32 rows "
+          "+ decode in one launch), B=32, 12/2 heads, hd 128, one layer",
+          "latency_us": round(us8f, 2), "kv_bytes": b8, "GB/s": round(b8 / us8f / 1e3, 1),
+          "kernel": PagedAttention.kernel_name(12, 2, 128, 16, KvDataType.FP8) +
+          " + eh_decode_tiles_merge"})
     del pools8
 
     # ---- config 3: bf16 chunked prefill, B=8, 512 new tokens on 2048 cached, 32/8 heads
