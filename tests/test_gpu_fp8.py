@@ -297,3 +297,57 @@ def test_e4m3_fused_step_matches_separate(dev, shape, grid):
     ref = orc.sdpa_decode_batched(dequant_pool(pb_np, nb, bt, n_kv, hd, ks, vs), tab, pos + 1, bt,
                                   q, n_head, n_kv, hd)
     check_close(ob, ref)
+
+
+def test_e4m3_fused_step_graph_replay(dev):
+    """The fused E4M3 step captured once and replayed as positions grow (the
+    work split follows the device lengths): every replay equals eager
+    quantising append + E4M3 decode, pool and output bit for bit."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl, B, steps = n_kv * hd, 6, 5
+    rng = np.random.default_rng(13)
+    start0 = np.array([0, 14, 31, 500, 1023, 77], np.int64)
+    tab, nb = make_tables(rng, start0 + steps + 1, bt)
+    codes = rng.integers(0, 256, nb * bt * 2 * rl).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C
+    host = torch.from_numpy(codes)
+    pool_g, pool_e = host.to(dev), host.to(dev)
+    lay = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
+    dtab, pos, cu = i32(tab, dev), i32(start0, dev), i32(np.arange(B + 1), dev)
+    ks = torch.from_numpy(rng.uniform(0.002, 0.05, n_kv).astype(np.float32)).to(dev)
+    vs = torch.from_numpy(rng.uniform(0.002, 0.05, n_kv).astype(np.float32)).to(dev)
+    k = torch.empty((B, rl), device=dev)
+    v = torch.empty_like(k)
+    q = torch.empty((B, n_head, hd), device=dev)
+    out_g, out_e = torch.empty_like(q), torch.empty_like(q)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(start0.max()) + steps + 1, 0,
+                               KvDataType.FP8)
+    ws_g, ws_e = PagedAttention.workspace(plan), PagedAttention.workspace(plan)
+    pa, kv = PagedAttention(0), PagedKvGpu(0)
+    k.zero_(); v.zero_(); q.zero_()
+    pa.append_decode_batched_e4m3(None, lay, pool_g, k, v, dtab, pos, q, out_g, n_head, hd, plan,
+                                  ws_g, ks, vs)
+    torch.cuda.synchronize()
+    pool_g.copy_(host.to(dev))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            pa.append_decode_batched_e4m3(s, lay, pool_g, k, v, dtab, pos, q, out_g, n_head, hd,
+                                          plan, ws_g, ks, vs)
+    torch.cuda.synchronize()
+    for step in range(steps):
+        k.copy_(torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)))
+        v.copy_(torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)))
+        q.copy_(torch.from_numpy(rng.standard_normal((B, n_head, hd)).astype(np.float32)))
+        pos.copy_(i32(start0 + step, dev))
+        torch.cuda.synchronize()
+        kv.append_kv_e4m3_batched(None, lay, pool_e, k, v, dtab, cu, pos, B, hd, ks, vs)
+        pa.decode_batched_e4m3(None, q, pool_e, dtab, pos + 1, out_e, n_head, n_kv, hd, bt, ks, vs,
+                               plan, ws_e)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(pool_g, pool_e), step
+        assert torch.equal(out_g.view(torch.int32), out_e.view(torch.int32)), step
