@@ -696,18 +696,21 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_merge(
     const uint64_t qrow = (uint64_t)b * n_head + qh;
     const float2* ml = reinterpret_cast<const float2*>(part_ml) + qrow * max_splits;
     const float* pa = part_acc + qrow * max_splits * head_dim + d;
+    // Partials in batches of NB: every load of a batch is in flight at once
+    // (one memory round trip for up to NB splits).
+    constexpr int NB = 32;
     float M = -INFINITY, Ls = 0.0f, A = 0.0f;
-    for (uint32_t s0 = 0; s0 < nsplit; s0 += 8) {
-        float2 v[8];
-        float x[8];
+    for (uint32_t s0 = 0; s0 < nsplit; s0 += NB) {
+        float2 v[NB];
+        float x[NB];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NB; ++i) {
             const uint32_t sidx = s0 + i < nsplit ? s0 + i : s0;
             v[i] = ml[sidx];
             x[i] = pa[(uint64_t)sidx * head_dim];
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NB; ++i) {
             if (s0 + i >= nsplit || !(v[i].y > 0.0f)) continue;
             if (v[i].x > M) {
                 const float c = fast_exp2(M - v[i].x);  // 0 on the first live split
