@@ -184,7 +184,7 @@ eh_status eh_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype
  *     cuts the batch's 16-token tiles evenly among them from the live
  *     lengths, so any context lengths are served (max_ctx is not a bound);
  *   - otherwise fixed splits: tokens_per_split (hint rounded up to the
- *     kernel's split granularity -- one round of its four waves, 8 to 64
+ *     kernel's split granularity -- one round of its four waves, 8 to 256
  *     tokens, for the per-token kernel -- or automatic; at most
  *     1022 * block_tokens) and the split bound max_splits (at most 256). */
 eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uint32_t n_head_kv,
