@@ -90,6 +90,12 @@ def test_decode_plan():
     # a split's block-table slice must fit the 1024-entry LDS stage
     assert L.eh_decode_plan(1, 1, 12, 2, 128, 1, 100000, 2048, C.byref(tps), C.byref(ms),
                             C.byref(ws)) == 1
+    # fixed-split kernel (f32): the split granularity is one round of its four
+    # waves (4 tokens each at head_dim 64), so a hint of 20 rounds up to 32
+    assert L.eh_decode_plan(0, 1, 14, 2, 64, 16, 512, 20, C.byref(tps), C.byref(ms),
+                            C.byref(ws)) == 0
+    assert (tps.value, ms.value) == (32, 16)
+    assert ws.value == 14 * 16 * (64 + 2) * 4
 
 
 class HostCache:
