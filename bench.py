@@ -298,6 +298,14 @@ def suite(args, dev):
           "hd 64, ctx 512", "latency_us": round(us1, 2),
           "kv_bytes": 512 * rl * 2 * 4, "GB/s": round(512 * rl * 2 * 4 / us1 / 1e3, 1)})
 
+    def step1f(st):
+        pa.append_flash_decoding(st, k1, v1, q1, pool1, tab1, o1, s1.n_head, s1.n_head_kv,
+                                 s1.head_dim, 16, 511)
+    us1f = graph_time_us(step1f, 20)
+    emit({"config": 1, "what": "the same step in one launch (eh_append_flash_decoding)",
+          "latency_us": round(us1f, 2), "kv_bytes": 512 * rl * 2 * 4,
+          "GB/s": round(512 * rl * 2 * 4 / us1f / 1e3, 1)})
+
     # ---- append / gather at config 2's shape (one layer)
     s2 = synth.config2(0, extra_tokens=1)
     tab2 = synth.block_tables(s2, extra_tokens=1)

@@ -173,6 +173,21 @@ eh_status eh_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype
                             float* out, uint64_t out_bytes, uint64_t n_head, uint64_t n_head_kv,
                             uint64_t head_dim, uint64_t block_tokens, uint64_t seq_tokens,
                             uint64_t query_pos, int causal, const uint32_t* pos_ptr);
+/* Single-sequence decode step in one launch (extension: PagedKvGpu::append_kv
+ * / append_kv_with_pos_ptr, paged_kv.rs:200-327, of one token followed by
+ * launch_flash_decoding, paged_attention.rs:352-490): keys/values [row_len]
+ * (pool element type) are written at position p = *pos_ptr (device) or
+ * query_pos, then q attends tokens 0..p.  Pool bytes after the call equal
+ * the append's, the output equals eh_flash_decoding's with seq_tokens = p + 1,
+ * query_pos = p, causal.  16-bit and f32 pages; FP8 returns EH_UNSUPPORTED. */
+eh_status eh_append_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                                   const void* keys, uint64_t keys_bytes, const void* values,
+                                   uint64_t values_bytes, const float* q, uint64_t q_bytes,
+                                   void* pool, uint64_t pool_bytes, const uint32_t* block_table,
+                                   uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                                   uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                                   uint64_t block_tokens, uint64_t query_pos,
+                                   const uint32_t* pos_ptr);
 
 /* ---- Batched decode (extension: B sequences in one launch).
  * eh_decode_plan picks the kernel and its launch shape for contexts up to

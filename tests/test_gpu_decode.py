@@ -381,3 +381,70 @@ def test_attention_validation_errors(dev):
     with pytest.raises(HipError) as e:
         pa.launch(None, q, pool, bt, out, 4, 2, 24, 4, 4, 3, True)
     assert e.value.kind in ("InvalidSize", "Unsupported")
+
+
+def test_config1_fused_step(dev):
+    """Benchmark config 1 as one launch (eh_append_flash_decoding): the pool
+    equals the oracle cache after the append, the output is within the f32
+    bar of sdpa_decode."""
+    s = synth.config1(0)
+    rng = np.random.default_rng(0)
+    rl = s.row_len
+    table = s.free_order[:32].copy()
+    c = orc.Cache(64, 16, s.n_head_kv, s.head_dim)
+    c.seed_free_list(s.free_order)
+    seq = c.new_sequence()
+    rows = rng.standard_normal((512, 2, rl)).astype(np.float32)
+    for t in range(511):
+        c.append(seq, rows[t, 0], rows[t, 1])
+    pool = torch.from_numpy(c.buffer()).to(dev)
+    c.append(seq, rows[511, 0], rows[511, 1])
+    q = rng.standard_normal(s.n_head * s.head_dim).astype(np.float32)
+    out = torch.full((s.n_head * s.head_dim,), float("nan"), device=dev)
+    PagedAttention(0).append_flash_decoding(None, torch.from_numpy(rows[511, 0]).to(dev),
+                                            torch.from_numpy(rows[511, 1]).to(dev),
+                                            torch.from_numpy(q).to(dev), pool, i32(table, dev), out,
+                                            s.n_head, s.n_head_kv, s.head_dim, 16, 511)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.cpu().numpy(), c.buffer())
+    ref = orc.sdpa_decode(c.buffer(), table, 16, 512, q, s.n_head, s.n_head_kv, s.head_dim,
+                          True, 511)
+    check_close(out.cpu().numpy(), ref, KvDataType.F32)
+
+
+@pytest.mark.parametrize("dtype,cfg", [(KvDataType.F32, (14, 2, 64, 16)),
+                                       (KvDataType.F16, (12, 2, 128, 16)),
+                                       (KvDataType.BF16, (8, 8, 128, 8)),
+                                       (KvDataType.F16, (4, 1, 32, 4))])
+def test_fused_step_matches_append_then_decode(dev, dtype, cfg):
+    """eh_append_flash_decoding equals append_kv + launch_flash_decoding:
+    pool bit for bit, output within the dtype's bar of sdpa_decode, at
+    positions on every slot of a page and past a page boundary, host and
+    device positions."""
+    n_head, n_kv, hd, bt = cfg
+    rl = n_kv * hd
+    rng = np.random.default_rng(hd + n_kv)
+    nb = 40
+    table = rng.permutation(nb).astype(np.uint32)
+    td = {KvDataType.F32: torch.float32, KvDataType.F16: torch.float16,
+          KvDataType.BF16: torch.bfloat16}[dtype]
+    base = torch.from_numpy(rng.standard_normal(nb * bt * 2 * rl).astype(np.float32)).to(td)
+    layout = PagedKvLayout(nb, bt, rl, dtype)
+    kv, pa = PagedKvGpu(0), PagedAttention(0)
+    dt = i32(table, dev)
+    for p in (0, bt - 1, bt, 3 * bt + 2, nb * bt - 1):
+        for dev_pos in (False, True):
+            k = torch.from_numpy(rng.standard_normal(rl).astype(np.float32)).to(td).to(dev)
+            v = torch.from_numpy(rng.standard_normal(rl).astype(np.float32)).to(td).to(dev)
+            q = torch.from_numpy(rng.standard_normal(n_head * hd).astype(np.float32)).to(dev)
+            pos = i32([p], dev) if dev_pos else None
+            pool_a, pool_b = base.to(dev), base.to(dev)
+            kv.append_kv(None, layout, pool_a, k, v, dt, p, 1)
+            out_b = torch.full((n_head * hd,), float("nan"), device=dev)
+            pa.append_flash_decoding(None, k, v, q, pool_b, dt, out_b, n_head, n_kv, hd, bt,
+                                     0 if dev_pos else p, pos, dtype)
+            torch.cuda.synchronize()
+            assert torch.equal(pool_a.view(torch.uint8), pool_b.view(torch.uint8)), (p, dev_pos)
+            pf = pool_a.float().cpu().numpy()
+            ref = orc.sdpa_decode(pf, table, bt, p + 1, q.cpu().numpy(), n_head, n_kv, hd, True, p)
+            check_close(out_b.cpu().numpy(), ref, dtype)

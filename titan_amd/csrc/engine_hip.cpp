@@ -211,13 +211,13 @@ struct decode_kernel {
 constexpr uint32_t kSlotSteps = 16;  // mirrors SLOT_STEPS in paged_decode.hip
 
 decode_kernel pick_decode_kernel(uint32_t kv_dtype, uint64_t head_dim, uint64_t n_head,
-                                 uint64_t n_head_kv, uint64_t block_tokens) {
+                                 uint64_t n_head_kv, uint64_t block_tokens, bool no_slots = false) {
     decode_kernel k;
     const uint32_t group = (uint32_t)(n_head / n_head_kv);
     const bool pow2_kv = n_head_kv && !(n_head_kv & (n_head_kv - 1));
     const bool pow2_bt = block_tokens && !(block_tokens & (block_tokens - 1));
-    if ((kv_dtype == EH_KV_F16 || kv_dtype == EH_KV_BF16) && (head_dim == 64 || head_dim == 128) &&
-        pow2_kv && pow2_bt && n_head_kv <= 8 && group >= 1) {
+    if (!no_slots && (kv_dtype == EH_KV_F16 || kv_dtype == EH_KV_BF16) &&
+        (head_dim == 64 || head_dim == 128) && pow2_kv && pow2_bt && n_head_kv <= 8 && group >= 1) {
         const uint32_t gh = group % 4 == 0 ? 4 : group % 3 == 0 ? 3 : group <= 4 ? group : 4;
         const uint32_t need = (group + gh - 1) / gh;  // head groups per kv head
         uint32_t hgr = 1;
@@ -256,6 +256,10 @@ struct decode_args {
     uint32_t tps, max_splits;
     float* part_acc;
     float* part_ml;
+    // fused append (split kernel only): the row written at the last live
+    // position, [row_len] of the pool type
+    const void* new_k = nullptr;
+    const void* new_v = nullptr;
 };
 
 eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
@@ -264,7 +268,8 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
     if (!supported_hd(a.kv_dtype, a.head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, a.head_dim);
     if (a.max_splits > kMaxSplits) return invalid_size(kMaxSplits, a.max_splits, "max_splits");
     const decode_kernel dk =
-        pick_decode_kernel(a.kv_dtype, a.head_dim, a.n_head, a.n_head_kv, a.block_tokens);
+        pick_decode_kernel(a.kv_dtype, a.head_dim, a.n_head, a.n_head_kv, a.block_tokens,
+                           a.new_k != nullptr);
     char name[64];
     if (dk.slots)
         std::snprintf(name, sizeof name, "eh_decode_slots_%s_hd%u_h%u", dn, a.head_dim, dk.gh);
@@ -289,7 +294,8 @@ eh_status run_decode(eh_context* c, eh_stream stream, const decode_args& a) {
                     dim3(kDecodeThreads), stream, a.q, (const uint8_t*)a.pool, a.bt, a.bt_stride,
                     a.lens_ptr, a.lens_mode, a.seq_tokens, a.query_pos, a.causal, a.out,
                     a.part_acc, a.part_ml, a.n_head, a.n_head_kv, a.block_tokens, bt_shift, a.tps,
-                    a.max_splits, scale_log2, a.n_blocks);
+                    a.max_splits, scale_log2, a.n_blocks, (const uint8_t*)a.new_k,
+                    (const uint8_t*)a.new_v);
     if (st != EH_OK || a.max_splits <= 1) return st;
     return launch(c, mod, "eh_decode_merge",
                   dim3((uint32_t)div_ceil((uint64_t)a.n_head * a.head_dim, 256), a.batch), dim3(256),
@@ -843,7 +849,8 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
                                       float* out, uint64_t out_bytes, uint64_t n_head,
                                       uint64_t n_head_kv, uint64_t head_dim, uint64_t block_tokens,
                                       uint64_t seq_tokens, uint64_t query_pos, int causal,
-                                      const uint32_t* pos_ptr, bool single_pass) {
+                                      const uint32_t* pos_ptr, bool single_pass,
+                                      const void* new_k = nullptr, const void* new_v = nullptr) {
     if (!c) return fail(EH_INVALID_ARGS, "null context");
     eh_status st = validate_attention(kv_dtype, q_bytes, pool_bytes, bt_bytes, out_bytes, n_head,
                                       n_head_kv, head_dim, block_tokens, seq_tokens, query_pos);
@@ -873,7 +880,8 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
     // device, so size the grid for everything the block table can address.
     uint64_t cap = seq_tokens;
     if (pos_ptr) cap = std::max<uint64_t>(cap, (uint64_t)a.bt_stride * block_tokens);
-    const decode_kernel dk = pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens);
+    const decode_kernel dk =
+        pick_decode_kernel(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, new_k != nullptr);
     const uint64_t chunk = dk.chunk;
     uint64_t tps = auto_tps(1, dk.units, cap, block_tokens, chunk, dk.slots ? 512 : 1024);
     if (single_pass && cap <= max_tps(block_tokens, chunk))
@@ -888,6 +896,8 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
     a.max_splits = (uint32_t)div_ceil(cap, tps);
     a.part_acc = c->scratch;
     a.part_ml = c->scratch + n_head * a.max_splits * head_dim;
+    a.new_k = new_k;
+    a.new_v = new_v;
     return run_decode(c, stream, a);
 }
 
@@ -911,6 +921,28 @@ eh_status eh_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype, 
     return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
                                 out_bytes, n_head, n_head_kv, head_dim, block_tokens, seq_tokens,
                                 query_pos, causal, pos_ptr, false);
+}
+
+eh_status eh_append_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                   const void* keys, uint64_t keys_bytes, const void* values,
+                                   uint64_t values_bytes, const float* q, uint64_t q_bytes,
+                                   void* pool, uint64_t pool_bytes, const uint32_t* bt,
+                                   uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                                   uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                                   uint64_t block_tokens, uint64_t query_pos,
+                                   const uint32_t* pos_ptr) {
+    if (kv_dtype == EH_KV_FP8) return fail(EH_UNSUPPORTED, "FP8 pages: fused single-sequence step");
+    if (!keys || !values) return fail(EH_INVALID_ARGS, "keys / values are null");
+    const uint64_t row = n_head_kv * head_dim * elt_bytes(kv_dtype);
+    if (keys_bytes < row) return invalid_size(row, keys_bytes);
+    if (values_bytes < row) return invalid_size(row, values_bytes);
+    // a host-known position must have its page (paged_kv.rs:240-271 checks
+    // the table for the appended range)
+    if (!pos_ptr && block_tokens && query_pos / block_tokens >= bt_bytes / 4)
+        return invalid_size((query_pos / block_tokens + 1) * 4, bt_bytes, "block_table");
+    return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
+                                out_bytes, n_head, n_head_kv, head_dim, block_tokens, query_pos + 1,
+                                query_pos, 1, pos_ptr, false, keys, values);
 }
 
 eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uint32_t n_head_kv,

@@ -75,6 +75,21 @@ __device__ __forceinline__ raw_t<NWORDS> load_raw(const uint8_t* p) {
     return r;
 }
 
+// Raw store of a raw vector (the inverse of load_raw).
+template <int NWORDS>
+__device__ __forceinline__ void store_raw(uint8_t* p, const raw_t<NWORDS>& r) {
+    if constexpr (NWORDS >= 4) {
+#pragma unroll
+        for (int i = 0; i < NWORDS / 4; ++i)
+            *reinterpret_cast<uint4*>(p + 16 * i) =
+                make_uint4(r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]);
+    } else if constexpr (NWORDS == 2) {
+        *reinterpret_cast<uint2*>(p) = make_uint2(r.w[0], r.w[1]);
+    } else {
+        *reinterpret_cast<uint32_t*>(p) = r.w[0];
+    }
+}
+
 // Element e of a raw vector, widened to f32 (exact for every storage type).
 template <int DT, int NWORDS>
 __device__ __forceinline__ float elem(const raw_t<NWORDS>& r, int e) {
@@ -146,11 +161,12 @@ __host__ __device__ constexpr int chunk_steps(int tpw) {
 
 template <int DT, int HD, int G>
 __device__ __forceinline__ void decode_split(
-    const float* __restrict__ q, const uint8_t* __restrict__ pool,
+    const float* __restrict__ q, const uint8_t* pool,  // written only by a fused append
     const uint32_t* __restrict__ bt, uint32_t bt_stride, len_src L, float* __restrict__ out,
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t n_head,
     uint32_t n_head_kv, uint32_t block_tokens, int bt_shift, uint32_t tps, uint32_t max_splits,
-    float scale_log2, uint64_t n_blocks) {
+    float scale_log2, uint64_t n_blocks, const uint8_t* __restrict__ new_k,
+    const uint8_t* __restrict__ new_v) {
     constexpr int ELT = dt_info<DT>::bytes;
     constexpr int EPL = (16 / ELT) < HD ? (16 / ELT) : HD;  // elements per lane
     constexpr int LPT = HD / EPL;                            // lanes per token row
@@ -266,8 +282,11 @@ __device__ __forceinline__ void decode_split(
             const bool pv = phys < n_blocks;
             const uint8_t* p = kbase + (uint64_t)(pv ? phys : 0u) * page_bytes +
                                (uint64_t)(tc - pg * block_tokens) * tok_bytes;
-            kr[j] = load_raw<NWORDS>(p);
-            vr[j] = load_raw<NWORDS>(p + row_bytes);
+            // fused append: the new token's row comes from new_k / new_v
+            const bool isnew = new_k != nullptr && valid && t == n - 1u;
+            const uint64_t noff = ((uint64_t)hk * HD + (uint64_t)sub * EPL) * ELT;
+            kr[j] = load_raw<NWORDS>(isnew ? new_k + noff : p);
+            vr[j] = load_raw<NWORDS>(isnew ? new_v + noff : p + row_bytes);
             ok[j] = valid && pv;
         };
 #pragma unroll
@@ -298,6 +317,16 @@ __device__ __forceinline__ void decode_split(
                 l[h] += p;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p, elem<DT>(vr[j], e), acc[h][e]);
+            }
+            if (new_k != nullptr && okj) {  // fused append: write the new row to its page
+                const uint32_t t = w0 + (uint32_t)(k * NW * TPW) + grp;
+                if (t == n - 1u) {
+                    const uint32_t pg = page_of(t);
+                    uint8_t* p = const_cast<uint8_t*>(kbase) + (uint64_t)s_bt[pg - pg0] * page_bytes +
+                                 (uint64_t)(t - pg * block_tokens) * tok_bytes;
+                    store_raw<NWORDS>(p, kr[j]);
+                    store_raw<NWORDS>(p + row_bytes, vr[j]);
+                }
             }
             if (k + DEPTH < STEPS) issue(k + DEPTH);  // refill the slot DEPTH steps ahead
         }
@@ -732,11 +761,12 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_merge(
         const uint32_t* lens_ptr, uint32_t lens_mode, uint32_t seq_tokens, uint32_t query_pos,  \
         uint32_t causal, float* out, float* part_acc, float* part_ml, uint32_t n_head,          \
         uint32_t n_head_kv, uint32_t block_tokens, int bt_shift, uint32_t tps,                  \
-        uint32_t max_splits, float scale_log2, uint64_t n_blocks) {                             \
+        uint32_t max_splits, float scale_log2, uint64_t n_blocks, const uint8_t* new_k,         \
+        const uint8_t* new_v) {                                                                 \
         const len_src L{lens_ptr, lens_mode, seq_tokens, query_pos, causal};                    \
         decode_split<DT, HD, G>(q, pool, bt, bt_stride, L, out, part_acc, part_ml, n_head,      \
                                 n_head_kv, block_tokens, bt_shift, tps, max_splits, scale_log2, \
-                                n_blocks);                                                      \
+                                n_blocks, new_k, new_v);                                        \
     }
 
 #define EH_DECODE_G(DTN, DT, HD) \

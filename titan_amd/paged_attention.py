@@ -51,6 +51,24 @@ class PagedAttention:
                    n_head_kv, head_dim, block_tokens, seq_tokens, query_pos, causal, pos_ptr,
                    kv_dtype)
 
+    def append_flash_decoding(self, stream, keys, values, q, pool, block_table, out, n_head,
+                              n_head_kv, head_dim, block_tokens, query_pos, pos_ptr=None,
+                              kv_dtype=KvDataType.F32):
+        """One decode step of one sequence in one launch: keys/values [row_len]
+        land at position *pos_ptr (or query_pos), then q attends tokens 0..that
+        position (PagedKvGpu.append_kv, paged_kv.rs:200-327, followed by
+        launch_flash_decoding, paged_attention.rs:352-490)."""
+        kp, kb = buf(keys)
+        vp_, vb = buf(values)
+        qp, qb = buf(q)
+        pp, pb = buf(pool)
+        bp, bb = buf(block_table)
+        op, ob = buf(out)
+        check(self._L.eh_append_flash_decoding(
+            self._ctx.handle, stream_handle(stream), int(kv_dtype), kp, kb, vp_, vb, qp, qb, pp, pb,
+            bp, bb, op, ob, int(n_head), int(n_head_kv), int(head_dim), int(block_tokens),
+            int(query_pos), buf(pos_ptr)[0]))
+
     def _call(self, fn, stream, q, pool, block_table, out, n_head, n_head_kv, head_dim,
               block_tokens, seq_tokens, query_pos, causal, pos_ptr, kv_dtype):
         qp, qb = buf(q)
