@@ -448,3 +448,26 @@ def test_fused_step_matches_append_then_decode(dev, dtype, cfg):
             pf = pool_a.float().cpu().numpy()
             ref = orc.sdpa_decode(pf, table, bt, p + 1, q.cpu().numpy(), n_head, n_kv, hd, True, p)
             check_close(out_b.cpu().numpy(), ref, dtype)
+
+
+def test_fused_step_errors(dev):
+    """eh_append_flash_decoding rejects FP8 pools, short rows and a host
+    position past the block table before any launch."""
+    n_head, n_kv, hd, bt, nb = 4, 2, 64, 16, 4
+    rl = n_kv * hd
+    pool = torch.zeros(nb * bt * 2 * rl, device=dev)
+    table = i32(np.arange(nb), dev)
+    k = torch.zeros(rl, device=dev)
+    q = torch.zeros(n_head * hd, device=dev)
+    out = torch.empty_like(q)
+    pa = PagedAttention(0)
+    with pytest.raises(HipError):       # rows shorter than row_len
+        pa.append_flash_decoding(None, k[:rl - 4], k, q, pool, table, out, n_head, n_kv, hd, bt, 3)
+    with pytest.raises(HipError):       # position 64 needs a fifth page
+        pa.append_flash_decoding(None, k, k, q, pool, table, out, n_head, n_kv, hd, bt, nb * bt)
+    with pytest.raises(HipError):       # FP8 pools: the scale-aware entries only
+        pa.append_flash_decoding(None, k, k, q, pool, table, out, n_head, n_kv, hd, bt, 3,
+                                 kv_dtype=KvDataType.FP8)
+    pa.append_flash_decoding(None, k, k, q, pool, table, out, n_head, n_kv, hd, bt, nb * bt - 1)
+    torch.cuda.synchronize()
+    assert torch.all(torch.isfinite(out))

@@ -351,3 +351,33 @@ def test_e4m3_fused_step_graph_replay(dev):
         torch.cuda.synchronize()
         assert torch.equal(pool_g, pool_e), step
         assert torch.equal(out_g.view(torch.int32), out_e.view(torch.int32)), step
+
+
+def test_e4m3_fused_step_errors(dev):
+    """The fused E4M3 step needs an FP8 layout, both scales and f32 rows; the
+    16-bit fused step refuses FP8 pools.  All before any launch."""
+    from titan_amd import HipError, KvCacheError
+    n_kv, hd, bt, nb, B = 2, 128, 16, 8, 2
+    rl = n_kv * hd
+    pool = torch.zeros(nb * bt * 2 * rl, dtype=torch.uint8, device=dev)
+    lay = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
+    keys = torch.zeros((B, rl), device=dev)
+    tab = torch.zeros((B, 4), dtype=torch.int32, device=dev)
+    pos = torch.zeros(B, dtype=torch.int32, device=dev)
+    q = torch.zeros((B, 12, hd), device=dev)
+    out = torch.empty_like(q)
+    sc = torch.ones(n_kv, device=dev)
+    plan = PagedAttention.plan(B, 12, n_kv, hd, bt, 64, 0, KvDataType.FP8)
+    ws = PagedAttention.workspace(plan)
+    pa = PagedAttention(0)
+    with pytest.raises(HipError):       # f32 rows shorter than B x row_len
+        pa.append_decode_batched_e4m3(None, lay, pool, keys[:1], keys, tab, pos, q, out, 12, hd,
+                                      plan, ws, sc, sc)
+    with pytest.raises((HipError, KvCacheError)):   # a 16-bit layout
+        pa.append_decode_batched_e4m3(None, PagedKvLayout(nb, bt, rl, KvDataType.F16), pool, keys,
+                                      keys, tab, pos, q, out, 12, hd, plan, ws, sc, sc)
+    with pytest.raises((HipError, KvCacheError)):   # null scale arrays
+        pa.append_decode_batched_e4m3(None, lay, pool, keys, keys, tab, pos, q, out, 12, hd, plan,
+                                      ws, None, None)
+    with pytest.raises(HipError):       # FP8 pools only through the scale-aware fused step
+        pa.append_decode_batched(None, lay, pool, keys, keys, tab, pos, q, out, 12, hd, plan, ws)
