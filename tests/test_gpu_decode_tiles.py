@@ -295,3 +295,42 @@ def test_fused_graph_replay_growing_positions(dev):
         torch.cuda.synchronize()
         assert torch.equal(pool_g.view(torch.int16), pool_e.view(torch.int16))
         assert torch.max(torch.abs(out_g - out_e)).item() < 1e-6
+
+
+def test_fused_config5_shape(dev):
+    """Benchmark config 5's shape through the path the benchmark times (fused
+    append + balanced decode, 32/8 heads, hd 128, f16) at batch 2: 32767
+    cached tokens + 1 appended per sequence on pages scattered by a seeded
+    permutation, 1 % of K rows scaled x8 (the softmax-range stress)."""
+    n_head, n_kv, hd, bt, ctx, B = 32, 8, 128, 16, 32768, 2
+    rl = n_kv * hd
+    rng = np.random.default_rng(55)
+    need = ctx // bt
+    nb = B * need + 7
+    perm = rng.permutation(nb).astype(np.uint32)
+    tab = perm[:B * need].reshape(B, need)
+    host = rng.standard_normal((nb, bt, 2, rl)).astype(np.float16)
+    stress = rng.random((nb, bt)) < 0.01
+    host[:, :, 0][stress] *= np.float16(8)
+    pool = torch.from_numpy(host.reshape(-1)).to(dev)
+    newk = rng.standard_normal((B, rl)).astype(np.float16)
+    newv = rng.standard_normal((B, rl)).astype(np.float16)
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    pos = np.full(B, ctx - 1, np.uint32)
+    layout = PagedKvLayout(nb, bt, rl, KvDataType.F16)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, ctx)
+    assert plan[0] == 0
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).append_decode_batched(None, layout, pool, torch.from_numpy(newk).to(dev),
+                                            torch.from_numpy(newv).to(dev), i32(tab, dev),
+                                            i32(pos, dev), torch.from_numpy(q).to(dev), out, n_head,
+                                            hd, plan, PagedAttention.workspace(plan))
+    torch.cuda.synchronize()
+    want = host.copy()
+    for b in range(B):
+        want[tab[b, -1], bt - 1, 0] = newk[b]
+        want[tab[b, -1], bt - 1, 1] = newv[b]
+    assert np.array_equal(pool.cpu().numpy(), want.reshape(-1))
+    ref = orc.sdpa_decode_batched(want.reshape(-1).astype(np.float32), tab,
+                                  np.full(B, ctx, np.uint32), bt, q, n_head, n_kv, hd)
+    check_close(out.cpu().numpy(), ref)
