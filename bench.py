@@ -19,6 +19,7 @@ import argparse
 import json
 import os
 import platform
+import shutil
 import subprocess
 import sys
 import time
@@ -41,6 +42,7 @@ def parse():
     p.add_argument("--graph", type=int, default=1, help="replay the step as a HIP graph")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
     p.add_argument("--roofline-iters", type=int, default=10)
     p.add_argument("--fuse", type=int, default=1,
                    help="one fused append+decode launch per layer when the balanced kernel applies")
@@ -53,23 +55,72 @@ def parse():
 
 
 def cpu_model():
+    """lscpu's model name with its family/model/stepping numbers (a VM may
+    report a generic name), and /proc/cpuinfo's when lscpu is absent."""
+    fields = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
         for ln in out.splitlines():
-            if ln.startswith("Model name"):
-                return ln.split(":", 1)[1].strip()
+            k, _, v = ln.partition(":")
+            fields[k.strip()] = v.strip()
     except Exception:
         pass
-    return platform.processor() or "unknown"
+    name = fields.get("Model name")
+    if not name:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for ln in f:
+                    if ln.startswith("model name"):
+                        name = ln.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    name = name or platform.processor() or "unknown"
+    ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if fields.get(k)]
+    return name + (f" ({', '.join(ids)})" if ids else "")
+
+
+def start_cpu_baseline(args):
+    """Starts the CPU baseline in a child process pinned to one core
+    (`taskset -c <cpu>`, the first core this process may use) BEFORE anything
+    touches the GPU; the child sees no GPU at all.  Returns the Popen."""
+    cpu = min(os.sched_getaffinity(0))
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-child",
+           "--cpu-seconds", str(args.cpu_seconds)]
+    taskset = shutil.which("taskset")
+    cmd = ([taskset, "-c", str(cpu)] + cmd) if taskset else cmd
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="",
+               ROCR_VISIBLE_DEVICES="", TITAN_CPU_PIN=str(cpu),
+               TITAN_CPU_PINNER="taskset" if taskset else "sched_setaffinity")
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                            env=env)
+
+
+def finish_cpu_baseline(proc):
+    try:
+        out, err = proc.communicate(timeout=600)
+    except subprocess.TimeoutExpired:
+        proc.kill()
+        return {"error": "cpu baseline timed out"}
+    lines = [ln for ln in out.splitlines() if ln.startswith("{")]
+    if proc.returncode != 0 or not lines:
+        return {"error": f"cpu baseline exited {proc.returncode}: {err[-400:]}"}
+    return json.loads(lines[-1])
 
 
 def main():
     args = parse()
+    if args.cpu_child:
+        cpu_child(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus above 1 is not supported "
                           "(the path shards by sequence or by kv head with no exchange inside it; one "
                           "GPU's share is what is measured)", "n_gpus": args.gpus}))
         sys.exit(2)
+
+    # the CPU baseline's child starts before this process touches the GPU
+    cpu_proc = None if (args.no_cpu or args.suite) else start_cpu_baseline(args)
 
     import numpy as np
     import torch
@@ -199,12 +250,14 @@ def main():
     # appended rows (B x 2 rows)
     per_launch_bytes = attended * NKV * HD * 2 * 2 + (2 * B * 2 * rl * 2 if fused else 0)
     achieved = per_launch_bytes / (avg_ms / 1e3) / 1e9
+    # HBM traffic per call from the committed counter profile, used only when
+    # it was captured from these exact kernel and launcher sources
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_config2_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             tr = json.load(f)
-        if tr.get("kernel") == kname:
+        if tr.get("kernel") == kname and tr.get("source_sha256") == decode_source_digest():
             traffic = tr.get("hbm_bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -213,9 +266,7 @@ def main():
                 "avg_launch_us": round(avg_ms * 1e3, 2),
                 "algorithmic_bytes_per_launch": per_launch_bytes}
 
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(args, shape, tab, pools[0], qs[0], newk[0], newv[0])
+    cpu = finish_cpu_baseline(cpu_proc) if cpu_proc is not None else None
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -258,6 +309,20 @@ def graph_time_us(fn, iters=20, per_graph=20, stream=None):
         b.record(s)
     torch.cuda.synchronize()
     return a.elapsed_time(b) * 1e3 / (iters * per_graph)
+
+
+DECODE_SOURCES = ("titan_amd/csrc/kernels/paged_decode_tiles.hip", "titan_amd/csrc/engine_hip.cpp")
+
+
+def decode_source_digest():
+    """sha256 over the decode kernel and launcher sources (the GPU box has no
+    .git, so a content hash ties a counter profile to the code it measured)."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in DECODE_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
 
 
 def emit(d):
@@ -472,22 +537,37 @@ def suite(args, dev):
           "GB/s": round(b5 / us5 / 1e3, 1), "frac_of_8TB/s": round(b5 / us5 / 1e3 / 8000.0, 4),
           "kernel": PagedAttention.kernel_name(32, 8, 128, 16, KvDataType.F16)})
 
-def cpu_baseline(args, shape, tab, pool0, q0, k0, v0):
-    """Oracle append + sdpa_decode (single thread) on whole layer-steps of the
-    same workload, repeated until the time budget is spent."""
+def cpu_child(args):
+    """The CPU baseline itself (runs in the pinned child, never touches a GPU):
+    the oracle's restatement of the reference's single-threaded
+    PagedKvCache::append row copies + sdpa_decode (cache.rs:153-192,
+    forward_cpu.rs:424-510) on whole layer-steps of config 2 -- the same
+    contexts, tables and shapes as the GPU run, seeded N(0,1) values widened
+    exactly from f16 (untimed).  Each layer-step is timed on its own; at
+    least 5 are run (more while the time budget lasts, at most 64) and the
+    median is reported."""
     import numpy as np
 
     from oracle import orc
+    from titan_amd import synth
 
+    if os.environ.get("TITAN_CPU_PINNER") == "sched_setaffinity":
+        os.sched_setaffinity(0, {int(os.environ["TITAN_CPU_PIN"])})
+    shape = synth.config2(0, extra_tokens=1)
+    tab = synth.block_tables(shape, extra_tokens=1)
     B, NQ, NKV, HD, BT = shape.batch, shape.n_head, shape.n_head_kv, shape.head_dim, shape.block_tokens
     rl = shape.row_len
-    pool = pool0.float().cpu().numpy().copy()           # exact widening, untimed
-    q = q0.cpu().numpy()
-    kn, vn = k0.float().cpu().numpy(), v0.float().cpu().numpy()
-    lens = shape.ctx_lens.astype(np.int64)
+    rng = np.random.default_rng(1)
     page = BT * 2 * rl
-    n_layers, secs, kv_bytes = 0, 0.0, 0
-    while secs < args.cpu_seconds and n_layers < 64:
+    pool = rng.standard_normal(shape.n_blocks * page, dtype=np.float32).astype(np.float16)
+    pool = pool.astype(np.float32)                       # exact widening, untimed
+    q = rng.standard_normal((B, NQ, HD), dtype=np.float32)
+    kn = rng.standard_normal((B, rl), dtype=np.float32).astype(np.float16).astype(np.float32)
+    vn = rng.standard_normal((B, rl), dtype=np.float32).astype(np.float16).astype(np.float32)
+    lens = shape.ctx_lens.astype(np.int64)
+    times = []
+    total = 0.0
+    while len(times) < 64 and (len(times) < 5 or total < args.cpu_seconds):
         t0 = time.perf_counter()
         for b in range(B):                               # PagedKvCache::append row copies
             L_b = int(lens[b])
@@ -495,15 +575,23 @@ def cpu_baseline(args, shape, tab, pool0, q0, k0, v0):
             pool[base:base + rl] = kn[b]
             pool[base + rl:base + 2 * rl] = vn[b]
         orc.sdpa_decode_batched(pool, tab, (lens + 1).astype(np.uint32), BT, q, NQ, NKV, HD)
-        secs += time.perf_counter() - t0
-        kv_bytes += int((lens + 1).sum()) * NKV * HD * 2 * 2
-        n_layers += 1
-    return {"value": round(kv_bytes / secs / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"{n_layers} layer-steps of config 2 (32 sequences, append + decode over "
-                      f"the f32-widened pool), {secs:.1f} s on 1 thread of {cpu_model()} "
-                      f"({os.cpu_count()} logical CPUs visible)",
-            "tok_s": round(B * n_layers / 28 / secs, 3)}
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        total += dt
+    med = float(np.median(times))
+    kv_bytes = int((lens + 1).sum()) * NKV * HD * 2 * 2
+    pin = os.environ.get("TITAN_CPU_PIN", "?")
+    print(json.dumps({
+        "value": round(kv_bytes / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"config 2 layer-steps (32 sequences, {int((lens + 1).sum())} attended tokens: "
+                  f"append + sdpa_decode over the f32-widened pool), median of {len(times)} "
+                  f"({total:.1f} s), 1 thread pinned to CPU {pin} "
+                  f"({os.environ.get('TITAN_CPU_PINNER', '?')}) of {cpu_model()}, "
+                  f"{len(os.sched_getaffinity(0))} CPU(s) in the child's mask; the reference "
+                  f"path is single-threaded",
+        "median_layer_step_ms": round(med * 1e3, 2),
+        "median_step_ms_28_layers": round(med * 28e3, 1),
+        "tok_s": round(B / (28 * med), 3)}), flush=True)
 
 
 if __name__ == "__main__":

@@ -179,7 +179,13 @@ eh_status eh_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype
  * (pool element type) are written at position p = *pos_ptr (device) or
  * query_pos, then q attends tokens 0..p.  Pool bytes after the call equal
  * the append's, the output equals eh_flash_decoding's with seq_tokens = p + 1,
- * query_pos = p, causal.  16-bit and f32 pages; FP8 returns EH_UNSUPPORTED. */
+ * query_pos = p, causal.  16-bit and f32 pages; FP8 returns EH_UNSUPPORTED.
+ * Masked page: a host query_pos whose page lies past the table is
+ * EH_INVALID_SIZE.  With pos_ptr, a position whose table entry lies past the
+ * table or whose page id is >= the pool's pages is masked like every other
+ * token on such a page: the row is NOT written, the call returns EH_OK and q
+ * attends only the tokens on valid pages (the same masking eh_flash_decoding
+ * applies). */
 eh_status eh_append_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
                                    const void* keys, uint64_t keys_bytes, const void* values,
                                    uint64_t values_bytes, const float* q, uint64_t q_bytes,
@@ -288,7 +294,11 @@ uint64_t eh_decode_mass_workspace_bytes(uint32_t batch, uint32_t bt_stride, uint
  * the token-balanced kernel (eh_decode_plan with hint 0 returns
  * tokens_per_split 0; its max_splits is `grid` and its workspace size
  * applies); other shapes return EH_UNSUPPORTED.  The appended page must not
- * be read by another sequence of the same call (copy-on-write first). */
+ * be read by another sequence of the same call (copy-on-write first).
+ * Masked page: when start_pos[b] / block_tokens >= bt_stride, or the table
+ * entry is 0xFFFFFFFF or >= the pool's pages, row b is NOT written and q row
+ * b attends only the tokens on valid pages (EH_OK; eh_paged_decode_batched
+ * masks such pages the same way). */
 eh_status eh_append_decode_batched(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
                                    void* pool, uint64_t pool_bytes, const void* keys,
                                    uint64_t keys_bytes, const void* values, uint64_t values_bytes,

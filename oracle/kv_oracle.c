@@ -802,7 +802,7 @@ void orc_stream_prune_blocks(const orc_stream* m, const uint32_t* table, size_t 
     size_t max_blocks = orc_stream_max_active_blocks(m->cfg);
     *n_evicted = 0;
     if (n <= max_blocks) {
-        memcpy(retained, table, n * sizeof(uint32_t));
+        if (n) memcpy(retained, table, n * sizeof(uint32_t));  /* table may be NULL when n == 0 */
         *n_retained = n;
         return;
     }

@@ -10,7 +10,8 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liborc_kv.so")
+# TITAN_ORACLE_LIB selects another build (the sanitized one).
+_LIB_PATH = os.environ.get("TITAN_ORACLE_LIB") or os.path.join(_HERE, "liborc_kv.so")
 
 OK, POOL_EXHAUSTED, INVALID_ARGS = 0, 20, 21
 
@@ -453,3 +454,27 @@ class Streaming:
         lib().orc_stream_prune_blocks(self._h, _p(t), t.size, _p(r), C.byref(nr), _p(e),
                                       C.byref(ne))
         return [int(x) for x in r[:nr.value]], [int(x) for x in e[:ne.value]]
+
+
+def compaction_plan(block_tables, n_used, n_blocks):
+    """Gather-compaction plan, restated with sets (the product policy has no
+    reference counterpart: the copy step of a compaction is only sketched in
+    openspec/changes/archive/2026-08-28-agent-runtime-optimizations/
+    design.md:134-148).  Rule: with k live pages, every live page at or
+    above id k moves to a free id below k, the i-th smallest such page to
+    the i-th smallest hole.  Returns (src, dst, remap) like
+    titan_amd.share.compaction_plan."""
+    bt = np.asarray(block_tables, dtype=np.uint32)
+    live = set()
+    for b in range(bt.shape[0]):
+        live.update(int(p) for p in bt[b, :int(n_used[b])])
+    if any(p >= n_blocks for p in live):
+        raise ValueError("a live block-table entry is outside the pool")
+    k = len(live)
+    movers = sorted(p for p in live if p >= k)
+    holes = sorted(set(range(k)) - live)
+    assert len(movers) == len(holes)
+    remap = np.arange(n_blocks, dtype=np.uint32)
+    for p, h in zip(movers, holes):
+        remap[p] = h
+    return (np.array(movers, dtype=np.uint32), np.array(holes, dtype=np.uint32), remap)

@@ -189,3 +189,93 @@ def test_host_reserve_many_equals_repeated_single():
         p.reserve(s, 1000)
     assert e.value.kind == "PoolExhausted"
     assert p.table(s) == o.seq_block_table(s).tolist()
+
+
+def _seed(p, order):
+    o = np.ascontiguousarray(order, dtype=np.uint32)
+    check(p.L.eh_kvcache_seed_free_list(p.h, o.ctypes.data, o.size), host=True)
+
+
+def test_host_seed_free_list_rejects_unsafe_orders():
+    p = HostCache(8, 4, 1, 2)
+    for bad, msg in (([0, 1, 2, 3, 4, 5, 6, 6], "duplicate page id"),
+                     ([0, 1, 2, 3, 4, 5, 6], "order must list every free page exactly once"),
+                     ([0, 1, 2, 3, 4, 5, 6, 9], "page id out of range")):
+        with pytest.raises(KvCacheError) as e:
+            _seed(p, bad)
+        assert e.value.kind == "InvalidArgs" and e.value.msg == msg
+    assert p.L.eh_kvcache_blocks_used(p.h) == 0
+    _seed(p, [5, 3, 0, 1, 2, 4, 6, 7])
+    s = p.L.eh_kvcache_new_sequence(p.h)
+    p.reserve(s, 5)                              # pops pages 5 and 3
+    assert p.table(s) == [5, 3]
+    # a page a sequence holds cannot be seeded again (it would get two owners)
+    with pytest.raises(KvCacheError) as e:
+        _seed(p, [5, 0, 1, 2, 4, 6])
+    assert e.value.msg == "page is in use"
+    # a permutation of the pages that are still free is accepted
+    _seed(p, [7, 6, 4, 2, 1, 0])
+    t = p.L.eh_kvcache_new_sequence(p.h)
+    p.reserve(t, 9)
+    assert p.table(t) == [7, 6, 4]
+    assert p.L.eh_kvcache_blocks_used(p.h) == 5
+
+
+def test_host_reserve_batch_all_or_nothing():
+    nb, bt = 10, 4
+    p, q = HostCache(nb, bt, 1, 2), HostCache(nb, bt, 1, 2)
+    for c in (p, q):
+        for _ in range(4):
+            c.L.eh_kvcache_new_sequence(c.h)
+    lens = [3, 4, 0, 7]
+    for s, n in enumerate(lens):
+        p.reserve(s, n)
+        q.reserve(s, n)
+    seqs = np.array([0, 1, 2, 3], np.uint64)
+    starts = np.zeros(4, np.uint64)
+    ones = np.ones(4, np.uint64)
+    check(p.L.eh_kvcache_reserve_batch(p.h, seqs.ctypes.data, 4, ones.ctypes.data,
+                                       starts.ctypes.data), host=True)
+    assert starts.tolist() == lens
+    for s in range(4):                            # equals the single reserves in list order
+        q.reserve(s, 1)
+        assert p.table(s) == q.table(s)
+    # exhaustion mid-batch: pages left = 10 - 7 = 3; the batch of 5 tokens each needs more
+    used = p.L.eh_kvcache_blocks_used(p.h)
+    before = [(p.table(s), p.L.eh_kvcache_token_count(p.h, s)) for s in range(4)]
+    with pytest.raises(KvCacheError) as e:
+        fives = np.full(4, 5, np.uint64)
+        check(p.L.eh_kvcache_reserve_batch(p.h, seqs.ctypes.data, 4, fives.ctypes.data,
+                                           starts.ctypes.data), host=True)
+    assert e.value.kind == "PoolExhausted"
+    assert (e.value.blocks_used, e.value.blocks_total) == (used, nb)
+    assert [(p.table(s), p.L.eh_kvcache_token_count(p.h, s)) for s in range(4)] == before
+    assert p.L.eh_kvcache_blocks_used(p.h) == used
+    # an unknown or repeated sequence changes nothing either
+    for bad in ([0, 9], [1, 1]):
+        b = np.array(bad, np.uint64)
+        with pytest.raises(KvCacheError):
+            check(p.L.eh_kvcache_reserve_batch(p.h, b.ctypes.data, 2, ones.ctypes.data,
+                                               starts.ctypes.data), host=True)
+        assert [(p.table(s), p.L.eh_kvcache_token_count(p.h, s)) for s in range(4)] == before
+
+
+def test_host_truncate_restores_free_list_order():
+    p, q = HostCache(12, 4, 1, 2), HostCache(12, 4, 1, 2)
+    for c in (p, q):
+        _seed(c, [3, 9, 1, 0, 11, 2, 5, 4, 6, 7, 8, 10])
+        for _ in range(2):
+            c.L.eh_kvcache_new_sequence(c.h)
+        c.reserve(0, 6)
+    p.reserve(1, 9)                               # pops 1, 0, 11
+    assert p.table(1) == [1, 0, 11]
+    check(p.L.eh_kvcache_truncate(p.h, 1, 0), host=True)
+    p.reserve(0, 3)                               # 6 -> 9 tokens: pops 1 again
+    q.reserve(0, 3)
+    assert p.table(0) == q.table(0) == [3, 9, 1]
+    p.reserve(1, 5)
+    q.reserve(1, 5)
+    assert p.table(1) == q.table(1) == [0, 11]
+    assert p.L.eh_kvcache_truncate(p.h, 0, 10) == 21    # past the count
+    check(p.L.eh_kvcache_truncate(p.h, 0, 5), host=True)
+    assert p.table(0) == [3, 9] and p.L.eh_kvcache_token_count(p.h, 0) == 5

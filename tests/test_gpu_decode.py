@@ -1,7 +1,8 @@
 """GPU parity of paged decode attention against the oracle's sdpa_decode.
 
 Tolerances (stated by the benchmark contract): f32 KV max-abs 1e-5; f16/bf16
-KV with f32 accumulation |gpu - ref| <= 2e-3 + 1e-3*|ref|.  The oracle runs
+KV with f32 accumulation max-abs <= 2e-3 and
+|gpu - ref| <= 2e-3 + 1e-3*|ref| (tests/parity.py).  The oracle runs
 on the exactly widened f32 pool.  Shapes follow the reference's own tests
 (engine-cuda/tests/paged_attention_gpu.rs, paged_attention_parity.rs,
 graph_dynamic_params_test.rs) plus the five benchmark configurations.
@@ -14,6 +15,8 @@ from oracle import orc
 from titan_amd import HipError, KvDataType, PagedAttention, PagedKvGpu, PagedKvLayout
 from titan_amd import synth
 
+import parity
+
 pytestmark = pytest.mark.gpu
 
 TD = {KvDataType.F32: torch.float32, KvDataType.F16: torch.float16,
@@ -24,15 +27,8 @@ def i32(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev)
 
 
-def check_close(gpu, ref, dtype):
-    gpu, ref = np.asarray(gpu, np.float64), np.asarray(ref, np.float64)
-    assert np.all(np.isfinite(gpu))
-    if dtype == KvDataType.F32:
-        err = np.max(np.abs(gpu - ref))
-        assert err <= 1e-5, f"max abs err {err}"
-    else:
-        bad = np.abs(gpu - ref) > 2e-3 + 1e-3 * np.abs(ref)
-        assert not bad.any(), f"max abs err {np.max(np.abs(gpu - ref))}"
+def check_close(gpu, ref, dtype, what=""):
+    parity.check_close(gpu, ref, f32=dtype == KvDataType.F32, what=what or KvDataType(dtype).name)
 
 
 def cosine(a, b):
@@ -471,3 +467,61 @@ def test_fused_step_errors(dev):
     pa.append_flash_decoding(None, k, k, q, pool, table, out, n_head, n_kv, hd, bt, nb * bt - 1)
     torch.cuda.synchronize()
     assert torch.all(torch.isfinite(out))
+
+
+def test_graph_replay_split_count_follows_device_position(dev):
+    """The reference sizes its split grid on the host from seq_tokens and
+    freezes it at capture (forward_driver.rs:2230-2243), and drops tokens
+    past 8192 (paged_attention.cu:244-247).  Here append(pos_ptr) +
+    flash_decoding(pos_ptr) are captured once over a 12288-token block table
+    and replayed at device positions that cross split boundaries and 8192;
+    every replay must equal sdpa_decode over tokens 0..pos (f32, 1e-5) and
+    write its row (graph_dynamic_params_test.rs:17-229 pattern)."""
+    n_head, n_kv, hd, bt, cap = 14, 2, 64, 16, 12288
+    rl = n_kv * hd
+    n_pages = cap // bt
+    nb = n_pages + 5
+    rng = np.random.default_rng(8192)
+    table_h = rng.permutation(nb)[:n_pages].astype(np.uint32)
+    layout = PagedKvLayout(nb, bt, rl)
+    host = rng.standard_normal(layout.floats_total()).astype(np.float32)
+    pool = torch.from_numpy(host).to(dev)
+    table = i32(table_h, dev)
+    kv, pa = PagedKvGpu(0), PagedAttention(0)
+    k = torch.empty(rl, device=dev)
+    v = torch.empty(rl, device=dev)
+    q = torch.empty(n_head * hd, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = torch.empty(n_head * hd, device=dev)
+    kv.append_kv_with_pos_ptr(None, layout, pool, k, v, table, 0, 1, pos)   # warm-up
+    pa.launch_flash_decoding(None, q, pool, table, out, n_head, n_kv, hd, bt, 1, 0, True, pos)
+    torch.cuda.synchronize()
+    pool.copy_(torch.from_numpy(host))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            kv.append_kv_with_pos_ptr(s, layout, pool, k, v, table, 0, 1, pos)
+            pa.launch_flash_decoding(s, q, pool, table, out, n_head, n_kv, hd, bt, 1, 0, True,
+                                     pos)
+    torch.cuda.synchronize()
+    page = bt * 2 * rl
+    for p in (0, 255, 256, 4095, 8191, 8192, 12287, 100):
+        kn = rng.standard_normal(rl).astype(np.float32)
+        vn = rng.standard_normal(rl).astype(np.float32)
+        qn = rng.standard_normal(n_head * hd).astype(np.float32)
+        k.copy_(torch.from_numpy(kn))
+        v.copy_(torch.from_numpy(vn))
+        q.copy_(torch.from_numpy(qn))
+        pos.fill_(p)
+        torch.cuda.synchronize()
+        print(f"[replay] position {p}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        base = int(table_h[p // bt]) * page + (p % bt) * 2 * rl
+        host[base:base + rl] = kn
+        host[base + rl:base + 2 * rl] = vn
+        assert np.array_equal(pool.cpu().numpy(), host), f"pool after replay at {p}"
+        ref = orc.sdpa_decode(host, table_h, bt, p + 1, qn, n_head, n_kv, hd, True, p)
+        check_close(out.cpu().numpy(), ref, KvDataType.F32, what=f"replay pos {p}")

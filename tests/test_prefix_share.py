@@ -18,10 +18,23 @@ from titan_amd.prefix_share import PrefixShareScenario, model_pool, run_on_gpu
 
 def _plan(seed, backend, **kw):
     if backend == "oracle":
-        scn = PrefixShareScenario(seed, cow_cls=orc.Cow, radix_cls=orc.Radix, **kw)
+        scn = PrefixShareScenario(seed, cow_cls=orc.Cow, radix_cls=orc.Radix,
+                                  compaction_plan=orc.compaction_plan, **kw)
     else:
         scn = PrefixShareScenario(seed, **kw)
     return scn, scn.plan()
+
+
+def _assert_same_plan(a, b):
+    assert a.n_blocks == b.n_blocks
+    assert a.cow_pairs == b.cow_pairs and a.cow_pairs > 0
+    assert a.victims == b.victims
+    assert a.evicted_seqs == b.evicted_seqs
+    assert a.tables == b.tables and a.compacted == b.compacted
+    assert a.strong_counts == b.strong_counts
+    assert np.array_equal(a.remap, b.remap)
+    assert np.array_equal(a.compaction.src, b.compaction.src)
+    assert np.array_equal(a.compaction.dst, b.compaction.dst)
 
 
 @pytest.mark.parametrize("seed", [0, 1])
@@ -29,12 +42,7 @@ def test_config4_bookkeeping_matches_oracle(seed):
     kw = dict(n_seqs=64, head_dim=8, n_kv=1)    # full config-4 page counts, tiny rows
     _, a = _plan(seed, "product", **kw)
     _, b = _plan(seed, "oracle", **kw)
-    assert a.cow_pairs == b.cow_pairs and a.cow_pairs > 0
-    assert a.victims == b.victims
-    assert a.evicted_seqs == b.evicted_seqs
-    assert a.tables == b.tables and a.compacted == b.compacted
-    assert a.strong_counts == b.strong_counts
-    assert np.array_equal(a.remap, b.remap)
+    _assert_same_plan(a, b)
     # >= 25 % of the live pages were freed, pinned prefix pages never
     assert len(a.victims) >= 0.25 * a.live_before_evict
     prefix_pages = set(next(iter(a.tables.values()))[:64])
@@ -47,12 +55,43 @@ def test_config4_bookkeeping_matches_oracle(seed):
         assert c == (len(a.tables) if p in {a.remap[q] for q in prefix_pages} else 1)
 
 
+def test_config4_plan_independent_of_row_size():
+    # the eviction touch order has its own generator: the bookkeeping of the
+    # full-size rows equals that of the tiny rows the CPU test compares
+    _, a = _plan(3, "product", n_seqs=16, head_dim=8, n_kv=1)
+    _, b = _plan(3, "product", n_seqs=16, head_dim=32, n_kv=2)
+    _assert_same_plan(a, b)
+
+
+def test_oracle_compaction_plan_matches_product():
+    from titan_amd.share import compaction_plan
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        nb = int(rng.integers(1, 200))
+        B = int(rng.integers(1, 8))
+        stride = int(rng.integers(1, 30))
+        tab = rng.integers(0, nb, size=(B, stride)).astype(np.uint32)
+        used = rng.integers(0, stride + 1, size=B).astype(np.uint32)
+        a, b = compaction_plan(tab, used, nb), orc.compaction_plan(tab, used, nb)
+        for x, y in zip(a, b):
+            assert np.array_equal(x, y)
+
+
 @pytest.mark.gpu
-def test_config4_page_moves_bit_exact(dev):
+@pytest.mark.parametrize("seed", [0, 1])
+def test_config4_page_moves_bit_exact(dev, seed):
     import torch
 
     from titan_amd import PagedKvGpu
-    scn, plan = _plan(0, "product")
+    scn, plan = _plan(seed, "product")
+    # config 4 at its real size (64 sequences, 8 kv heads, hd 128): the plan
+    # the GPU executes equals the one the oracle's CoW / radix restatements
+    # and compaction rule produce on the same seed
+    _, oplan = _plan(seed, "oracle", n_seqs=64, head_dim=128, n_kv=8)
+    _assert_same_plan(plan, oplan)
+    print(f"config4 seed {seed}: {len(plan.victims)} victims of {plan.live_before_evict} live "
+          f"pages, {plan.cow_pairs} CoW copies, {len(plan.compaction.src)} compaction moves",
+          flush=True)
     pool, tables, counts, layout = run_on_gpu(scn, plan)
     # block tables after remap
     got = tables.cpu().numpy().view(np.uint32)

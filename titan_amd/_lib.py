@@ -9,7 +9,9 @@ import os
 import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libengine_hip.so")
+# TITAN_AMD_HOST_LIB selects another build of the host library (the sanitized
+# one of `python -m titan_amd.build --sanitize`); the code objects stay in LIB_DIR.
+LIB_PATH = os.environ.get("TITAN_AMD_HOST_LIB") or os.path.join(LIB_DIR, "libengine_hip.so")
 
 _lock = threading.Lock()
 _lib = None
@@ -87,6 +89,8 @@ _SIGS = {
     "eh_kvcache_token_count": (u64, [vp, u64]),
     "eh_kvcache_block_table": (i64, [vp, u64, vp, u64]),
     "eh_kvcache_reserve": (i32, [vp, u64, u64, P(u64)]),
+    "eh_kvcache_reserve_batch": (i32, [vp, vp, u64, vp, vp]),
+    "eh_kvcache_truncate": (i32, [vp, u64, u64]),
     "eh_kvcache_export_tables": (i32, [vp, vp, u64, vp, u64, vp]),
     # prefix sharing (kv_share.h)
     "eh_cow_new": (vp, []),

@@ -67,29 +67,68 @@ def _run_parallel(cmds, verbose):
         raise RuntimeError("build failed:\n" + msg)
 
 
-def build(verbose=False):
+HOST_SOURCES = ("engine_hip.cpp", "kv_host.cpp", "kv_share.cpp")
+SANITIZE = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-fno-sanitize-recover=undefined"]
+
+
+def _host_cmd(out, extra=()):
+    """g++ line of the C-ABI host library (no device code in these sources)."""
+    return [
+        "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
+        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", *extra,
+        *(os.path.join(CSRC, f) for f in HOST_SOURCES),
+        "-o", out, f"-L{ROCM}/lib", "-lamdhip64", "-ldl", f"-Wl,-rpath,{ROCM}/lib",
+    ]
+
+
+def build(verbose=False, host_only=False):
     os.makedirs(LIB, exist_ok=True)
     hipcc = _hipcc()
     cmds = []
-    for name, srcname, defs in KERNELS:
+    kernels = [] if host_only else KERNELS
+    for name, srcname, defs in kernels:
         src = os.path.join(CSRC, "kernels", srcname + ".hip")
         out = os.path.join(LIB, name + ".hsaco")
         cmds.append((name, [hipcc, *HIP_DEVICE_FLAGS, *defs, src, "-o", out + ".tmp"]))
     host_out = os.path.join(LIB, "libengine_hip.so")
-    cmds.append(("libengine_hip", [
-        "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
-        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
-        os.path.join(CSRC, "engine_hip.cpp"), os.path.join(CSRC, "kv_host.cpp"),
-        os.path.join(CSRC, "kv_share.cpp"),
-        "-o", host_out + ".tmp", f"-L{ROCM}/lib", "-lamdhip64", "-ldl",
-        f"-Wl,-rpath,{ROCM}/lib",
-    ]))
+    cmds.append(("libengine_hip", _host_cmd(host_out + ".tmp")))
     _run_parallel(cmds, verbose)
-    for name, _, _ in KERNELS:
+    for name, _, _ in kernels:
         out = os.path.join(LIB, name + ".hsaco")
         os.replace(out + ".tmp", out)
     os.replace(host_out + ".tmp", host_out)
     return LIB
+
+
+def sanitize_check(pytest_args=("-x", "-q", "-m", "not gpu")):
+    """Builds the host library (kv_host.cpp, kv_share.cpp, engine_hip.cpp) and
+    the CPU oracle with AddressSanitizer + UndefinedBehaviorSanitizer into
+    _build/sanitize/ and runs the CPU test suite against those builds (the
+    GPU kernels are not involved).  Returns pytest's exit status."""
+    out_dir = os.path.join(ROOT, "_build", "sanitize")
+    os.makedirs(out_dir, exist_ok=True)
+    host = os.path.join(out_dir, "libengine_hip.so")
+    orc = os.path.join(out_dir, "liborc_kv.so")
+    _run_parallel([
+        ("libengine_hip (sanitized)", _host_cmd(host, SANITIZE)),
+        ("liborc_kv (sanitized)", ["gcc", "-O1", "-ffp-contract=off", "-fno-fast-math", "-fPIC",
+                                   "-std=c11", "-Wall", "-Wextra", *SANITIZE, "-shared", "-o", orc,
+                                   os.path.join(ROOT, "oracle", "kv_oracle.c"), "-lm"]),
+    ], verbose=True)
+    preload = [subprocess.run(["gcc", f"-print-file-name={n}"], capture_output=True,
+                              text=True).stdout.strip() for n in ("libasan.so", "libubsan.so")]
+    env = dict(os.environ)
+    env.update({
+        "TITAN_AMD_HOST_LIB": host, "TITAN_ORACLE_LIB": orc,
+        "LD_PRELOAD": " ".join(preload),
+        # the interpreter itself is not instrumented: only report errors of
+        # the instrumented libraries, not Python's own allocations at exit
+        "ASAN_OPTIONS": "detect_leaks=0:abort_on_error=1",
+        "UBSAN_OPTIONS": "print_stacktrace=1:halt_on_error=1",
+    })
+    cmd = [sys.executable, "-m", "pytest", os.path.join(ROOT, "tests"), *pytest_args]
+    print("[sanitize]", " ".join(cmd), flush=True)
+    return subprocess.run(cmd, env=env, cwd=ROOT).returncode
 
 
 def build_oracle(verbose=False):
@@ -100,6 +139,8 @@ def build_oracle(verbose=False):
 
 
 if __name__ == "__main__":
-    build(verbose="-v" in sys.argv)
+    if "--sanitize" in sys.argv:
+        sys.exit(sanitize_check())
+    build(verbose="-v" in sys.argv, host_only="--host" in sys.argv)
     build_oracle(verbose="-v" in sys.argv)
     print("built", LIB)

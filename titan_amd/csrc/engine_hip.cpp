@@ -936,8 +936,10 @@ eh_status eh_append_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_
     const uint64_t row = n_head_kv * head_dim * elt_bytes(kv_dtype);
     if (keys_bytes < row) return invalid_size(row, keys_bytes);
     if (values_bytes < row) return invalid_size(row, values_bytes);
-    // a host-known position must have its page (paged_kv.rs:240-271 checks
-    // the table for the appended range)
+    // A host-known position must have its page in the table.  This is
+    // stricter than the reference, whose append only rejects an empty table
+    // (paged_kv.rs:262-267); a device position is checked in the kernel,
+    // where a page past the table or the pool is masked (row not written).
     if (!pos_ptr && block_tokens && query_pos / block_tokens >= bt_bytes / 4)
         return invalid_size((query_pos / block_tokens + 1) * 4, bt_bytes, "block_table");
     return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,

@@ -14,8 +14,10 @@
 //     rows of a tile are (query token, q head of the GQA group) pairs, so one
 //     K/V tile in LDS serves every q head of the group;
 //   * K/V tiles of N keys are gathered through the block table into LDS,
-//     K row-major and V transposed, double-buffered: the global loads of the
-//     next tile are in flight while MFMAs consume the current one;
+//     K and V both row-major (padded rows), double-buffered: the global loads
+//     of the next tile are in flight while MFMAs consume the current one; the
+//     V^T operand of P.V is read from the row-major V tile with the gfx950
+//     transposed LDS read ds_read_b64_tr_b16;
 //   * each wave owns 32 rows: S^T = K Q^T on 32x32 MFMA tiles, online softmax
 //     in the log2 domain on the accumulator registers (the S^T layout puts one
 //     query row per lane column, so row statistics stay lane-local up to one

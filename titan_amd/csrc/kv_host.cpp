@@ -65,9 +65,22 @@ eh_status eh_kvcache_new(uint64_t n_blocks, uint64_t block_tokens, uint64_t head
 void eh_kvcache_destroy(eh_kvcache* c) { delete c; }
 
 eh_status eh_kvcache_seed_free_list(eh_kvcache* c, const uint32_t* order, uint64_t n) {
-    // Extension: successive pops return order[0], order[1], ...
-    for (uint64_t i = 0; i < n; ++i)
-        if (order[i] >= c->n_blocks) return invalid("page id out of range");
+    // Extension: successive pops return order[0], order[1], ...  The order
+    // must be a permutation of the pages that are free now (all of them
+    // while no page is in use): a duplicate or a page some sequence holds
+    // would hand one physical page to two owners.
+    if (!c) return invalid("cache is null");
+    if (n != c->free_list.size()) return invalid("order must list every free page exactly once");
+    if (n && !order) return invalid("order is null");
+    std::vector<uint8_t> is_free(c->n_blocks, 0), seen(c->n_blocks, 0);
+    for (uint32_t p : c->free_list) is_free[p] = 1;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t p = order[i];
+        if (p >= c->n_blocks) return invalid("page id out of range");
+        if (seen[p]) return invalid("duplicate page id");
+        if (!is_free[p]) return invalid("page is in use");
+        seen[p] = 1;
+    }
     c->free_list.assign(order, order + n);
     std::vector<uint32_t> rev(c->free_list.rbegin(), c->free_list.rend());
     c->free_list.swap(rev);
@@ -128,6 +141,58 @@ eh_status eh_kvcache_reserve(eh_kvcache* c, uint64_t seq, uint64_t n_tokens, uin
     }
     if (start_pos) *start_pos = pos;
     c->tokens[seq] = pos + n_tokens;
+    return EH_OK;
+}
+
+eh_status eh_kvcache_reserve_batch(eh_kvcache* c, const uint64_t* seqs, uint64_t n_seqs,
+                                   const uint64_t* n_tokens, uint64_t* start_pos) {
+    // eh_kvcache_reserve of n_tokens[i] for every listed sequence, all or
+    // nothing: the pages the whole batch needs are counted first; on
+    // PoolExhausted (or an unknown / repeated sequence) no count and no table
+    // changes.  Pages are popped in list order, as repeated single reserves
+    // would pop them.
+    if (!c) return invalid("cache is null");
+    if (n_seqs && (!seqs || !n_tokens)) return invalid("seqs / n_tokens is null");
+    const uint64_t bt = c->block_tokens;
+    uint64_t fresh = 0;
+    std::vector<uint8_t> seen(c->tables.size(), 0);
+    for (uint64_t i = 0; i < n_seqs; ++i) {
+        const uint64_t s = seqs[i];
+        if (s >= c->tables.size()) return invalid("unknown sequence id");
+        if (seen[s]) return invalid("sequence listed twice");
+        seen[s] = 1;
+        const uint64_t need = (c->tokens[s] + n_tokens[i] + bt - 1) / bt;
+        const uint64_t have = c->tables[s].size();
+        fresh += need > have ? need - have : 0;
+    }
+    if (fresh > c->free_list.size()) {
+        g_used = eh_kvcache_blocks_used(c);
+        g_total = c->n_blocks;
+        g_msg = "pool exhausted";
+        return EH_POOL_EXHAUSTED;
+    }
+    for (uint64_t i = 0; i < n_seqs; ++i) {
+        const eh_status st = eh_kvcache_reserve(c, seqs[i], n_tokens[i], start_pos ? start_pos + i : nullptr);
+        if (st != EH_OK) return st;  // cannot happen: checked above
+    }
+    return EH_OK;
+}
+
+eh_status eh_kvcache_truncate(eh_kvcache* c, uint64_t seq, uint64_t n_tokens) {
+    // Undo of eh_kvcache_reserve: the count drops to n_tokens and the pages
+    // past ceil(n_tokens / block_tokens) go back on the free list in reverse,
+    // so the free list is again what it was before they were popped (the
+    // return order of cache.rs:131).  Page bytes are left as they are.
+    if (!c) return invalid("cache is null");
+    if (seq >= c->tables.size()) return invalid("unknown sequence id");
+    if (n_tokens > c->tokens[seq]) return invalid("truncate past the token count");
+    auto& t = c->tables[seq];
+    const uint64_t keep = (n_tokens + c->block_tokens - 1) / c->block_tokens;
+    while (t.size() > keep) {
+        c->free_list.push_back(t.back());
+        t.pop_back();
+    }
+    c->tokens[seq] = n_tokens;
     return EH_OK;
 }
 

@@ -121,14 +121,30 @@ class PagedKvCache:
         bt = self.seq_block_table(seq)
         return torch.tensor(bt if bt else [0], dtype=torch.int32, device=self.device)
 
+    def truncate(self, seq, n_tokens):
+        """Extension: roll a reservation back to n_tokens; the released pages
+        return to the free list in the order they were popped from."""
+        check(self._L.eh_kvcache_truncate(self._h, int(seq), int(n_tokens)), host=True)
+
     def append(self, seq, key, value, stream=None):
-        """cache.rs:153-192: one token's K and V rows."""
+        """cache.rs:153-192: one token's K and V rows.  All or nothing, as the
+        reference: the row lengths and the sequence are checked first
+        (same order, same messages); if the launch fails after the page
+        was reserved, the reservation is rolled back before the error
+        propagates."""
         k, v = self._row_tensor(key), self._row_tensor(value)
         m = self._cfg.row_len()
         if k.numel() != m or v.numel() != m:
             raise KvCacheError("InvalidArgs", "key/value length must equal heads * head_dim")
+        if seq >= self.sequences():
+            raise KvCacheError("InvalidArgs", "unknown sequence id")
+        before = self.token_count(seq)
         pos = self.reserve(seq, 1)
-        self._kv.append_kv(stream, self.layout, self.pool, k, v, self._table_dev(seq), pos, 1)
+        try:
+            self._kv.append_kv(stream, self.layout, self.pool, k, v, self._table_dev(seq), pos, 1)
+        except BaseException:
+            self.truncate(seq, before)
+            raise
 
     def _read(self, seq, start, n, is_value, stream=None):
         out = torch.empty(max(n, 1) * self._cfg.row_len(), dtype=TORCH_DTYPE[self.dtype],
@@ -180,14 +196,71 @@ class PagedKvCache:
         return (torch.from_numpy(tab.view(np.int32)).to(self.device),
                 torch.from_numpy(lens.view(np.int32)).to(self.device))
 
-    def append_batch(self, seqs, keys, values, stream=None, stride=None):
-        """Append one token to every sequence in `seqs` with one kernel launch.
-        keys/values: [len(seqs), row_len] device tensors in the pool dtype."""
-        starts = [self.reserve(int(s), 1) for s in seqs]
-        tables, _ = self.block_tables(seqs, stride)
+    def reserve_batch(self, seqs, counts):
+        """Extension: reserve counts[i] tokens for seqs[i], all or nothing
+        (PoolExhausted leaves every sequence unchanged); returns the first
+        new position of each sequence."""
+        seqs_a = np.ascontiguousarray([int(s) for s in seqs], dtype=np.uint64)
+        cnt = np.ascontiguousarray([int(n) for n in counts], dtype=np.uint64)
+        if cnt.size != seqs_a.size:
+            raise KvCacheError("InvalidArgs", "one count per sequence")
+        starts = np.zeros(max(seqs_a.size, 1), dtype=np.uint64)
+        check(self._L.eh_kvcache_reserve_batch(self._h, seqs_a.ctypes.data, seqs_a.size,
+                                               cnt.ctypes.data, starts.ctypes.data), host=True)
+        return starts[:seqs_a.size].astype(np.int64)
+
+    def extend_batch(self, seqs, counts, keys, values, stream=None, stride=None):
+        """Append counts[i] tokens to seqs[i] for every listed sequence with one
+        kernel launch (a ragged batch: prompt prefill, or one token each at
+        decode).  keys/values: [sum(counts), row_len] device tensors in the
+        pool dtype, sequence by sequence.  Returns (device block tables
+        [B, stride], device start positions [B] int32, host token counts
+        after the append).
+
+        All or nothing: shapes, dtype, device and the table stride are checked
+        before any page is reserved; the batch's pages are reserved in one
+        step (PoolExhausted leaves every sequence unchanged); a failed launch
+        rolls every reservation back."""
         B = len(seqs)
-        cu = torch.arange(B + 1, dtype=torch.int32, device=self.device)
-        sp = torch.tensor(starts, dtype=torch.int32, device=self.device)
-        self._kv.append_kv_batched(stream, self.layout, self.pool, keys.contiguous(),
-                                   values.contiguous(), tables, cu, sp, B)
-        return tables
+        counts = [int(n) for n in counts]
+        if len(counts) != B:
+            raise KvCacheError("InvalidArgs", "one count per sequence")
+        m = self._cfg.row_len()
+        total = sum(counts)
+        want = TORCH_DTYPE[self.dtype]
+        for t in (keys, values):
+            if tuple(t.shape) != (total, m):
+                raise KvCacheError("InvalidArgs", "key/value length must equal heads * head_dim")
+            if t.dtype != want or t.device != self.device:
+                raise KvCacheError("InvalidArgs", "keys/values must be pool-dtype tensors on the "
+                                                  "pool's device")
+        for s in seqs:
+            if int(s) >= self.sequences():
+                raise KvCacheError("InvalidArgs", "unknown sequence id")
+        before = [self.token_count(int(s)) for s in seqs]
+        bt = self._cfg.block_tokens
+        need = max([(n + c + bt - 1) // bt for n, c in zip(before, counts)] or [1])
+        if stride is None:
+            stride = max(1, need)
+        elif stride < need:
+            raise KvCacheError("InvalidArgs", "stride shorter than a block table")
+        starts = self.reserve_batch(seqs, counts)
+        try:
+            tables, _ = self.block_tables(seqs, stride)
+            cu = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32))
+            sp = torch.from_numpy(starts.astype(np.int32)).to(self.device)
+            if total:
+                self._kv.append_kv_batched(stream, self.layout, self.pool, keys.contiguous(),
+                                           values.contiguous(), tables, cu.to(self.device), sp,
+                                           total)
+        except BaseException:
+            for s, n in reversed(list(zip(seqs, before))):
+                self.truncate(int(s), n)
+            raise
+        return tables, sp, [n + c for n, c in zip(before, counts)]
+
+    def append_batch(self, seqs, keys, values, stream=None, stride=None):
+        """Append one token to every sequence in `seqs` with one kernel launch
+        (extend_batch with a count of 1 each; same all-or-nothing rule).
+        keys/values: [len(seqs), row_len] device tensors in the pool dtype."""
+        return self.extend_batch(seqs, [1] * len(seqs), keys, values, stream, stride)

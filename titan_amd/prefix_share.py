@@ -82,6 +82,11 @@ class PrefixShareScenario:
             compaction_plan = compaction_plan or cp
         self.cow_cls, self.radix_cls, self.compaction_plan = cow_cls, radix_cls, compaction_plan
         self.rng = np.random.default_rng(seed)
+        # The touch order that drives LRU eviction has a generator of its own,
+        # created before any row is drawn: the plan (victims, tables, remap)
+        # then depends on the seed and the page counts only, not on how many
+        # random values the rows consumed (row_len).
+        self.touch_rng = np.random.default_rng([seed, 0x70C4])
         self.n_seqs, self.prefix_tokens, self.append = n_seqs, prefix_tokens, append
         self.n_kv, self.head_dim, self.bt = n_kv, head_dim, block_tokens
         self.row_len = n_kv * head_dim
@@ -179,7 +184,7 @@ class PrefixShareScenario:
             n_tok = self.prefix_tokens + int(self.suffix[s]) + self.append
             tok[s] = pre_tokens + [1_000_000 + s * 10_000 + i for i in range(n_tok - self.prefix_tokens)]
             radix.insert(tok[s], cids[s], False)
-        for s in self.rng.permutation(self.n_seqs):
+        for s in self.touch_rng.permutation(self.n_seqs):
             m, blk = _match(radix, tok[int(s)])
             assert m == len(tok[int(s)]) and blk == cids[int(s)]
         target = int(np.ceil(self.evict_frac * len(live)))
