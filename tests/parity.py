@@ -30,14 +30,20 @@ def _record(what, gpu, ref):
     return d, max_abs
 
 
-def check_close(gpu, ref, f32=False, what=""):
+def check_close(gpu, ref, f32=False, what="", stress=False):
+    """`stress`: inputs deliberately far outside the contract's N(0,1) data
+    (every E4M3 code, |V| up to ~20): only the per-element bound
+    2e-3 + 1e-3 * |ref| applies there, since a 2e-3 absolute bar on outputs
+    of magnitude ~20 would demand more than the 11-bit precision of the f16
+    softmax weights."""
     gpu, ref = np.asarray(gpu, np.float64), np.asarray(ref, np.float64)
     assert gpu.shape == ref.shape, f"{what}: shape {gpu.shape} vs {ref.shape}"
     assert np.all(np.isfinite(gpu)), f"{what}: non-finite output"
-    d, max_abs = _record(what, gpu, ref)
+    d, max_abs = _record(what + (" [stress]" if stress else ""), gpu, ref)
     if f32:
         assert max_abs <= ABS_F32, f"{what}: max abs err {max_abs}"
         return
-    assert max_abs <= ABS_16, f"{what}: max abs err {max_abs} at {np.argwhere(d > ABS_16)[:4]}"
+    if not stress:
+        assert max_abs <= ABS_16, f"{what}: max abs err {max_abs} at {np.argwhere(d > ABS_16)[:4]}"
     bad = d > ABS_16 + REL_16 * np.abs(ref)
     assert not bad.any(), f"{what}: max abs err {max_abs} at {np.argwhere(bad)[:4]}"

@@ -3,9 +3,11 @@ gather and the token-balanced decode over an E4M3 pool, against the oracle's
 E4M3 restatement (tests/test_oracle_fp8.py pins it).
 
 Bars: append and gather bit-exact (codes; dequantised f32 bits, NaN where the
-code is NaN); decode max-abs <= 2e-3 and
+code is NaN); decode over quantised N(0,1) K/V (scale max|x| / 448, as a
+quantiser stores the contract's data) max-abs <= 2e-3 and
 |gpu - ref| <= 2e-3 + 1e-3*|ref| (tests/parity.py) against sdpa_decode on
-the dequantised pool (decode(code) * scale); and the acceptance of the
+the dequantised pool (decode(code) * scale); decode over every code (|x| up
+to ~22, a stress case) the per-element bound only; and the acceptance of the
 reference's FP8 KV spec (openspec/archive/2026-08-28-fp8-kv-cache-quantization/
 specs/kv-compression/spec.md:12-15): cosine similarity >= 0.999 between the
 E4M3 attention output and the f16 one on the same K/V.
@@ -18,6 +20,7 @@ from oracle import orc
 from titan_amd import KvDataType, PagedAttention, PagedKvGpu, PagedKvLayout
 
 import parity
+from e4m3_data import all_codes, gauss_codes
 
 pytestmark = pytest.mark.gpu
 
@@ -116,14 +119,11 @@ def test_e4m3_gather_all_codes(dev):
         assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
 
 
-def run_decode_e4m3(dev, lens, shape, seed, grid=None):
+def run_decode_e4m3(dev, lens, shape, seed, grid=None, data="gauss"):
     n_head, n_kv, hd, bt = shape
     rng = np.random.default_rng(seed)
     tab, nb = make_tables(rng, lens, bt)
-    codes = rng.integers(0, 256, nb * bt * 2 * n_kv * hd).astype(np.uint8)
-    codes[(codes & 0x7F) == 0x7F] = 0x3C             # no NaN codes in the pool
-    ks = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
-    vs = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
+    codes, ks, vs = (gauss_codes if data == "gauss" else all_codes)(rng, nb, bt, n_kv, hd)
     B = len(lens)
     q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
     plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(max(lens)), 0, KvDataType.FP8)
@@ -143,8 +143,8 @@ def run_decode_e4m3(dev, lens, shape, seed, grid=None):
     return out.cpu().numpy(), ref
 
 
-def check_close(gpu, ref, what="e4m3"):
-    parity.check_close(gpu, ref, what=what)
+def check_close(gpu, ref, what="e4m3", stress=False):
+    parity.check_close(gpu, ref, what=what, stress=stress)
 
 
 @pytest.mark.parametrize("shape", [(12, 2, 128, 16), (32, 8, 128, 16), (8, 1, 128, 32),
@@ -154,6 +154,16 @@ def test_e4m3_decode_matches_sdpa(dev, shape):
     lens = np.array([0, 1, 15, 16, 17, 300, 2049, 0, 33, 1000, 7], np.int64)
     out, ref = run_decode_e4m3(dev, lens, shape, 40 + sum(shape))
     check_close(out, ref)
+
+
+@pytest.mark.parametrize("shape", [(12, 2, 128, 16), (32, 8, 128, 16)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_e4m3_decode_all_codes_stress(dev, shape):
+    """Every E4M3 code (random scales, |K|, |V| up to ~22): outputs of
+    magnitude up to ~20, checked with the per-element bound."""
+    lens = np.array([0, 1, 15, 16, 17, 300, 2049, 0, 33, 1000, 7], np.int64)
+    out, ref = run_decode_e4m3(dev, lens, shape, 40 + sum(shape), data="codes")
+    check_close(out, ref, stress=True)
 
 
 @pytest.mark.parametrize("grid", [1, 3, 64])
@@ -254,16 +264,14 @@ def test_e4m3_fused_step_matches_separate(dev, shape, grid):
     bit-identical to eh_paged_decode_batched_e4m3 after that append (lens =
     start_pos + 1), and within tolerance of sdpa_decode on the dequantised
     pool.  The appended rows include values that saturate (|x/scale| >= 448),
-    and contexts that end on every slot of a page."""
+    and contexts that end on every slot of a page.  Pool: quantised N(0,1)
+    K/V (scales max|x| / 448)."""
     n_head, n_kv, hd, bt = shape
     rng = np.random.default_rng(77 + n_kv)
     pos = np.concatenate([[0, 1, 15, 16, 17, 31, 32, 255], rng.integers(1, 700, 8)]).astype(np.uint32)
     B, rl = len(pos), n_kv * hd
     tab, nb = make_tables(rng, pos + 1, bt)
-    codes = rng.integers(0, 256, nb * bt * 2 * rl).astype(np.uint8)
-    codes[(codes & 0x7F) == 0x7F] = 0x3C
-    ks = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
-    vs = rng.uniform(0.002, 0.05, n_kv).astype(np.float32)
+    codes, ks, vs = gauss_codes(rng, nb, bt, n_kv, hd)
     newk = rng.standard_normal((B, rl)).astype(np.float32)
     newv = rng.standard_normal((B, rl)).astype(np.float32)
     newk[0, :4] = [30.0, -30.0, 1e-7, 0.0]               # saturating, subnormal, zero

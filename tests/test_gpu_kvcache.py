@@ -2,7 +2,7 @@
 restatement of engine-kvcache/src/cache.rs.
 
 1. The reference's own known-answer tests (cache.rs:258-472) on the product
-   surface: exact floats, reads across scattered pages, exhaustion with no
+   surface: exact floats, reads across non-adjacent pages, exhaustion with no
    partial state, free then reuse, the budget bound -- and after each one the
    device pool equals orc.Cache's pool byte for byte.
 2. All-or-nothing appends: a failed launch rolls the reservation back; a batch
@@ -73,7 +73,7 @@ def test_append_single_token_reads_back_exact_floats(dev):
 
 
 def test_append_spanning_scattered_blocks(dev):
-    # cache.rs:304-370: sequence A on physical pages 0 and 3
+    # cache.rs:304-370: sequence A on non-adjacent physical pages
     c, o = pair(4, 4, 1, 2)
     a, b = c.new_sequence(), c.new_sequence()
     o.new_sequence(), o.new_sequence()
@@ -84,7 +84,10 @@ def test_append_spanning_scattered_blocks(dev):
     for t in range(4, 8):
         both_append(c, o, a, [t, t * 10.0], [0.0, 0.0])
     assert c.token_count(a) == 8
-    assert c.seq_block_table(a) == [0, 3] and c.seq_block_table(b) == [1, 2]
+    # (the reference's comment expects pages 0 and 3 for A, but B's 4 tokens
+    # fit one 4-token page, so A continues on page 2; its test checks data only)
+    assert c.seq_block_table(a) == o.seq_block_table(a).tolist() == [0, 2]
+    assert c.seq_block_table(b) == o.seq_block_table(b).tolist() == [1]
     keys = c.read_keys(a).cpu().numpy().reshape(8, 2)
     assert keys.tolist() == [[t, t * 10.0] for t in range(8)]
     same_pool(c, o)
