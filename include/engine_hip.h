@@ -307,6 +307,26 @@ eh_status eh_append_decode_batched(eh_context* ctx, eh_stream stream, const eh_k
                                    const float* q, uint64_t q_bytes, float* out, uint64_t out_bytes,
                                    uint32_t n_head, uint32_t head_dim, uint32_t grid,
                                    void* workspace, uint64_t workspace_bytes);
+/* ---- eh_append_decode_batched without a workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No reference counterpart.
+ * Same arguments and results as eh_append_decode_batched; the partial states
+ * live in a 32 MiB scratch array that the library holds on every GPU it runs
+ * on until the process ends.  Shapes whose partials need more
+ * (4 * (grid + batch) * n_head * 130 bytes > 32 MiB) return EH_INVALID_SIZE
+ * (expected = the limit, actual = the need) before any launch.  The call
+ * allocates nothing; all calls on one GPU share its scratch, so calls that
+ * overlap in time on one GPU (two streams, two threads) race. */
+eh_status eh_append_decode_batched_noalloc(eh_context* ctx, eh_stream stream,
+                                          const eh_kv_layout* layout, void* pool,
+                                          uint64_t pool_bytes, const void* keys,
+                                          uint64_t keys_bytes, const void* values,
+                                          uint64_t values_bytes, const uint32_t* block_tables,
+                                          uint64_t bt_bytes, uint32_t bt_stride,
+                                          const uint32_t* start_pos, uint32_t batch,
+                                          const float* q, uint64_t q_bytes, float* out,
+                                          uint64_t out_bytes, uint32_t n_head, uint32_t head_dim,
+                                          uint32_t grid);
 /* The same fused decode step over E4M3 pages (extension: the quantising
  * append of eh_append_kv_e4m3_batched, then eh_paged_decode_batched_e4m3, in
  * one launch): keys/values [batch, row_len] f32 are quantised in the launch

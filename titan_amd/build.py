@@ -71,12 +71,26 @@ HOST_SOURCES = ("engine_hip.cpp", "kv_host.cpp", "kv_share.cpp")
 SANITIZE = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-fno-sanitize-recover=undefined"]
 
 
+# The one host-library source with device code: the static scratch array of
+# eh_append_decode_batched_noalloc (compiled by hipcc, linked by g++).
+NOALLOC_SRC = os.path.join(CSRC, "noalloc.hip")
+OBJ_DIR = os.path.join(ROOT, "_build", "obj")
+NOALLOC_OBJ = os.path.join(OBJ_DIR, "noalloc.o")
+
+
+def _noalloc_cmd(hipcc):
+    return [hipcc, f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-c",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            NOALLOC_SRC, "-o", NOALLOC_OBJ]
+
+
 def _host_cmd(out, extra=()):
-    """g++ line of the C-ABI host library (no device code in these sources)."""
+    """g++ line of the C-ABI host library (the hipcc-built noalloc object is
+    linked in as is)."""
     return [
         "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", *extra,
-        *(os.path.join(CSRC, f) for f in HOST_SOURCES),
+        *(os.path.join(CSRC, f) for f in HOST_SOURCES), NOALLOC_OBJ,
         "-o", out, f"-L{ROCM}/lib", "-lamdhip64", "-ldl", f"-Wl,-rpath,{ROCM}/lib",
     ]
 
@@ -90,6 +104,8 @@ def build(verbose=False, host_only=False):
         src = os.path.join(CSRC, "kernels", srcname + ".hip")
         out = os.path.join(LIB, name + ".hsaco")
         cmds.append((name, [hipcc, *HIP_DEVICE_FLAGS, *defs, src, "-o", out + ".tmp"]))
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    _run_parallel([("noalloc", _noalloc_cmd(hipcc))], verbose)
     host_out = os.path.join(LIB, "libengine_hip.so")
     cmds.append(("libengine_hip", _host_cmd(host_out + ".tmp")))
     _run_parallel(cmds, verbose)
@@ -107,6 +123,8 @@ def sanitize_check(pytest_args=("-x", "-q", "-m", "not gpu")):
     GPU kernels are not involved).  Returns pytest's exit status."""
     out_dir = os.path.join(ROOT, "_build", "sanitize")
     os.makedirs(out_dir, exist_ok=True)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    _run_parallel([("noalloc", _noalloc_cmd(_hipcc()))], verbose=True)
     host = os.path.join(out_dir, "libengine_hip.so")
     orc = os.path.join(out_dir, "liborc_kv.so")
     _run_parallel([

@@ -31,7 +31,15 @@ struct eh_context {
     // (the reference does the same at paged_attention.rs:111-123).
     float* scratch = nullptr;
     uint64_t scratch_floats = 0;
+    // This device's copy of the library's static scratch array (noalloc.hip),
+    // looked up once at creation: the workspace of
+    // eh_append_decode_batched_noalloc.
+    void* noalloc = nullptr;
+    uint64_t noalloc_bytes = 0;
 };
+
+// noalloc.hip
+extern "C" int eh_noalloc_scratch_setup(void** ptr, uint64_t* bytes);
 
 namespace {
 
@@ -601,6 +609,13 @@ eh_status eh_create(int device, const char* code_object_dir, eh_context** out) {
         return fail(EH_ALLOC_FAILED, "hipMalloc(split-K scratch)", 0, 0, (int)e);
     }
     c->scratch_floats = kScratchFloats;
+    // device address of the static scratch array on this device (the device
+    // is current here)
+    const int se = eh_noalloc_scratch_setup(&c->noalloc, &c->noalloc_bytes);
+    if (se != 0) {
+        eh_destroy(c);
+        return fail(EH_KERNEL_LOAD, "hipGetSymbolAddress(scratch)", 0, 0, se);
+    }
     *out = c;
     return EH_OK;
 }
@@ -1260,6 +1275,33 @@ eh_status eh_append_decode_batched(eh_context* c, eh_stream stream, const eh_kv_
                               values_bytes, bt, bt_bytes, bt_stride, start_pos, batch, q, q_bytes,
                               out, out_bytes, n_head, head_dim, grid, ws, ws_bytes, nullptr,
                               nullptr);
+}
+
+eh_status eh_append_decode_batched_noalloc(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                                          void* pool, uint64_t pool_bytes, const void* keys,
+                                          uint64_t keys_bytes, const void* values,
+                                          uint64_t values_bytes, const uint32_t* bt,
+                                          uint64_t bt_bytes, uint32_t bt_stride,
+                                          const uint32_t* start_pos, uint32_t batch,
+                                          const float* q, uint64_t q_bytes, float* out,
+                                          uint64_t out_bytes, uint32_t n_head, uint32_t head_dim,
+                                          uint32_t grid) {
+    // eh_append_decode_batched with this device's static scratch array as the
+    // workspace: no device allocation anywhere on this path.  The partials
+    // are fully written by each call before they are read, so nothing in the
+    // scratch needs clearing; calls on one device share it and must not
+    // overlap in time.
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (!c->noalloc) return fail(EH_KERNEL_LOAD, "no-alloc scratch missing");
+    if (grid >= 1 && batch >= 1) {
+        const uint64_t need = tiles_ws_bytes(grid, batch, n_head);
+        if (need > c->noalloc_bytes)
+            return invalid_size(c->noalloc_bytes, need, "no-alloc scratch limit");
+    }
+    return append_decode_body(c, stream, l, pool, pool_bytes, keys, keys_bytes, values,
+                              values_bytes, bt, bt_bytes, bt_stride, start_pos, batch, q, q_bytes,
+                              out, out_bytes, n_head, head_dim, grid, c->noalloc, c->noalloc_bytes,
+                              nullptr, nullptr);
 }
 
 eh_status eh_append_decode_batched_e4m3(eh_context* c, eh_stream stream, const eh_kv_layout* l,

@@ -189,6 +189,26 @@ class PagedAttention:
             int(stride), buf(start_pos)[0], int(batch), qp, qb, op, ob, int(n_head), int(head_dim),
             int(plan[1]), wp, wb))
 
+    def append_decode_batched_noalloc(self, stream, layout, pool, keys, values, block_tables,
+                                      start_pos, q, out, n_head, head_dim, grid):
+        """append_decode_batched with the library's per-GPU static scratch in
+        place of a workspace: for callers that cannot allocate device memory.
+        `grid` is plan[1] of a token-balanced plan; shapes whose partials
+        exceed the 32 MiB scratch raise InvalidSize.  Calls that overlap in
+        time on one GPU race on the shared scratch."""
+        batch, stride = block_tables.shape
+        pp, pb = buf(pool)
+        kp, kb = buf(keys)
+        vp_, vb = buf(values)
+        bp, bb = buf(block_tables)
+        qp, qb = buf(q)
+        op, ob = buf(out)
+        lay = layout.c()
+        check(self._L.eh_append_decode_batched_noalloc(
+            self._ctx.handle, stream_handle(stream), C.byref(lay), pp, pb, kp, kb, vp_, vb, bp, bb,
+            int(stride), buf(start_pos)[0], int(batch), qp, qb, op, ob, int(n_head), int(head_dim),
+            int(grid)))
+
     def append_decode_batched_e4m3(self, stream, layout, pool, keys, values, block_tables,
                                    start_pos, q, out, n_head, head_dim, plan, workspace, k_scale,
                                    v_scale):
