@@ -46,6 +46,9 @@ def parse():
     p.add_argument("--roofline-iters", type=int, default=10)
     p.add_argument("--fuse", type=int, default=1,
                    help="one fused append+decode launch per layer when the balanced kernel applies")
+    p.add_argument("--sched", type=int, default=1,
+                   help="build the step's work split once per step (eh_decode_schedule) and run "
+                        "every layer from it")
     p.add_argument("--suite", action="store_true",
                    help="instead of the headline line, time the other benchmark configurations "
                         "(1, 3, 4, 5) and append/gather, one JSON line each")
@@ -161,10 +164,16 @@ def main():
     kname = PagedAttention.kernel_name(NQ, NKV, HD, BT, KvDataType.F16)
     balanced = plan[0] == 0
     fused = balanced and bool(args.fuse)
+    scheduled = fused and bool(args.sched)
+    stride = int(tab.shape[1])
+    sched = PagedAttention.schedule_buffer(B, stride, BT, plan) if scheduled else None
     kv, pa = PagedKvGpu(0), PagedAttention(0)
 
     def layer(i, s=None):
-        if fused:  # append + decode in one launch of the balanced kernel
+        if scheduled:  # append + decode in one launch, split read from the step schedule
+            pa.append_decode_scheduled(s, layout, pools[i], newk[i], newv[i], sched, stride, qs[i],
+                                       outs[i], NQ, HD, plan, ws)
+        elif fused:  # append + decode in one launch of the balanced kernel
             pa.append_decode_batched(s, layout, pools[i], newk[i], newv[i], d_tab, start, qs[i],
                                      outs[i], NQ, HD, plan, ws)
         else:
@@ -173,6 +182,8 @@ def main():
                               KvDataType.F16, plan, ws)
 
     def step(s=None):
+        if scheduled:  # the step's work split, shared by its 28 layers
+            pa.build_schedule(s, layout, d_tab, start, 1, plan, sched)
         for i in range(L):
             layer(i, s)
         start.add_(1)
@@ -228,8 +239,13 @@ def main():
     dgraph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(dstream):
         with torch.cuda.graph(dgraph, stream=dstream):
+            if scheduled:
+                pa.build_schedule(dstream, layout, d_tab, start, 1, plan, sched)
             for i in range(L):
-                if fused:
+                if scheduled:
+                    pa.append_decode_scheduled(dstream, layout, pools[i], newk[i], newv[i], sched,
+                                               stride, qs[i], outs[i], NQ, HD, plan, ws)
+                elif fused:
                     pa.append_decode_batched(dstream, layout, pools[i], newk[i], newv[i], d_tab,
                                              start, qs[i], outs[i], NQ, HD, plan, ws)
                 else:
@@ -261,8 +277,10 @@ def main():
             traffic = tr.get("hbm_bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": kname + (" + eh_decode_tiles_merge" if balanced else " + eh_decode_merge")
-                + (" (fused append)" if fused else ""),
+                "kernel": (kname + "_sched + eh_decode_tiles_merge_sched (fused append; "
+                           "+ 1/28 of eh_decode_tiles_schedule per step)") if scheduled else
+                (kname + (" + eh_decode_tiles_merge" if balanced else " + eh_decode_merge")
+                 + (" (fused append)" if fused else "")),
                 "avg_launch_us": round(avg_ms * 1e3, 2),
                 "algorithmic_bytes_per_launch": per_launch_bytes}
 
@@ -277,7 +295,8 @@ def main():
                                "page 16, f16 KV, ctx U[128,4096], 28 layers (append + decode)",
                    "batch": B, "layers": L, "n_head": NQ, "n_head_kv": NKV, "head_dim": HD,
                    "block_tokens": BT, "ctx_sum": ctx_before, "tokens_per_split": plan[0],
-                   "grid": plan[1], "fused_append": fused, "graph": bool(args.graph)},
+                   "grid": plan[1], "fused_append": fused, "step_schedule": scheduled,
+                   "graph": bool(args.graph)},
         "tok_s": round(tok_s, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": roofline, "cpu_baseline": cpu,
     }

@@ -307,6 +307,49 @@ eh_status eh_append_decode_batched(eh_context* ctx, eh_stream stream, const eh_k
                                    const float* q, uint64_t q_bytes, float* out, uint64_t out_bytes,
                                    uint32_t n_head, uint32_t head_dim, uint32_t grid,
                                    void* workspace, uint64_t workspace_bytes);
+/* ---- Decode step schedule (extension): the layers of one decode step share
+ * one block table and one set of positions (the reference passes one bt_dev
+ * to every layer, engine-core/src/forward_driver.rs:2230-2243), so the
+ * token-balanced work split -- which pages each run reads, which sequence
+ * each tile belongs to, which runs hold each sequence -- is computed once per
+ * step by eh_decode_schedule and read by every layer's
+ * eh_append_decode_scheduled, instead of each layer's launch deriving it
+ * from the lengths and tables again.  The schedule is device-side: a
+ * captured graph that rebuilds it each step stays correct as contexts grow.
+ *
+ * Bytes of a schedule for batch sequences, bt_stride table entries each and
+ * grid runs (grid = max_splits of eh_decode_plan with hint 0). */
+uint64_t eh_decode_schedule_bytes(uint32_t batch, uint32_t bt_stride, uint32_t block_tokens,
+                                  uint32_t grid);
+/* Builds the schedule from block_tables [batch, bt_stride] and the lengths
+ * lens[b] + lens_add (lens_add = 1 with the positions a fused step appends
+ * at) for a pool of layout->n_blocks pages of layout->block_tokens tokens
+ * (a power of two, >= 16).  Tiles the table cannot address are dropped
+ * (their tokens are masked in every decode form).  One launch. */
+eh_status eh_decode_schedule(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                             const uint32_t* block_tables, uint64_t bt_bytes, uint32_t bt_stride,
+                             const uint32_t* lens, uint32_t lens_add, uint32_t batch, uint32_t grid,
+                             void* sched, uint64_t sched_bytes);
+/* One layer's decode step from a schedule (extension: eh_append_decode_batched
+ * / eh_append_decode_batched_e4m3 with the work split read from `sched`
+ * rather than derived from the lengths): row b of keys/values is written at
+ * the position the schedule was built with (lens[b] when lens_add = 1) and q
+ * row b attends the schedule's tokens of sequence b.  keys = values = NULL
+ * skips the append (a decode over a schedule built with lens_add = 0, as
+ * eh_paged_decode_batched / eh_paged_decode_batched_e4m3).  E4M3 pages take
+ * f32 rows and both scales.  layout, bt_stride, batch and grid must be those
+ * the schedule was built with; the pool may differ per layer (same layout).
+ * Outputs equal the self-scheduled forms'; workspace as eh_decode_plan. */
+eh_status eh_append_decode_scheduled(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                                     void* pool, uint64_t pool_bytes, const void* keys,
+                                     uint64_t keys_bytes, const void* values,
+                                     uint64_t values_bytes, const void* sched,
+                                     uint64_t sched_bytes, uint32_t bt_stride, uint32_t batch,
+                                     const float* q, uint64_t q_bytes, float* out,
+                                     uint64_t out_bytes, uint32_t n_head, uint32_t head_dim,
+                                     uint32_t grid, void* workspace, uint64_t workspace_bytes,
+                                     const float* k_scale, const float* v_scale);
+
 /* ---- eh_append_decode_batched without a workspace argument, for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  No reference counterpart.

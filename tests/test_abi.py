@@ -49,7 +49,9 @@ def test_code_objects_contain_launched_kernels():
         for g in (1, 2, 4, 6, 8):
             assert f"eh_decode_tiles_{dt}_hd128_g{g}".encode() in tl
             assert f"eh_decode_tiles_{dt}_hd128_g{g}_ext".encode() in tl
+            assert f"eh_decode_tiles_{dt}_hd128_g{g}_sched".encode() in tl
         assert b"eh_decode_tiles_merge" in tl and b"eh_decode_tiles_mass" in tl
+        assert b"eh_decode_tiles_merge_sched" in tl and b"eh_decode_tiles_schedule" in tl
     pf = open(os.path.join(_lib.LIB_DIR, "paged_prefill.hsaco"), "rb").read()
     for dt in ("f32", "f16", "bf16"):
         for hd in (64, 128):

@@ -395,3 +395,227 @@ def test_config5_full_size_offsets_past_4gib(dev):
                                             ctx - 1, True, kv_dtype=KvDataType.F16)
     torch.cuda.synchronize()
     check_close(out1.cpu().numpy(), ref[2].ravel(), what="config5 flash_decoding seq 2")
+
+
+# ---- step schedule (eh_decode_schedule + eh_append_decode_scheduled) ----------
+
+def sched_case(dev, shape, pos, seed, dtype=KvDataType.F16, spare=3):
+    n_head, n_kv, hd, bt = shape
+    rng = np.random.default_rng(seed)
+    pos = np.asarray(pos, np.int64)
+    tab, nb = make_tables(rng, pos + 1, bt, spare)
+    pool, _ = make_pool(rng, nb, bt, n_kv, hd, dtype, dev)
+    B, rl = len(pos), n_kv * hd
+    td = TD[dtype]
+    k = torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).to(td).to(dev)
+    v = torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).to(td).to(dev)
+    q = torch.from_numpy(rng.standard_normal((B, n_head, hd)).astype(np.float32)).to(dev)
+    return tab, nb, pool, k, v, q
+
+
+def run_both(dev, shape, pos, seed, dtype=KvDataType.F16, grid=None, layers=1):
+    """Self-scheduled fused steps vs one schedule shared by `layers` layers:
+    pools and outputs must be bit-identical."""
+    n_head, n_kv, hd, bt = shape
+    pos = np.asarray(pos, np.int64)
+    B = len(pos)
+    pa = PagedAttention(0)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, dtype)
+    assert plan[0] == 0
+    if grid is not None:
+        plan = (0, grid, plan[2])
+    tab, nb, _, _, _, _ = sched_case(dev, shape, pos, seed, dtype)
+    layout = PagedKvLayout(nb, bt, n_kv * hd, dtype)
+    dtab, dpos = i32(tab, dev), i32(pos, dev)
+    sched = PagedAttention.schedule_buffer(B, tab.shape[1], bt, plan)
+    pa.build_schedule(None, layout, dtab, dpos, 1, plan, sched)
+    ws = PagedAttention.workspace(plan)
+    outs = []
+    for layer in range(layers):
+        _, _, pool, k, v, q = sched_case(dev, shape, pos, seed + 1000 * (layer + 1), dtype)
+        pool_a, pool_b = pool.clone(), pool.clone()
+        out_a = torch.full((B, n_head, hd), float("nan"), device=dev)
+        out_b = torch.full((B, n_head, hd), float("nan"), device=dev)
+        pa.append_decode_batched(None, layout, pool_a, k, v, dtab, dpos, q, out_a, n_head, hd, plan,
+                                 ws)
+        pa.append_decode_scheduled(None, layout, pool_b, k, v, sched, tab.shape[1], q, out_b,
+                                   n_head, hd, plan, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(pool_a.view(torch.int16), pool_b.view(torch.int16)), layer
+        assert torch.equal(out_a.view(torch.int32), out_b.view(torch.int32)), layer
+        outs.append((pool_b, out_b, q))
+    return tab, nb, outs
+
+
+SCHED_POS = [0, 1, 14, 15, 16, 31, 299, 2048, 33, 999, 6, 4000]
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
+@pytest.mark.parametrize("shape", [(12, 2, 128, 16), (32, 8, 128, 16), (8, 1, 128, 32),
+                                   (16, 4, 128, 16), (4, 4, 128, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_scheduled_step_equals_self_scheduled(dev, dtype, shape):
+    tab, nb, outs = run_both(dev, shape, SCHED_POS, 61 + sum(shape), dtype)
+    # and the oracle on the appended pool
+    n_head, n_kv, hd, bt = shape
+    pool_b, out_b, q = outs[0]
+    ref = orc.sdpa_decode_batched(pool_b.float().cpu().numpy(), tab,
+                                  np.asarray(SCHED_POS, np.uint32) + 1, bt, q.cpu().numpy(),
+                                  n_head, n_kv, hd)
+    check_close(out_b.cpu().numpy(), ref, what="scheduled")
+
+
+@pytest.mark.parametrize("grid", [1, 3, 64, 1023])
+def test_scheduled_small_grids(dev, grid):
+    """Runs over many sequences, more than 64 items per run (grid 1, 3)."""
+    run_both(dev, (12, 2, 128, 16), [3000, 0, 1, 2000, 5, 1500, 16, 31, 777], 70 + grid, grid=grid)
+
+
+def test_one_schedule_serves_every_layer(dev):
+    run_both(dev, (12, 2, 128, 16), np.random.default_rng(3).integers(127, 4096, 32), 90, layers=4)
+
+
+def test_scheduled_decode_only_equals_decode_batched(dev):
+    """keys = values = None with a schedule of lens_add 0: eh_paged_decode_batched's result."""
+    n_head, n_kv, hd, bt = 16, 4, 128, 16
+    lens = np.array([0, 1, 17, 300, 2049, 0, 64], np.int64)
+    rng = np.random.default_rng(12)
+    tab, nb = make_tables(rng, lens, bt)
+    pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)
+    B = len(lens)
+    q = torch.from_numpy(rng.standard_normal((B, n_head, hd)).astype(np.float32)).to(dev)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(lens.max()))
+    pa = PagedAttention(0)
+    ws = PagedAttention.workspace(plan)
+    out_a = torch.empty((B, n_head, hd), device=dev)
+    out_b = torch.empty_like(out_a)
+    dtab = i32(tab, dev)
+    pa.decode_batched(None, q, pool, dtab, i32(lens, dev), out_a, n_head, n_kv, hd, bt,
+                      KvDataType.F16, plan, ws)
+    layout = PagedKvLayout(nb, bt, n_kv * hd, KvDataType.F16)
+    sched = PagedAttention.schedule_buffer(B, tab.shape[1], bt, plan)
+    pa.build_schedule(None, layout, dtab, i32(lens, dev), 0, plan, sched)
+    pa.append_decode_scheduled(None, layout, pool, None, None, sched, tab.shape[1], q, out_b,
+                               n_head, hd, plan, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int32), out_b.view(torch.int32))
+    ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q.cpu().numpy(),
+                                  n_head, n_kv, hd)
+    check_close(out_b.cpu().numpy(), ref, what="scheduled decode-only")
+
+
+def test_scheduled_e4m3_step_equals_self_scheduled(dev):
+    from e4m3_data import gauss_codes
+    n_head, n_kv, hd, bt = 32, 8, 128, 16
+    pos = np.array(SCHED_POS, np.int64)
+    B, rl = len(pos), n_kv * hd
+    rng = np.random.default_rng(81)
+    tab, nb = make_tables(rng, pos + 1, bt)
+    codes, ks, vs = gauss_codes(rng, nb, bt, n_kv, hd)
+    layout = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    k = t(rng.standard_normal((B, rl)).astype(np.float32))
+    v = t(rng.standard_normal((B, rl)).astype(np.float32))
+    q = t(rng.standard_normal((B, n_head, hd)).astype(np.float32))
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, KvDataType.FP8)
+    pa = PagedAttention(0)
+    ws = PagedAttention.workspace(plan)
+    dtab, dpos, dks, dvs = i32(tab, dev), i32(pos, dev), t(ks), t(vs)
+    pool_a, pool_b = t(codes.copy()), t(codes.copy())
+    out_a = torch.empty((B, n_head, hd), device=dev)
+    out_b = torch.empty_like(out_a)
+    pa.append_decode_batched_e4m3(None, layout, pool_a, k, v, dtab, dpos, q, out_a, n_head, hd,
+                                  plan, ws, dks, dvs)
+    sched = PagedAttention.schedule_buffer(B, tab.shape[1], bt, plan)
+    pa.build_schedule(None, layout, dtab, dpos, 1, plan, sched)
+    pa.append_decode_scheduled(None, layout, pool_b, k, v, sched, tab.shape[1], q, out_b, n_head,
+                               hd, plan, ws, dks, dvs)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a, pool_b)
+    assert torch.equal(out_a.view(torch.int32), out_b.view(torch.int32))
+
+
+def test_scheduled_graph_replay_growing_positions(dev):
+    """Schedule + two layers captured once; replays as the positions grow
+    equal eager self-scheduled fused steps, pools and outputs bit for bit."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl, steps = n_kv * hd, 6
+    start = np.array([0, 14, 15, 31, 500, 1023, 77, 4094], np.int64)
+    B = len(start)
+    rng = np.random.default_rng(17)
+    tab, nb = make_tables(rng, start + steps + 1, bt)
+    layout = PagedKvLayout(nb, bt, rl, KvDataType.F16)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(start.max()) + steps + 1)
+    pa = PagedAttention(0)
+    dtab = i32(tab, dev)
+    pos = i32(start, dev)
+    sched = PagedAttention.schedule_buffer(B, tab.shape[1], bt, plan)
+    ws = PagedAttention.workspace(plan)
+    pools_g = [make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)[0] for _ in range(2)]
+    pools_e = [p.clone() for p in pools_g]
+    k = torch.empty((B, rl), dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    q = torch.empty((B, n_head, hd), device=dev)
+    outs_g = [torch.empty_like(q) for _ in range(2)]
+    outs_e = [torch.empty_like(q) for _ in range(2)]
+
+    def step(s, pools, outs):
+        pa.build_schedule(s, layout, dtab, pos, 1, plan, sched)
+        for i in range(2):
+            pa.append_decode_scheduled(s, layout, pools[i], k, v, sched, tab.shape[1], q, outs[i],
+                                       n_head, hd, plan, ws)
+    k.zero_(); v.zero_(); q.zero_()
+    scratch_pools = [p.clone() for p in pools_g]
+    step(None, scratch_pools, [torch.empty_like(q) for _ in range(2)])   # warm-up
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step(s, pools_g, outs_g)
+    torch.cuda.synchronize()
+    ws_e = PagedAttention.workspace(plan)
+    for st in range(steps):
+        k.copy_(torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float16)))
+        v.copy_(torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float16)))
+        q.copy_(torch.from_numpy(rng.standard_normal((B, n_head, hd)).astype(np.float32)))
+        pos.copy_(i32(start + st, dev))
+        torch.cuda.synchronize()
+        for i in range(2):
+            pa.append_decode_batched(None, layout, pools_e[i], k, v, dtab, pos, q, outs_e[i],
+                                     n_head, hd, plan, ws_e)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(pools_g[i].view(torch.int16), pools_e[i].view(torch.int16)), (st, i)
+            assert torch.equal(outs_g[i].view(torch.int32), outs_e[i].view(torch.int32)), (st, i)
+
+
+def test_scheduled_tables_shorter_than_lengths(dev):
+    """Lengths past what the table addresses: those tiles are dropped from the
+    schedule (masked in every form); the result is attention over the
+    addressable tokens, and the out-of-table appended row is not written."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    lens = np.array([100, 40, 16, 0, 33], np.int64)       # tables hold 2 pages (32 tokens)
+    B = len(lens)
+    rng = np.random.default_rng(23)
+    nb = B * 2 + 2
+    perm = rng.permutation(nb).astype(np.uint32)
+    tab = perm[:B * 2].reshape(B, 2)
+    pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)
+    q = torch.from_numpy(rng.standard_normal((B, n_head, hd)).astype(np.float32)).to(dev)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, 128)
+    pa = PagedAttention(0)
+    layout = PagedKvLayout(nb, bt, n_kv * hd, KvDataType.F16)
+    sched = PagedAttention.schedule_buffer(B, 2, bt, plan)
+    dtab = i32(tab, dev)
+    pa.build_schedule(None, layout, dtab, i32(lens, dev), 0, plan, sched)
+    out = torch.empty((B, n_head, hd), device=dev)
+    pa.append_decode_scheduled(None, layout, pool, None, None, sched, 2, q, out, n_head, hd, plan,
+                               PagedAttention.workspace(plan))
+    torch.cuda.synchronize()
+    ref = orc.sdpa_decode_batched(pool_f32, tab, np.minimum(lens, 32).astype(np.uint32), bt,
+                                  q.cpu().numpy(), n_head, n_kv, hd)
+    check_close(out.cpu().numpy(), ref, what="scheduled, short tables")

@@ -366,6 +366,19 @@ uint64_t mass_ws_bytes(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens
     return 8ull * batch * n_head * (mass_rec_row(bt_stride, block_tokens) + 1);
 }
 
+// Step schedule (eh_decode_schedule): P run headers, P * cap item
+// descriptors and batch sequence records, 16 bytes each; cap = the most
+// tiles one run can hold, from the tiles the block tables can address.
+uint64_t sched_tile_bound(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens) {
+    return batch * bt_stride * (block_tokens / 16);
+}
+uint64_t sched_cap(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens, uint64_t grid) {
+    return std::max<uint64_t>(div_ceil(sched_tile_bound(batch, bt_stride, block_tokens), grid), 1);
+}
+uint64_t sched_bytes(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens, uint64_t grid) {
+    return 16ull * (grid + grid * sched_cap(batch, bt_stride, block_tokens, grid) + batch);
+}
+
 struct tiles_args {
     uint32_t kv_dtype;
     const float* q;
@@ -386,6 +399,8 @@ struct tiles_args {
     uint32_t sink, window;  // protected-sinks range; window 0 attends every token
     float* block_mass;      // optional H2O scores [n_blocks]: += attention mass per page
     void* mass_ws;          // tile records + final (M, L), mass_ws_bytes
+    const void* sched;      // step schedule (eh_decode_schedule) or null: self-scheduled
+    uint32_t cap;           // items per run in the schedule
 };
 
 eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const tiles_cfg& t) {
@@ -393,7 +408,7 @@ eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const 
     const bool f8 = a.kv_dtype == EH_KV_FP8;
     const bool ext = a.window != 0 || a.block_mass != nullptr;  // sinks/window or mass records
     std::snprintf(name, sizeof name, "eh_decode_tiles_%s_hd128_g%u%s", f8 ? "fp8" : dt_name(a.kv_dtype),
-                  t.g, ext ? "_ext" : "");
+                  t.g, ext ? "_ext" : a.sched ? "_sched" : "");
     const hipModule_t mod = c->mod_tiles[f8 ? 2 : a.kv_dtype == EH_KV_F16 ? 0 : 1];
     const float scale_log2 = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;  // paged_attention.rs:286
     // per-wave V tiles (16 rows x kTilesVRow bytes) and staged q rows
@@ -413,10 +428,15 @@ eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const 
                               (const uint8_t*)a.new_k, (const uint8_t*)a.new_v, a.batch, a.out,
                               part_acc, part_ml, a.n_head, a.n_head_kv, a.block_tokens,
                               (uint32_t)log2_exact(a.block_tokens), scale_log2, a.grid, a.sink,
-                              a.window, tile_rec, fin, rec_row, a.k_scale, a.v_scale);
+                              a.window, tile_rec, fin, rec_row, a.k_scale, a.v_scale, a.sched,
+                              a.cap);
     if (st != EH_OK) return st;
-    st = launch(c, mod, "eh_decode_tiles_merge",
-                dim3((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch), dim3(256), stream,
+    const dim3 mgrid((uint32_t)div_ceil((uint64_t)a.n_head * 128, 64), a.batch);
+    if (a.sched)
+        return launch(c, mod, "eh_decode_tiles_merge_sched", mgrid, dim3(256), stream,
+                      (const float*)part_acc, (const float*)part_ml, a.out, a.sched, a.grid, a.cap,
+                      a.batch, a.n_head, 128u);
+    st = launch(c, mod, "eh_decode_tiles_merge", mgrid, dim3(256), stream,
                   (const float*)part_acc, (const float*)part_ml, a.out, a.lens, a.lens_add, a.batch,
                   a.n_head, 128u, a.grid, a.sink, a.window, fin);
     if (st != EH_OK || !a.block_mass) return st;
@@ -1318,6 +1338,117 @@ eh_status eh_append_decode_batched_e4m3(eh_context* c, eh_stream stream, const e
                               values_bytes, bt, bt_bytes, bt_stride, start_pos, batch, q, q_bytes,
                               out, out_bytes, n_head, head_dim, grid, ws, ws_bytes, k_scale,
                               v_scale);
+}
+
+uint64_t eh_decode_schedule_bytes(uint32_t batch, uint32_t bt_stride, uint32_t block_tokens,
+                                  uint32_t grid) {
+    if (batch == 0 || bt_stride == 0 || grid == 0 || block_tokens < 16) return 0;
+    return sched_bytes(batch, bt_stride, block_tokens, grid);
+}
+
+// Shape checks shared by the schedule builder and the scheduled decode.
+static eh_status check_sched_shape(const eh_kv_layout* l, uint32_t batch, uint32_t bt_stride,
+                                   uint32_t grid, uint64_t sched_bytes_given) {
+    if (!l) return fail(EH_INVALID_ARGS, "null layout");
+    if (l->block_tokens < 16 || (l->block_tokens & (l->block_tokens - 1)) ||
+        l->block_tokens > 0xFFFFFFFFull)
+        return fail(EH_UNSUPPORTED, "block_tokens: a power of two of at least 16");
+    if (batch > kTilesMaxBatch) return invalid_size(kTilesMaxBatch, batch, "batch");
+    if (bt_stride == 0) return invalid_size(1, 0, "bt_stride");
+    if (grid < 1) return invalid_size(1, grid, "grid");
+    const uint64_t tb = sched_tile_bound(batch, bt_stride, l->block_tokens);
+    if (tb > 0x7FFFFFFFull) return invalid_size(0x7FFFFFFFull, tb, "schedule tiles");
+    const uint64_t need = sched_bytes(batch, bt_stride, l->block_tokens, grid);
+    if (sched_bytes_given < need) return invalid_size(need, sched_bytes_given, "schedule");
+    return EH_OK;
+}
+
+eh_status eh_decode_schedule(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                             const uint32_t* bt, uint64_t bt_bytes, uint32_t bt_stride,
+                             const uint32_t* lens, uint32_t lens_add, uint32_t batch, uint32_t grid,
+                             void* sched, uint64_t sched_bytes_given) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (batch == 0) return EH_OK;
+    eh_status st = check_sched_shape(l, batch, bt_stride, grid, sched_bytes_given);
+    if (st) return st;
+    if (!lens || !bt || !sched) return fail(EH_INVALID_ARGS, "lens / block_tables / schedule is null");
+    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
+    if (l->n_blocks < 1) return fail(EH_INVALID_ARGS, "layout");
+    st = bind(c);
+    if (st) return st;
+    const uint64_t cap = sched_cap(batch, bt_stride, l->block_tokens, grid);
+    const uint64_t n_index = std::max<uint64_t>(
+        std::max<uint64_t>(grid, batch), sched_tile_bound(batch, bt_stride, l->block_tokens));
+    const uint32_t wgs = (uint32_t)std::min<uint64_t>(div_ceil(n_index, 256), 1024);
+    return launch_lds(c, c->mod_tiles[0], "eh_decode_tiles_schedule", dim3(wgs), dim3(256),
+                      4u * (2u * batch + 1u), stream, lens, lens_add, bt, bt_stride,
+                      (uint64_t)l->n_blocks, batch, (uint32_t)l->block_tokens,
+                      (uint32_t)log2_exact(l->block_tokens), grid, (uint32_t)cap,
+                      (uint32_t)n_index, sched);
+}
+
+eh_status eh_append_decode_scheduled(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                                     void* pool, uint64_t pool_bytes, const void* keys,
+                                     uint64_t keys_bytes, const void* values,
+                                     uint64_t values_bytes, const void* sched,
+                                     uint64_t sched_bytes_given, uint32_t bt_stride,
+                                     uint32_t batch, const float* q, uint64_t q_bytes, float* out,
+                                     uint64_t out_bytes, uint32_t n_head, uint32_t head_dim,
+                                     uint32_t grid, void* ws, uint64_t ws_bytes,
+                                     const float* k_scale, const float* v_scale) {
+    if (!c) return fail(EH_INVALID_ARGS, "null context");
+    if (batch == 0) return EH_OK;
+    eh_status st = check_sched_shape(l, batch, bt_stride, grid, sched_bytes_given);
+    if (st) return st;
+    if (!sched) return fail(EH_INVALID_ARGS, "schedule is null");
+    if ((keys == nullptr) != (values == nullptr)) return fail(EH_INVALID_ARGS, "keys / values");
+    if (head_dim < 1 || l->row_len % head_dim) return invalid_size(head_dim, l->row_len % (head_dim ? head_dim : 1));
+    const uint64_t n_head_kv = l->row_len / head_dim;
+    if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return invalid_size(n_head_kv, n_head);
+    const bool f8 = l->data_type == EH_KV_FP8;
+    if (f8 && (!k_scale || !v_scale)) return fail(EH_INVALID_ARGS, "E4M3 pages: both scales");
+    const uint64_t elt = elt_bytes(l->data_type);
+    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    if (l->n_blocks < 1 || page_bytes == 0) return fail(EH_INVALID_ARGS, "layout");
+    if (pool_bytes < l->n_blocks * page_bytes) return invalid_size(l->n_blocks * page_bytes, pool_bytes);
+    if (keys) {  // E4M3: the appended rows arrive as f32 and are quantised in the launch
+        const uint64_t row_expected = (uint64_t)batch * l->row_len * (f8 ? 4 : elt);
+        if (keys_bytes < row_expected) return invalid_size(row_expected, keys_bytes);
+        if (values_bytes < row_expected) return invalid_size(row_expected, values_bytes);
+    }
+    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
+    if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
+    const tiles_cfg tc = pick_tiles(l->data_type, head_dim, n_head, n_head_kv, l->block_tokens, batch);
+    if (!tc.ok) return fail(EH_UNSUPPORTED, "scheduled decode: shape outside the balanced kernel");
+    const uint64_t ws_need = tiles_ws_bytes(grid, batch, n_head);
+    if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
+    st = bind(c);
+    if (st) return st;
+    tiles_args a{};
+    a.kv_dtype = l->data_type;
+    a.q = q;
+    a.pool = pool;
+    a.n_blocks = l->n_blocks;
+    a.bt = nullptr;
+    a.bt_stride = bt_stride;
+    a.lens = nullptr;
+    a.lens_add = 0;
+    a.new_k = keys;
+    a.new_v = values;
+    a.batch = batch;
+    a.out = out;
+    a.n_head = n_head;
+    a.n_head_kv = (uint32_t)n_head_kv;
+    a.block_tokens = (uint32_t)l->block_tokens;
+    a.grid = grid;
+    a.ws = ws;
+    a.k_scale = f8 ? k_scale : nullptr;
+    a.v_scale = f8 ? v_scale : nullptr;
+    a.sched = sched;
+    a.cap = (uint32_t)sched_cap(batch, bt_stride, l->block_tokens, grid);
+    return run_tiles(c, stream, a, tc);
 }
 
 eh_status eh_flash_attention_prefill(eh_context* c, eh_stream stream, uint32_t kv_dtype,

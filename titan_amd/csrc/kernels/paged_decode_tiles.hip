@@ -228,17 +228,47 @@ __device__ __forceinline__ u32x4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Work item descriptors.  Every run walks a list of 16-token tiles; item k
+// of a run is one uint32x4 {phys, b, tok0, info}: the physical page (~0 =
+// masked), the sequence, the tile's first token and info = nvalid (tokens of
+// the tile before the sequence end, 1..16) | HOLDS_LAST << 8 (the tile holds
+// the sequence's last token, the appended one in a fused step) | WHOLE << 9
+// (the run holds every tile of the sequence: its rows are final, no partial).
+// They are built in registers from the live lengths (self-scheduled launch)
+// or read from a step schedule built once per decode step
+// (eh_decode_tiles_schedule) and shared by every layer.
+constexpr uint32_t INFO_LAST = 1u << 8;
+constexpr uint32_t INFO_WHOLE = 1u << 9;
+constexpr uint32_t NO_PAGE = 0xFFFFFFFFu;
+
+// Step schedule layout (uint32x4 records): P run headers {n_items, b_first,
+// b_last, 0}; P x cap item descriptors (run w's at w * cap); batch sequence
+// records {w0, w1, tokens, tiles} (the runs holding the sequence's first and
+// last tile).
+struct sched_view {
+    const u32x4* hdr;
+    const u32x4* items;
+    const u32x4* seqs;
+};
+__device__ __forceinline__ sched_view view_of(const u32x4* s, uint32_t P, uint32_t cap) {
+    return sched_view{s, s + P, s + P + (uint64_t)P * cap};
+}
+
+// ---------------------------------------------------------------------------
 // Split kernel.  Grid: 1-D workgroups of SUB * n_kv waves holding SUB runs
 // each (n_runs in all; the surplus runs of the last workgroup are empty);
 // wave kv of a run serves kv head kv on every tile of the run.  Dynamic LDS
 // (bytes): waves*16*VROW (V tiles) + waves*QSEG*G*128*4 (staged q rows) +
-// 4*(2*batch + 1) (tile prefix, token counts).  lens[b] + lens_add = tokens
-// sequence b attends (lens_add = 1 when lens are the positions of a fused
-// append).  Partials: slot w + b for workgroup w and sequence b,
-// part_acc [slots, n_head, 128], part_ml [slots, n_head, 2], slots = P + batch.
+// 4*(2*batch + 1) (tile prefix, token counts; self-scheduled launches only).
+// lens[b] + lens_add = tokens sequence b attends (lens_add = 1 when lens are
+// the positions of a fused append).  Partials: slot w + b for run w and
+// sequence b, part_acc [slots, n_head, 128], part_ml [slots, n_head, 2],
+// slots = P + batch.
 // EXT: the protected-sinks range and the per-tile attention-mass records are
 // compiled in (the plain instantiation keeps the hot loop free of them).
-template <int DT, int G, int DEPTH, int CHUNK, bool EXT>
+// SCHED: the run's items come from a step schedule (sched, cap) instead of
+// the lengths and block tables.
+template <int DT, int G, int DEPTH, int CHUNK, bool EXT, bool SCHED>
 __device__ __forceinline__ void decode_tiles(
     const float* __restrict__ q, uint8_t* pool, uint64_t n_blocks,
     const uint32_t* __restrict__ bt, uint32_t bt_stride, const uint32_t* __restrict__ lens,
@@ -247,7 +277,8 @@ __device__ __forceinline__ void decode_tiles(
     float* __restrict__ part_ml, uint32_t n_head, uint32_t n_head_kv,
     uint32_t block_tokens, uint32_t bt_shift, float scale_log2, uint32_t n_runs,
     uint32_t sink, uint32_t window, float* __restrict__ tile_rec, float* __restrict__ fin,
-    uint32_t rec_row, const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
+    uint32_t rec_row, const float* __restrict__ k_scale, const float* __restrict__ v_scale,
+    const u32x4* __restrict__ sched, uint32_t cap) {
     constexpr int HD = 128;
     constexpr int KSTEPS = HD / 32;  // MFMA steps over head_dim
     // E4M3 pages are converted to f16 in registers (exact) and use the f16 path
@@ -259,12 +290,12 @@ __device__ __forceinline__ void decode_tiles(
     typedef kvt<CT> K;
     typedef typename K::v8 V8;
     static_assert(G <= 16, "one 16-column score tile per kv head");
+    static_assert(!(EXT && SCHED), "the protected-sinks range is self-scheduled");
 
     extern __shared__ __align__(16) uint8_t smem[];
 
     // A workgroup holds SUB = waves / n_kv independent runs side by side
-    // (one wave per kv head each), sharing one scan of the lengths; run
-    // w = blockIdx * SUB + sub of P = gridDim * SUB.
+    // (one wave per kv head each); run w = blockIdx * SUB + sub of P = n_runs.
     const uint32_t NW = blockDim.x >> 6;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -282,69 +313,91 @@ __device__ __forceinline__ void decode_tiles(
     uint32_t* cum = reinterpret_cast<uint32_t*>(smem + NW * (TILE * VROW + QSEG * G * HD * 4));
     uint32_t* ntok = cum + batch + 1;
 
-    // ---- tile prefix over the batch (wave 0), from the live lengths
-    if (wave == 0) {
-        uint32_t run = 0;
-        for (uint32_t base = 0; base < batch; base += 64) {
-            const uint32_t j = base + lane;
-            const uint32_t n = j < batch ? lens[j] + lens_add : 0u;
-            uint32_t t = make_span(n, EXT ? sink : 0u, EXT ? window : 0u).tiles;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t y = __shfl_up(t, o, 64);
-                if (lane >= (uint32_t)o) t += y;
+    // ---- the run's items: n_items tiles, descriptors of items kb + lane in
+    // dsc (current batch of 64) and dsc_next (the following one)
+    uint32_t n_items, b0, b_last;
+    u32x4 dsc, dsc_next = u32x4{NO_PAGE, 0u, 0u, 0u};
+    tile_split ts{0u, 0u};
+    uint32_t F0 = 0;
+    auto make_desc = [&](uint32_t kb) -> u32x4 {  // self-scheduled: item kb + lane
+        const uint32_t k = kb + lane;
+        u32x4 d = {NO_PAGE, 0u, 0u, 1u};
+        if (k < n_items) {
+            const uint32_t f = F0 + k;
+            uint32_t b = b0;
+            while (cum[b + 1] <= f) ++b;
+            const uint32_t j = f - cum[b];
+            const uint32_t n = ntok[b];
+            const uint32_t tok0 = (EXT && window ? make_span(n, sink, window).tile(j) : j) * TILE;
+            const uint32_t page = tok0 >> bt_shift;
+            uint32_t phys = NO_PAGE;
+            if (page < bt_stride) {
+                const uint32_t p = bt[(uint64_t)b * bt_stride + page];
+                phys = (uint64_t)p < n_blocks ? p : NO_PAGE;
             }
-            if (j < batch) { cum[j + 1] = run + t; ntok[j] = n; }
-            run += __shfl(t, 63, 64);
+            const uint32_t nv = n - tok0 < (uint32_t)TILE ? n - tok0 : (uint32_t)TILE;
+            const bool whole = ts.owner(cum[b]) == ts.owner(cum[b + 1] - 1);
+            d = u32x4{phys, b, tok0, nv | (tok0 + TILE >= n ? INFO_LAST : 0u) | (whole ? INFO_WHOLE : 0u)};
         }
-        if (lane == 0) cum[0] = 0;
+        return d;
+    };
+    if constexpr (SCHED) {
+        if (w >= P) return;
+        const sched_view sv = view_of(sched, P, cap);
+        const u32x4 h = sv.hdr[w];
+        const u32x4* it = sv.items + (uint64_t)w * cap;
+        dsc = lane < cap ? it[lane] : u32x4{NO_PAGE, 0u, 0u, 1u};
+        n_items = uni(h[0]);
+        b0 = uni(h[1]);
+        b_last = uni(h[2]);
+        if (n_items == 0) return;
+        if (n_items > 64) dsc_next = lane + 64 < n_items ? it[lane + 64] : u32x4{NO_PAGE, 0u, 0u, 1u};
+    } else {
+        // tile prefix over the batch (wave 0), from the live lengths
+        if (wave == 0) {
+            uint32_t run = 0;
+            for (uint32_t base = 0; base < batch; base += 64) {
+                const uint32_t j = base + lane;
+                const uint32_t n = j < batch ? lens[j] + lens_add : 0u;
+                uint32_t t = make_span(n, EXT ? sink : 0u, EXT ? window : 0u).tiles;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const uint32_t y = __shfl_up(t, o, 64);
+                    if (lane >= (uint32_t)o) t += y;
+                }
+                if (j < batch) { cum[j + 1] = run + t; ntok[j] = n; }
+                run += __shfl(t, 63, 64);
+            }
+            if (lane == 0) cum[0] = 0;
+        }
+        lds_barrier();
+        // T = q P + r: runs 0..r-1 take q+1 tiles, the rest q
+        const uint32_t T = cum[batch];
+        ts = make_split(T, P);
+        F0 = w < P ? ts.first(w) : T;
+        const uint32_t F1 = w < P ? ts.first(w + 1) : T;
+        if (F0 >= F1) return;  // uniform over the wave: no tiles for this run (no barrier follows)
+        n_items = F1 - F0;
+        // sequence holding tile f (f < T)
+        auto seq_of = [&](uint32_t f) -> uint32_t {
+            uint32_t lo = 0, hi = batch - 1;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (cum[mid + 1] > f) hi = mid; else lo = mid + 1;
+            }
+            return lo;
+        };
+        b0 = uni(seq_of(F0));
+        b_last = uni(seq_of(F1 - 1));
+        dsc = make_desc(0);
+        if (n_items > 64) dsc_next = make_desc(64);
     }
-    lds_barrier();
-
-    // T = q P + r: workgroups 0..r-1 take q+1 tiles, the rest q
-    const uint32_t T = cum[batch];
-    const tile_split ts = make_split(T, P);
-    const uint32_t F0 = w < P ? ts.first(w) : T;
-    const uint32_t F1 = w < P ? ts.first(w + 1) : T;
-    if (F0 >= F1) return;  // uniform over the wave: no tiles for this run (no barrier follows)
-    const uint32_t n_items = F1 - F0;
 
     const uint32_t row_bytes = n_head_kv * HD * ELT;
     const uint32_t slot_bytes = 2u * row_bytes;
     const uint64_t page_bytes = (uint64_t)block_tokens * slot_bytes;
     const uint32_t kv_off = kv * HD * ELT;
     const uint32_t slot_mask = block_tokens - 1u;
-
-    // first sequence with tiles past f (f < T)
-    auto seq_of = [&](uint32_t f) -> uint32_t {
-        uint32_t lo = 0, hi = batch - 1;
-        while (lo < hi) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (cum[mid + 1] > f) hi = mid; else lo = mid + 1;
-        }
-        return lo;
-    };
-    const uint32_t b0 = uni(seq_of(F0));  // first sequence of the run
-
-    // page id of item kb + lane (invalid -> ~0): sequence found from b0 up
-    auto load_pages = [&](uint32_t kb) -> uint32_t {
-        const uint32_t k = kb + lane;
-        uint32_t phys = 0xFFFFFFFFu;
-        if (k < n_items) {
-            const uint32_t f = F0 + k;
-            uint32_t b = b0;
-            while (cum[b + 1] <= f) ++b;
-            const uint32_t j = f - cum[b];
-            const uint32_t page = ((EXT && window ? make_span(ntok[b], sink, window).tile(j) : j) * TILE) >> bt_shift;
-            if (page < bt_stride) {
-                const uint32_t p = bt[(uint64_t)b * bt_stride + page];
-                phys = (uint64_t)p < n_blocks ? p : 0xFFFFFFFFu;
-            }
-        }
-        return phys;
-    };
-    uint32_t pv = load_pages(0);
-    uint32_t pv_next = n_items > 64 ? load_pages(64) : 0u;
 
     // ---- q of this lane's head x (dims 32s + 8g .. +7: the MFMA B operand),
     // scaled into the log2 domain, split into hi + lo 16-bit halves; heads
@@ -368,7 +421,6 @@ __device__ __forceinline__ void decode_tiles(
             }
         }
     };
-    const uint32_t b_last = uni(seq_of(F1 - 1));
     const uint32_t n_stage = b_last - b0 + 1 < (uint32_t)QSEG ? b_last - b0 + 1 : (uint32_t)QSEG;
     {
         // float4 i of the staged block: sequence i / (G*32), row (i / 32) % G
@@ -409,31 +461,29 @@ __device__ __forceinline__ void decode_tiles(
         set_q(a, c);
     };
 
-    // ---- item k of the run: tile f = F0 + k of sequence seq[k]
-    // (the sequence of each item is tracked incrementally on both streams)
+    // ---- item k of the run (its descriptor, in ring slot D while in flight)
     u32x4 kr[DEPTH][KREG], vr[DEPTH][VREG];
-    uint32_t physp[DEPTH];
-    uint32_t iss_b = b0, iss_c0 = uni(cum[b0]), iss_c1 = uni(cum[b0 + 1]);
+    uint32_t physp[DEPTH], tokp[DEPTH], infop[DEPTH], seqp[DEPTH];
     // Loads of item k into ring slot D.  Tokens past the sequence re-read
     // the tile's first token (masked); with a fused append the appended
     // token is read from new_k / new_v.
     auto issue = [&](auto Dc, uint32_t k) {
         constexpr int D = decltype(Dc)::value;
-        const uint32_t f = F0 + k;
-        while (f >= iss_c1) {  // uniform: next sequence
-            ++iss_b;
-            iss_c0 = iss_c1;
-            iss_c1 = uni(cum[iss_b + 1]);
-        }
-        const uint32_t ntk = uni(ntok[iss_b]);
-        const uint32_t tok0 = (EXT && window ? make_span(ntk, sink, window).tile(f - iss_c0) : f - iss_c0) * TILE;
-        const uint32_t phys = uni((uint32_t)__builtin_amdgcn_readlane((int)pv, (int)(k & 63u)));
-        const bool pok = phys != 0xFFFFFFFFu;
+        const uint32_t li = k & 63u;
+        const u32x4& src = dsc;
+        const uint32_t phys = uni((uint32_t)__builtin_amdgcn_readlane((int)src[0], (int)li));
+        const uint32_t ib = uni((uint32_t)__builtin_amdgcn_readlane((int)src[1], (int)li));
+        const uint32_t tok0 = uni((uint32_t)__builtin_amdgcn_readlane((int)src[2], (int)li));
+        const uint32_t info = uni((uint32_t)__builtin_amdgcn_readlane((int)src[3], (int)li));
         physp[D] = phys;
+        tokp[D] = tok0;
+        infop[D] = info;
+        seqp[D] = ib;
+        const bool pok = phys != NO_PAGE;
         const uint8_t* base = pool + (uint64_t)(pok ? phys : 0u) * page_bytes +
                               (uint64_t)(tok0 & slot_mask) * slot_bytes + kv_off;
-        const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
-        const bool last = new_k != nullptr && tok0 + TILE >= ntk;  // holds the appended token
+        const uint32_t nvalid = info & 31u;
+        const bool last = new_k != nullptr && (info & INFO_LAST) != 0u;  // holds the appended token
         // K: token x of the tile; 16-bit: dims 32 st + 8 g .. (16 B per step),
         // E4M3: dims 32 g .. 32 g + 31 (two 16 B loads).  V (row layout):
         // 16-bit: tokens 4 g + r, dims 8 x ..; E4M3: tokens l / 8 + 8 j, dims
@@ -473,10 +523,10 @@ __device__ __forceinline__ void decode_tiles(
                 // ds_bpermute -- K: lane (g, pos) takes dims 32 g + 16 j + 4 w
                 // from lane 8 g + 4 j + w; V: a lane holding token pos takes
                 // dims 16 (lane % 8) + 4 w from lane 32 + 4 (lane % 8) + w.
-                const uint32_t pos = ntk - 1u - tok0;
+                const uint32_t pos = nvalid - 1u;
                 const bool kh = lane < 32u;
                 const float* nrow = reinterpret_cast<const float*>(kh ? new_k : new_v) +
-                                    (uint64_t)iss_b * n_head_kv * HD + kv * HD + 4u * (lane & 31u);
+                                    (uint64_t)ib * n_head_kv * HD + kv * HD + 4u * (lane & 31u);
                 const float4 nv = *reinterpret_cast<const float4*>(nrow);
                 const float sc = kh ? k_scale[kv] : v_scale[kv];
                 const uint32_t c4 = e4m3_code(nv.x / sc) | (e4m3_code(nv.y / sc) << 8) |
@@ -499,8 +549,8 @@ __device__ __forceinline__ void decode_tiles(
                 });
             }
         } else {
-            const uint32_t pos = ntk - 1u - tok0;  // appended token within the tile
-            const uint64_t nrow = (uint64_t)iss_b * row_bytes + kv_off;
+            const uint32_t pos = nvalid - 1u;  // appended token within the tile (when last)
+            const uint64_t nrow = (uint64_t)ib * row_bytes + kv_off;
             {
                 const bool isnew = last && x == pos;
                 const uint8_t* src = isnew ? new_k + nrow : base + (x < nvalid ? x : 0u) * slot_bytes;
@@ -529,15 +579,13 @@ __device__ __forceinline__ void decode_tiles(
     for (int db = 0; db < HD / 16; ++db) acc[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // Write this wave's state for sequence b: the final rows when the whole
-    // sequence lies in this workgroup, else the partial for slot w + b; reset.
+    // sequence lies in this run, else the partial for slot w + b; reset.
     // E4M3 pages: the V scale of this kv head multiplies the weighted sum
     const float vsc = F8 ? v_scale[kv] : 1.0f;
-    auto flush = [&](uint32_t b) {
+    auto flush = [&](uint32_t b, bool whole) {
         float L = l_own;
         L += __shfl_xor(L, 16, 64);
         L += __shfl_xor(L, 32, 64);
-        const uint32_t c0 = cum[b], c1 = cum[b + 1];
-        const bool whole = ts.owner(c0) == ts.owner(c1 - 1);
         if (hv) {
             const uint32_t qh = kv * group + x;
             if (whole) {
@@ -565,18 +613,16 @@ __device__ __forceinline__ void decode_tiles(
     // transposed-read address of lane (g, r*4+b): token row 4g + r,
     // dims 4b .. 4b+3 of each 16-dim block
     const uint32_t tr_off = (4 * g + (x >> 2)) * VROW + (x & 3u) * 8;
-    uint32_t cmp_b = b0, cmp_c0 = uni(cum[b0]), cmp_c1 = uni(cum[b0 + 1]);
 
-    auto compute = [&](auto Dc, uint32_t k) {
+    auto compute = [&](auto Dc) {
         constexpr int D = decltype(Dc)::value;
-        const uint32_t f = F0 + k;
-        const uint32_t ntk = uni(ntok[cmp_b]);
-        const bool win = EXT && window != 0u;
-        const span sp = make_span(ntk, win ? sink : 0u, win ? window : 0u);
-        const uint32_t tok0 = (win ? sp.tile(f - cmp_c0) : f - cmp_c0) * TILE;
-        const uint32_t nvalid = ntk - tok0 < (uint32_t)TILE ? ntk - tok0 : (uint32_t)TILE;
         const uint32_t phys = physp[D];
-        if (phys == 0xFFFFFFFFu) return;  // masked page: its tokens do not count (uniform)
+        if (phys == NO_PAGE) return;  // masked page: its tokens do not count (uniform)
+        const uint32_t tok0 = tokp[D];
+        const uint32_t info = infop[D];
+        const uint32_t nvalid = info & 31u;
+        const uint32_t cb = seqp[D];
+        const bool win = EXT && window != 0u;
 
         // V tile rows into LDS as f16 (16-bit lane (g, x): tokens 4g..4g+3,
         // dims 8x..8x+7; E4M3 lane l: tokens l/8 and l/8 + 8, dims 16 (l%8)..)
@@ -610,19 +656,29 @@ __device__ __forceinline__ void decode_tiles(
             s = K::mma(a, qa[st], s);
             s = K::mma(a, qb[st], s);
         }
-        if (win ? sp.partial(tok0) : nvalid < (uint32_t)TILE) {  // uniform
+        if constexpr (EXT) {
+            if (win) {  // uniform
+                const span sp = make_span(ntok[cb], sink, window);
+                if (sp.partial(tok0)) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const bool ok = win ? sp.valid(tok0 + 4 * g + r) : 4 * g + r < nvalid;
-                s[r] = ok ? s[r] : -__builtin_inff();
+                    for (int r = 0; r < 4; ++r)
+                        s[r] = sp.valid(tok0 + 4 * g + r) ? s[r] : -__builtin_inff();
+                }
+            } else if (nvalid < (uint32_t)TILE) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] = 4 * g + r < nvalid ? s[r] : -__builtin_inff();
             }
+        } else if (nvalid < (uint32_t)TILE) {  // uniform
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] = 4 * g + r < nvalid ? s[r] : -__builtin_inff();
         }
         // fused append: store the appended token's K/V slice of this kv
         // head from the registers that already hold it (E4M3: its codes;
         // K lane (g, pos): dims 32 g .. 32 g + 31, V: the lanes holding
         // token pos, dims 16 (lane % 8) ..)
-        if constexpr (F8) if (new_k != nullptr && tok0 + TILE >= ntk) {
-            const uint32_t pos = ntk - 1u - tok0;
+        const bool app = new_k != nullptr && (info & INFO_LAST) != 0u;
+        if constexpr (F8) if (app) {
+            const uint32_t pos = nvalid - 1u;
             uint8_t* dst = pool + (uint64_t)phys * page_bytes +
                            (uint64_t)((tok0 & slot_mask) + pos) * slot_bytes + kv_off;
             if (x == pos) {
@@ -637,8 +693,8 @@ __device__ __forceinline__ void decode_tiles(
                     *reinterpret_cast<u32x4*>(dst + row_bytes + 16 * (lane & 7u)) = vr[D][j];
             });
         }
-        if constexpr (!F8) if (new_k != nullptr && tok0 + TILE >= ntk) {
-            const uint32_t pos = ntk - 1u - tok0;
+        if constexpr (!F8) if (app) {
+            const uint32_t pos = nvalid - 1u;
             uint8_t* dst = pool + (uint64_t)phys * page_bytes +
                            (uint64_t)((tok0 & slot_mask) + pos) * slot_bytes + kv_off;
             if (x == pos) {
@@ -673,7 +729,7 @@ __device__ __forceinline__ void decode_tiles(
             e += __shfl_xor(e, 32, 64);
             const uint32_t a = tok0 / TILE;
             if (g == 0 && hv && a < rec_row)
-                reinterpret_cast<float2*>(tile_rec)[((uint64_t)cmp_b * rec_row + a) * n_head +
+                reinterpret_cast<float2*>(tile_rec)[((uint64_t)cb * rec_row + a) * n_head +
                                                     kv * group + x] = make_float2(e, m_own);
         }
         // P^T operand (tokens 4g..4g+3 of head x) straight from the scores
@@ -697,13 +753,24 @@ __device__ __forceinline__ void decode_tiles(
     // chunk issues the same load stream -- DEPTH tiles up front, one refill
     // per step while the chunk lasts; refills past the chunk's last tile
     // re-read that tile (a cache hit, never computed) -- and the steps nest,
-    // so each step waits for exactly its own tile.
+    // so each step waits for exactly its own tile.  A chunk never straddles
+    // a batch of 64 descriptors (CHUNK divides 64).
+    static_assert(64 % CHUNK == 0, "chunks stay inside one descriptor batch");
+    uint32_t cmp_b = b0;
+    bool cmp_whole = (uni((uint32_t)__builtin_amdgcn_readlane((int)dsc[3], 0)) & INFO_WHOLE) != 0u;
     load_q(b0);
     for (uint32_t c0 = 0; c0 < n_items; c0 += CHUNK) {
         const uint32_t cn = n_items - c0 < (uint32_t)CHUNK ? n_items - c0 : (uint32_t)CHUNK;
-        if (c0 != 0 && (c0 & 63u) == 0u) {  // next batch of page ids
-            pv = pv_next;
-            if (c0 + 64 < n_items) pv_next = load_pages(c0 + 64);
+        if (c0 != 0 && (c0 & 63u) == 0u) {  // next batch of descriptors
+            dsc = dsc_next;
+            if (c0 + 64 < n_items) {
+                if constexpr (SCHED) {
+                    const u32x4* it = view_of(sched, P, cap).items + (uint64_t)w * cap;
+                    dsc_next = c0 + 64 + lane < n_items ? it[c0 + 64 + lane] : u32x4{NO_PAGE, 0u, 0u, 1u};
+                } else {
+                    dsc_next = make_desc(c0 + 64);
+                }
+            }
         }
         const uint32_t klast = c0 + cn - 1;
         static_for<0, DEPTH>([&](auto Dc) {
@@ -715,16 +782,13 @@ __device__ __forceinline__ void decode_tiles(
             constexpr int D = kk % DEPTH;
             if ((uint32_t)kk >= cn) return false;  // uniform
             const uint32_t k = c0 + kk;
-            if (F0 + k >= cmp_c1) {  // uniform: the run moves to the next sequence
-                flush(cmp_b);
-                do {
-                    ++cmp_b;
-                    cmp_c0 = cmp_c1;
-                    cmp_c1 = uni(cum[cmp_b + 1]);
-                } while (F0 + k >= cmp_c1);
+            if (seqp[D] != cmp_b) {  // uniform: the run moves to the next sequence
+                flush(cmp_b, cmp_whole);
+                cmp_b = seqp[D];
+                cmp_whole = (infop[D] & INFO_WHOLE) != 0u;
                 load_q(cmp_b);
             }
-            compute(ic<D>{}, k);
+            compute(ic<D>{});
             // the refill stays below the slot's last use, so its loads reuse
             // the slot's registers
             __builtin_amdgcn_sched_barrier(0);
@@ -735,63 +799,90 @@ __device__ __forceinline__ void decode_tiles(
             return true;
         });
     }
-    flush(cmp_b);
+    flush(cmp_b, cmp_whole);
 }
 
-// Log-sum-exp merge of the workgroup partials of every sequence that spans
-// more than one workgroup.  Grid (ceil(n_head*128/64), batch), 256 threads:
-// lane = output element, the 4 waves split the sequence's partials (each
-// wave fetches up to NB of them in one memory round trip) and combine their
-// results through LDS.  Recomputes the split kernel's tile runs from the same
-// lengths (every workgroup between a sequence's first and last holds tiles
-// of it); writes zeros for empty sequences; sequences inside one workgroup
-// were finished by the split kernel.
-extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
+// Log-sum-exp merge of the run partials of every sequence that spans more
+// than one run.  Grid (ceil(n_head*128/64), batch), 256 threads: lane =
+// output element, the 4 waves split the sequence's partials (each wave
+// fetches up to NB of them in one memory round trip) and combine their
+// results through LDS.  The runs holding the sequence (every run between
+// its first and last holds tiles of it) come from the step schedule (SCHED)
+// or are recomputed from the same lengths as the split kernel; writes zeros
+// for empty sequences; sequences inside one run were finished by the split
+// kernel.
+template <bool SCHED>
+__device__ __forceinline__ void merge_body(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
     const uint32_t* __restrict__ lens, uint32_t lens_add, uint32_t batch, uint32_t n_head,
-    uint32_t head_dim, uint32_t P, uint32_t sink, uint32_t window, float* __restrict__ fin) {
+    uint32_t head_dim, uint32_t P, uint32_t sink, uint32_t window, float* __restrict__ fin,
+    const u32x4* __restrict__ seqs) {
     constexpr int NB = 16;
     __shared__ float sM[4][64], sL[4][64], sA[4][64];
     const uint32_t b = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6;
-    uint32_t tot = 0, before = 0, mine = 0;
-    for (uint32_t j = lane; j < batch; j += 64) {
-        const uint32_t t = make_span(lens[j] + lens_add, sink, window).tiles;
-        tot += t;
-        before += j < b ? t : 0u;
-        mine += j == b ? t : 0u;
-    }
+    uint32_t w0, w1;
+    bool empty;
+    if constexpr (SCHED) {
+        const u32x4 r = seqs[b];
+        w0 = uni(r[0]);
+        w1 = uni(r[1]);
+        empty = uni(r[3]) == 0u;
+    } else {
+        uint32_t tot = 0, before = 0, mine = 0;
+        for (uint32_t j = lane; j < batch; j += 64) {
+            const uint32_t t = make_span(lens[j] + lens_add, sink, window).tiles;
+            tot += t;
+            before += j < b ? t : 0u;
+            mine += j == b ? t : 0u;
+        }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        tot += __shfl_xor(tot, o, 64);
-        before += __shfl_xor(before, o, 64);
-        mine += __shfl_xor(mine, o, 64);
+        for (int o = 32; o >= 1; o >>= 1) {
+            tot += __shfl_xor(tot, o, 64);
+            before += __shfl_xor(before, o, 64);
+            mine += __shfl_xor(mine, o, 64);
+        }
+        empty = mine == 0;
+        const tile_split ts = make_split(tot, P);
+        w0 = empty ? 0u : ts.owner(before);
+        w1 = empty ? 0u : ts.owner(before + mine - 1);
     }
     const uint32_t e = blockIdx.x * 64 + lane;
     const bool live = e < n_head * head_dim;
     const uint64_t orow = (uint64_t)b * n_head * head_dim + e;
-    if (mine == 0) {  // uniform
+    if (empty) {  // uniform
         if (wave == 0 && live) out[orow] = 0.0f;
         return;
     }
-    const tile_split ts = make_split(tot, P);
-    const uint32_t w0 = ts.owner(before), w1 = ts.owner(before + mine - 1);
     if (w0 == w1) return;  // finished by the split kernel
     const uint32_t ec = live ? e : 0u;
-    const uint32_t qh = ec / head_dim, d = ec - qh * head_dim;
+    // the 64 lanes lie in one head (head_dim is a multiple of 64): the slot
+    // index is wave-uniform, so (m, l) come by scalar loads and every acc
+    // load is one SGPR base plus the lane's dim, all issued before any wait
+    const uint32_t qh = uni(blockIdx.x * 64u / head_dim), d = ec - qh * head_dim;
     const uint32_t ns = w1 - w0 + 1;
     float M = NEG_BIG, Ls = 0.0f, A = 0.0f;
-    for (uint32_t s0 = wave; s0 < ns; s0 += 4 * NB) {
+    static_assert(NB <= 64, "one (m, l) per lane");
+    for (uint32_t s0 = uni(wave); s0 < ns; s0 += 4 * NB) {
+        // (m, l) of the wave's NB partials by one vector load (lane i % NB
+        // takes partial s0 + 4 i), read back by readlane; acc: NB loads
+        const uint32_t li = lane & (NB - 1);
+        const uint32_t sl = s0 + 4 * li < ns ? s0 + 4 * li : s0;
+        const float2 mlv = reinterpret_cast<const float2*>(part_ml)[(uint64_t)(w0 + sl + b) * n_head + qh];
         float2 v[NB];
         float a[NB];
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const uint32_t s = s0 + 4 * i < ns ? s0 + 4 * i : s0;
             const uint64_t slot = (uint64_t)(w0 + s + b) * n_head + qh;
-            v[i] = reinterpret_cast<const float2*>(part_ml)[slot];
-            a[i] = part_acc[slot * head_dim + d];
+            a[i] = (part_acc + slot * head_dim)[d];
         }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any wait
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            v[i] = make_float2(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mlv.x), i)),
+                               __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mlv.y), i)));
         float mx = M;
 #pragma unroll
         for (int i = 0; i < NB; ++i)
@@ -827,6 +918,109 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
     }
     out[orow] = L > 0.0f ? Acc / L : 0.0f;
     if (fin != nullptr && d == 0) reinterpret_cast<float2*>(fin)[(uint64_t)b * n_head + qh] = make_float2(Mx, L);
+}
+
+
+extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge(
+    const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
+    const uint32_t* __restrict__ lens, uint32_t lens_add, uint32_t batch, uint32_t n_head,
+    uint32_t head_dim, uint32_t P, uint32_t sink, uint32_t window, float* __restrict__ fin) {
+    merge_body<false>(part_acc, part_ml, out, lens, lens_add, batch, n_head, head_dim, P, sink,
+                      window, fin, nullptr);
+}
+
+// The merge of a scheduled call: the sequence's runs are the step
+// schedule's sequence records.
+extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_merge_sched(
+    const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
+    const u32x4* __restrict__ sched, uint32_t P, uint32_t cap, uint32_t batch, uint32_t n_head,
+    uint32_t head_dim) {
+    merge_body<true>(part_acc, part_ml, out, nullptr, 0u, batch, n_head, head_dim, P, 0u, 0u,
+                     nullptr, view_of(sched, P, cap).seqs);
+}
+
+// Step schedule of the token-balanced decode, built once per decode step
+// from the live lengths and block tables and read by every layer's split and
+// merge kernels (the layers of a step share one block table and one set of
+// positions).  The batch's 16-token tiles -- at most the tiles the block
+// table can address per sequence; tokens past the table are masked in any
+// case -- are cut into P equal runs as the self-scheduled kernel cuts them,
+// and every tile gets its item descriptor.  Grid-stride over
+// max(P, batch, batch * bt_stride * block_tokens / 16) indices, 256 threads
+// per workgroup; dynamic LDS 4 * (2 * batch + 1) bytes (each workgroup scans
+// the lengths itself).
+extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_schedule(
+    const uint32_t* __restrict__ lens, uint32_t lens_add, const uint32_t* __restrict__ bt,
+    uint32_t bt_stride, uint64_t n_blocks, uint32_t batch, uint32_t block_tokens, uint32_t bt_shift,
+    uint32_t P, uint32_t cap, uint32_t n_index, u32x4* __restrict__ sched) {
+    extern __shared__ __align__(16) uint32_t sm[];
+    uint32_t* cum = sm;
+    uint32_t* ntok = sm + batch + 1;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t max_tiles = bt_stride * (block_tokens / TILE);
+    if (threadIdx.x < 64) {
+        uint32_t run = 0;
+        for (uint32_t base = 0; base < batch; base += 64) {
+            const uint32_t j = base + lane;
+            const uint32_t n = j < batch ? lens[j] + lens_add : 0u;
+            const uint32_t full = n / TILE + (n % TILE != 0u);
+            uint32_t t = full < max_tiles ? full : max_tiles;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t y = __shfl_up(t, o, 64);
+                if (lane >= (uint32_t)o) t += y;
+            }
+            if (j < batch) { cum[j + 1] = run + t; ntok[j] = n; }
+            run += __shfl(t, 63, 64);
+        }
+        if (lane == 0) cum[0] = 0;
+    }
+    __syncthreads();
+    const uint32_t T = cum[batch];
+    const tile_split ts = make_split(T, P);
+    auto seq_of = [&](uint32_t f) -> uint32_t {  // sequence holding tile f < T
+        uint32_t lo = 0, hi = batch - 1;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (cum[mid + 1] > f) hi = mid; else lo = mid + 1;
+        }
+        return lo;
+    };
+    const sched_view sv = view_of(sched, P, cap);
+    u32x4* hdr = const_cast<u32x4*>(sv.hdr);
+    u32x4* items = const_cast<u32x4*>(sv.items);
+    u32x4* seqs = const_cast<u32x4*>(sv.seqs);
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n_index; i += gridDim.x * blockDim.x) {
+        if (i < P) {  // run header
+            const uint32_t f0 = ts.first(i) < T ? ts.first(i) : T;
+            const uint32_t f1 = ts.first(i + 1) < T ? ts.first(i + 1) : T;
+            const uint32_t n = f1 > f0 ? f1 - f0 : 0u;
+            hdr[i] = u32x4{n, n ? seq_of(f0) : 0u, n ? seq_of(f1 - 1) : 0u, 0u};
+        }
+        if (i < T) {  // item descriptor of tile i
+            const uint32_t b = seq_of(i);
+            const uint32_t c0 = cum[b], c1 = cum[b + 1];
+            const uint32_t tok0 = (i - c0) * TILE;
+            const uint32_t n = ntok[b];
+            const uint32_t page = tok0 >> bt_shift;
+            uint32_t phys = NO_PAGE;
+            if (page < bt_stride) {
+                const uint32_t p = bt[(uint64_t)b * bt_stride + page];
+                phys = (uint64_t)p < n_blocks ? p : NO_PAGE;
+            }
+            const uint32_t nv = n - tok0 < (uint32_t)TILE ? n - tok0 : (uint32_t)TILE;
+            const bool whole = ts.owner(c0) == ts.owner(c1 - 1);
+            const uint32_t w = ts.owner(i);
+            const uint32_t k = i - ts.first(w);  // < cap: a run holds at most ceil(T / P) tiles
+            items[(uint64_t)w * cap + k] =
+                u32x4{phys, b, tok0, nv | (tok0 + TILE >= n ? INFO_LAST : 0u) | (whole ? INFO_WHOLE : 0u)};
+        }
+        if (i < batch) {  // sequence record
+            const uint32_t c0 = cum[i], c1 = cum[i + 1];
+            seqs[i] = c1 > c0 ? u32x4{ts.owner(c0), ts.owner(c1 - 1), ntok[i], c1 - c0}
+                              : u32x4{0u, 0u, ntok[i], 0u};
+        }
+    }
 }
 
 // H2O attention mass of one decode call (the score StreamingKvManager::
@@ -867,23 +1061,27 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_mass(
 // (256 VGPRs, no AGPR copies, which would wait for the loads they copy); 2
 // tiles in flight per wave (measured faster than 4: deeper queues slow the
 // random page reads).
-#define EH_TILES_ONE(NAME, DT, G, EXT)                                                              \
+#define EH_TILES_ONE(NAME, DT, G, EXT, SCHED)                                                       \
     extern "C" __global__ __launch_bounds__(512, 1) void NAME(                                     \
         const float* q, uint8_t* pool, uint64_t n_blocks, const uint32_t* bt, uint32_t bt_stride,  \
         const uint32_t* lens, uint32_t lens_add, const uint8_t* new_k, const uint8_t* new_v,       \
         uint32_t batch, float* out, float* part_acc, float* part_ml, uint32_t n_head,              \
         uint32_t n_head_kv, uint32_t block_tokens, uint32_t bt_shift, float scale_log2,            \
         uint32_t n_runs, uint32_t sink, uint32_t window, float* tile_rec, float* fin,              \
-        uint32_t rec_row, const float* k_scale, const float* v_scale) {                            \
-        decode_tiles<DT, G, 2, 16, EXT>(q, pool, n_blocks, bt, bt_stride, lens, lens_add, new_k,   \
-                                        new_v, batch, out, part_acc, part_ml, n_head, n_head_kv,   \
-                                        block_tokens, bt_shift, scale_log2, n_runs, sink, window,  \
-                                        tile_rec, fin, rec_row, k_scale, v_scale);                 \
+        uint32_t rec_row, const float* k_scale, const float* v_scale, const u32x4* sched,          \
+        uint32_t cap) {                                                                            \
+        decode_tiles<DT, G, 2, 16, EXT, SCHED>(q, pool, n_blocks, bt, bt_stride, lens, lens_add,   \
+                                               new_k, new_v, batch, out, part_acc, part_ml, n_head, \
+                                               n_head_kv, block_tokens, bt_shift, scale_log2,      \
+                                               n_runs, sink, window, tile_rec, fin, rec_row,       \
+                                               k_scale, v_scale, sched, cap);                      \
     }
-// _ext: with the protected-sinks range and attention-mass records
-#define EH_TILES(DTN, DT, G)                                                       \
-    EH_TILES_ONE(eh_decode_tiles_##DTN##_hd128_g##G, DT, G, false)                \
-    EH_TILES_ONE(eh_decode_tiles_##DTN##_hd128_g##G##_ext, DT, G, true)
+// _ext: with the protected-sinks range and attention-mass records;
+// _sched: the run's items from a step schedule
+#define EH_TILES(DTN, DT, G)                                                         \
+    EH_TILES_ONE(eh_decode_tiles_##DTN##_hd128_g##G, DT, G, false, false)           \
+    EH_TILES_ONE(eh_decode_tiles_##DTN##_hd128_g##G##_ext, DT, G, true, false)      \
+    EH_TILES_ONE(eh_decode_tiles_##DTN##_hd128_g##G##_sched, DT, G, false, true)
 
 #define EH_TILES_ALL(DTN, DT) \
     EH_TILES(DTN, DT, 1)      \

@@ -189,6 +189,55 @@ class PagedAttention:
             int(stride), buf(start_pos)[0], int(batch), qp, qb, op, ob, int(n_head), int(head_dim),
             int(plan[1]), wp, wb))
 
+    # ---- step schedule: the work split computed once per decode step -------
+    @staticmethod
+    def schedule_bytes(batch, bt_stride, block_tokens, plan):
+        """Bytes of the step schedule for `batch` sequences with tables of
+        `bt_stride` entries and a token-balanced plan."""
+        return int(_lib.load().eh_decode_schedule_bytes(int(batch), int(bt_stride),
+                                                         int(block_tokens), int(plan[1])))
+
+    @staticmethod
+    def schedule_buffer(batch, bt_stride, block_tokens, plan, device="cuda"):
+        n = PagedAttention.schedule_bytes(batch, bt_stride, block_tokens, plan)
+        return torch.empty((n + 15) // 16 * 4, dtype=torch.int32, device=device)
+
+    def build_schedule(self, stream, layout, block_tables, lens, lens_add, plan, sched):
+        """eh_decode_schedule: the token-balanced split of the step, from
+        block_tables [B, stride] and lens [B] (+ lens_add: 1 with the
+        positions a fused step appends at)."""
+        if plan[0] != 0:
+            raise ValueError("a step schedule needs a token-balanced plan (tokens_per_split 0)")
+        batch, stride = block_tables.shape
+        bp, bb = buf(block_tables)
+        sp, sb = buf(sched)
+        lay = layout.c()
+        check(self._L.eh_decode_schedule(self._ctx.handle, stream_handle(stream), C.byref(lay), bp,
+                                         bb, int(stride), buf(lens)[0], int(lens_add), int(batch),
+                                         int(plan[1]), sp, sb))
+
+    def append_decode_scheduled(self, stream, layout, pool, keys, values, sched, bt_stride, q,
+                                out, n_head, head_dim, plan, workspace, k_scale=None,
+                                v_scale=None):
+        """One layer's decode step from a step schedule: keys/values [B,
+        row_len] appended at the schedule's positions (None: decode only),
+        then q [B, n_head, head_dim] attends (append_decode_batched /
+        decode_batched with the split read from `sched`).  E4M3 pools pass
+        f32 rows and k_scale / v_scale."""
+        batch = q.shape[0]
+        pp, pb = buf(pool)
+        kp, kb = buf(keys)
+        vp_, vb = buf(values)
+        sp, sb = buf(sched)
+        qp, qb = buf(q)
+        op, ob = buf(out)
+        wp, wb = buf(workspace)
+        lay = layout.c()
+        check(self._L.eh_append_decode_scheduled(
+            self._ctx.handle, stream_handle(stream), C.byref(lay), pp, pb, kp, kb, vp_, vb, sp, sb,
+            int(bt_stride), int(batch), qp, qb, op, ob, int(n_head), int(head_dim), int(plan[1]),
+            wp, wb, buf(k_scale)[0], buf(v_scale)[0]))
+
     def append_decode_batched_noalloc(self, stream, layout, pool, keys, values, block_tables,
                                       start_pos, q, out, n_head, head_dim, grid):
         """append_decode_batched with the library's per-GPU static scratch in
