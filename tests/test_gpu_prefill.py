@@ -118,6 +118,38 @@ def test_chunk_on_scattered_context(dev, case):
     check_close(out.cpu().numpy(), ref, dtype, str(case))
 
 
+@pytest.mark.parametrize("hd,nh,nkv", [(128, 32, 8), (64, 16, 2)])
+def test_bf16_values_beyond_f16_range(dev, hd, nh, nkv):
+    """bf16 pages are staged as f16 (exact below 2^16); a tile holding a finite
+    value of magnitude >= 2^16 takes the exact bf16 path.  Large V values in
+    some tiles, a large K value in another (its key then dominates the
+    softmax), normal tiles around them: every row against the oracle."""
+    bt, p0, nq = 16, 700, 140
+    rng = np.random.default_rng(4242 + hd)
+    total = p0 + nq
+    n_pages = -(-total // bt)
+    pool_pages = n_pages + 5
+    table = rng.permutation(pool_pages)[:n_pages].astype(np.uint32)
+    host = rng.standard_normal((pool_pages, bt, 2, nkv, hd)).astype(np.float32)
+    # V values beyond f16's range on the page holding keys 64.. (first tile)
+    host[table[4], 3, 1, 0, :8] = [7.0e4, -3.1e5, 1.0e6, 65536.0, -65536.0, 2.5e7, 9.0e4, -7.0e4]
+    # a K value beyond f16's range on the page holding keys 512..
+    host[table[32], 5, 0, nkv - 1, 3] = 1.2e5
+    # near the limit but in range (65280 is the largest bf16 below 2^16): f16 path
+    host[table[20], 0, 1, 0, :2] = [65280.0, -65280.0]
+    t = torch.from_numpy(host.reshape(-1)).to(torch.bfloat16)
+    dpool, hpool = t.to(dev), t.to(torch.float32).numpy()
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    out = torch.full((nq, nh, hd), float("nan"), device=dev)
+    FlashAttention2(0).launch(None, torch.from_numpy(q).to(dev), dpool, i32(table, dev), out, nh,
+                              nkv, hd, bt, nq, p0, kv_dtype=KvDataType.BF16)
+    torch.cuda.synchronize()
+    ref = orc.prefill_causal(hpool, table, bt, q, nq, p0, nh, nkv, hd)
+    g = out.cpu().numpy()
+    assert np.abs(ref).max() > 1e3                       # the large values reach the output
+    check_close(g, ref, KvDataType.BF16, "bf16 beyond f16 range", stress=True)
+
+
 def test_pos_ptr_overrides_offset(dev):
     # flash_attention_2.cu:43: a device position replaces the host pos_offset.
     dtype, nh, nkv, hd, bt = KvDataType.F16, 8, 2, 128, 16

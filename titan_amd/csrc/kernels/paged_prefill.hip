@@ -25,10 +25,14 @@
 //     straight from registers (keys permuted consistently between P and V^T);
 //   * the accumulators are rescaled only when a row maximum grows by more
 //     than 2^8 (exact: every term uses the same stale maximum);
-//   * operands: f16 KV -> f16 MFMA with f16 Q and P; bf16 KV -> bf16 MFMA
-//     with Q and P each split into hi + lo bf16 parts (two MFMAs per product,
-//     ~16 significant bits, so short contexts stay within 2e-3); f32 KV ->
-//     f32 MFMA (no operand rounding);
+//   * operands: f16 KV -> f16 MFMA with f16 Q and P; bf16 KV -> widened to
+//     f16 as the tiles are staged (exact: a bf16 significand has 8 bits, and
+//     every finite bf16 below 2^16 in magnitude is an f16, down to 2^-14;
+//     below that the f16 subnormals keep the value to 2^-24), then the f16
+//     path; a staged tile holding a finite bf16 of magnitude >= 2^16 is
+//     re-staged raw and computed on bf16 MFMAs with Q and P each split into
+//     hi + lo bf16 parts (two MFMAs per product, ~16 significant bits);
+//     f32 KV -> f32 MFMA (no operand rounding);
 //   * workgroups are mapped XCD-major so the tiles of one (sequence, kv head)
 //     share one XCD's L2.
 // Invalid block-table entries (beyond the table or >= n_blocks) mask their
@@ -165,7 +169,28 @@ __device__ __forceinline__ uint4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
 struct lds_hdr {
     uint32_t tile_bad[2];  // tile index whose keys include an invalid page
     uint32_t slice_base;
+    uint32_t tile_big[2];  // bf16 pages: tile index holding a value beyond f16's range
 };
+
+// Eight bf16 (four dwords) as eight f16, and the running packed maximum of
+// the bf16 exponent fields (finite values of magnitude >= 2^16 -- exponent
+// field >= 143 -- do not fit an f16; inf / NaN fields count too, which only
+// sends such a tile to the exact bf16 path).  In-range values convert
+// exactly; the rounding mode only matters below 2^-14 (f16 subnormals).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 bf16x8_to_f16(uint4 w, u16x2& emax) {
+    uint32_t r[4];
+    const uint32_t in[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = __builtin_bit_cast(float, in[i] << 16);
+        const float hi = __builtin_bit_cast(float, in[i] & 0xFFFF0000u);
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+        emax = __builtin_elementwise_max(emax, __builtin_bit_cast(u16x2, in[i] & 0x7F807F80u));
+    }
+    return make_uint4(r[0], r[1], r[2], r[3]);
+}
+constexpr unsigned short BF16_F16_LIMIT = 143u << 7;  // exponent field of 2^16
 
 template <int DT, int HD>
 __device__ __forceinline__ void prefill(
@@ -176,7 +201,11 @@ __device__ __forceinline__ void prefill(
     float* __restrict__ out, uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens,
     int bt_shift, uint32_t row_bytes, float scale_log2, uint64_t n_blocks, uint8_t* smem,
     const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
-    typedef op_t<DT> O;
+    // bf16 pages are staged as f16 and take the f16 operands; OB: the exact
+    // bf16 path of tiles beyond f16's range
+    constexpr bool B2H = DT == DT_BF16;
+    typedef op_t<B2H ? DT_F16 : DT> O;
+    typedef op_t<DT_BF16> OB;
     typedef typename O::v opv;
     typedef geo<DT, HD> Gm;
     constexpr int N = Gm::N;
@@ -270,7 +299,7 @@ __device__ __forceinline__ void prefill(
     const uint64_t page_bytes = (uint64_t)block_tokens * 2u * row_bytes;
     // E4M3 pages: one byte per element, a load item is 8 codes per key
     constexpr bool F8 = DT == DT_FP8;
-    constexpr int CT = F8 ? DT_F16 : DT;  // MFMA operand type
+    constexpr int CT = (F8 || B2H) ? DT_F16 : DT;  // MFMA operand type
     constexpr uint32_t SE = F8 ? 1u : (uint32_t)Gm::ELT;  // stored element bytes
     const uint32_t head_off = hk * HD * SE + part * (16 / Gm::ELT) * SE;
     uint4 kr[4], vr[4];
@@ -278,13 +307,24 @@ __device__ __forceinline__ void prefill(
 
     const uint32_t slot_bytes = 2u * row_bytes;
     const bool page4 = (block_tokens & 3u) == 0u;  // 4 aligned keys share a page
-    auto issue = [&](uint32_t t) {
-        const uint32_t base = hdr->slice_base;
+    // page id of table entry e: from the LDS slice, or (direct) from the
+    // global table with the slice's bounds checks -- the re-stage of a tile
+    // runs after the slice may have moved on to the next tile
+    auto page_of = [&](uint32_t e, bool direct) -> uint32_t {
+        if (!direct) return slice[e - hdr->slice_base];
+        uint32_t v = 0xFFFFFFFFu;
+        if (e < bt_entries) {
+            const uint32_t p = bt[e];
+            if ((uint64_t)p < n_blocks) v = p;
+        }
+        return v;
+    };
+    auto issue = [&](uint32_t t, bool direct = false) {
         const uint32_t key0 = t * N + 4 * kg;
         okbits = 0;
         if (page4) {
             const uint32_t e = entry_of(key0);
-            const uint32_t phys = slice[e - base];
+            const uint32_t phys = page_of(e, direct);
             const uint32_t slot = key0 - e * block_tokens;
             const bool pv = phys != 0xFFFFFFFFu;
             const uint8_t* p = pool + (uint64_t)(pv ? phys : 0u) * page_bytes +
@@ -308,7 +348,7 @@ __device__ __forceinline__ void prefill(
         } else {
             uint32_t phys[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) phys[j] = slice[entry_of(key0 + j) - base];
+            for (int j = 0; j < 4; ++j) phys[j] = page_of(entry_of(key0 + j), direct);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t key = key0 + j;
@@ -332,7 +372,7 @@ __device__ __forceinline__ void prefill(
         }
     };
 
-    auto commit = [&](uint32_t t, int buf) {
+    auto commit = [&](uint32_t t, int buf, bool raw = false) {
         uint8_t* ks = stage + buf * Gm::STAGE;
         uint8_t* vs = ks + Gm::KBYTES;
         if constexpr (F8) {  // codes -> f16, then the f16 staging below
@@ -340,6 +380,17 @@ __device__ __forceinline__ void prefill(
             for (int j = 0; j < 4; ++j) {
                 kr[j] = e4m3x8_to_f16(kr[j].x, kr[j].y);
                 vr[j] = e4m3x8_to_f16(vr[j].x, vr[j].y);
+            }
+        }
+        if constexpr (B2H) {
+            if (!raw) {  // bf16 -> f16; a value beyond f16's range flags the tile
+                u16x2 emax = {0, 0};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    kr[j] = bf16x8_to_f16(kr[j], emax);
+                    vr[j] = bf16x8_to_f16(vr[j], emax);
+                }
+                if (emax[0] >= BF16_F16_LIMIT || emax[1] >= BF16_F16_LIMIT) hdr->tile_big[buf] = t;
             }
         }
 #pragma unroll
@@ -415,7 +466,12 @@ __device__ __forceinline__ void prefill(
     float m_run = -1e30f, l_run = 0.f;
 
     // ---- prologue
-    if (tid == 0) { hdr->tile_bad[0] = 0xFFFFFFFFu; hdr->tile_bad[1] = 0xFFFFFFFFu; }
+    if (tid == 0) {
+        hdr->tile_bad[0] = 0xFFFFFFFFu;
+        hdr->tile_bad[1] = 0xFFFFFFFFu;
+        hdr->tile_big[0] = 0xFFFFFFFFu;
+        hdr->tile_big[1] = 0xFFFFFFFFu;
+    }
     stage_slice(0);
     __syncthreads();
     const bool loader = tid < NL;  // uniform per wave
@@ -432,6 +488,17 @@ __device__ __forceinline__ void prefill(
             }
         }
         __syncthreads();
+        bool big = false;  // bf16 tile beyond f16's range: re-staged raw, exact bf16 path
+        if constexpr (B2H) {
+            big = hdr->tile_big[buf] == j;  // uniform: read after the barrier
+            if (big) {
+                if (loader) {
+                    issue(j, true);
+                    commit(j, buf, true);
+                }
+                __syncthreads();
+            }
+        }
         if (loader && j + 1 < n_tiles) issue(j + 1);
 
         const uint8_t* ks = stage + buf * Gm::STAGE;
@@ -445,11 +512,29 @@ __device__ __forceinline__ void prefill(
             f32x16 s = f32x16{};
             const uint8_t* krow = ks + (sb * 32 + l32) * Gm::KPITCH;
             if constexpr (Gm::ELT == 2) {
+                if (B2H && big) {  // uniform: raw bf16 keys, q's f16 value split hi + lo bf16 (exact)
 #pragma unroll
-                for (int t = 0; t < QSTEPS; ++t) {
-                    const opv a = *reinterpret_cast<const opv*>(krow + (16 * t + 8 * h) * 2);
-                    s = O::mma(a, qa[t], s);
-                    if constexpr (O::SPLIT) s = O::mma(a, qb[t], s);
+                    for (int t = 0; t < QSTEPS; ++t) {
+                        const typename OB::v a = *reinterpret_cast<const typename OB::v*>(krow + (16 * t + 8 * h) * 2);
+                        // recomputed per use (kept out of the loop-invariant set:
+                        // hoisted for every step it would hold 64 more registers)
+                        opv qt = qa[t];
+                        asm volatile("" : "+v"(qt));
+                        float x[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) x[e] = (float)qt[e];
+                        typename OB::v qh, ql;
+                        pack8<DT_BF16>(x, qh, ql);
+                        s = OB::mma(a, qh, s);
+                        s = OB::mma(a, ql, s);
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < QSTEPS; ++t) {
+                        const opv a = *reinterpret_cast<const opv*>(krow + (16 * t + 8 * h) * 2);
+                        s = O::mma(a, qa[t], s);
+                        if constexpr (O::SPLIT) s = O::mma(a, qb[t], s);
+                    }
                 }
             } else {
 #pragma unroll
@@ -500,6 +585,7 @@ __device__ __forceinline__ void prefill(
                 opv pa[2], pb[2];
                 pack8<CT>(p, pa[0], pb[0]);
                 pack8<CT>(p + 8, pa[1], pb[1]);
+
                 const uint8_t* vtr = vs + vtr_off;
                 // A = V^T[dims db*32 + l32][keys]: lane (l32, h) takes keys
                 // 16st + 4h + 0..3 and 16st + 8 + 4h + 0..3 (the order P^T holds
@@ -515,9 +601,17 @@ __device__ __forceinline__ void prefill(
                         const uint64_t r1 = lds_read_tr(vp + 8 * Gm::VRPITCH);
                         const uint4 w = make_uint4((uint32_t)r0, (uint32_t)(r0 >> 32), (uint32_t)r1,
                                                    (uint32_t)(r1 >> 32));
-                        const opv a = __builtin_bit_cast(opv, w);
-                        acc[db] = O::mma(a, pa[st], acc[db]);
-                        if constexpr (O::SPLIT && !F8) acc[db] = O::mma(a, pb[st], acc[db]);
+                        if (B2H && big) {  // uniform; P as hi + lo bf16, packed per step (rare path)
+                            typename OB::v pbh, pbl;
+                            pack8<DT_BF16>(p + 8 * st, pbh, pbl);
+                            const typename OB::v ab = __builtin_bit_cast(typename OB::v, w);
+                            acc[db] = OB::mma(ab, pbh, acc[db]);
+                            acc[db] = OB::mma(ab, pbl, acc[db]);
+                        } else {
+                            const opv a = __builtin_bit_cast(opv, w);
+                            acc[db] = O::mma(a, pa[st], acc[db]);
+                            if constexpr (O::SPLIT && !F8) acc[db] = O::mma(a, pb[st], acc[db]);
+                        }
                     }
                 }
             } else {
