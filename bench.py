@@ -54,6 +54,8 @@ def parse():
                         "(1, 3, 4, 5) and append/gather, one JSON line each")
     p.add_argument("--c5-pool-frac", type=float, default=0.9,
                    help="config 5 pool size as a fraction of free HBM")
+    p.add_argument("--parts", default="c1,append,e4m3,c3,c4,c5",
+                   help="suite parts to run (comma list of c1, append, e4m3, c3, c4, c5)")
     return p.parse_args()
 
 
@@ -351,7 +353,10 @@ def emit(d):
 def suite(args, dev):
     """The benchmark configurations other than the headline (config 2), each
     on synthetic seeded inputs resident in HBM; timings are HIP events around
-    graph replays (launch cost inside the graph, host enqueue outside)."""
+    graph replays (launch cost inside the graph, host enqueue outside).
+    --parts selects: c1 (config 1), append (config 2 append / gather), e4m3
+    (config 2 decode over E4M3 pages), c3 (config 3 prefill), c4 (config 4
+    compaction), c5 (config 5 long-context decode on a ~90 % HBM pool)."""
     import numpy as np
     import torch
 
@@ -361,200 +366,239 @@ def suite(args, dev):
     kv, pa, fa = PagedKvGpu(0), PagedAttention(0), FlashAttention2(0)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
+    parts = set(args.parts.split(","))
 
-    # ---- config 1: f32, B=1, 14/2 heads, hd 64, page 16, 511 cached + 1 appended
-    s1 = synth.config1(0)
-    rl = s1.row_len
-    lay1 = PagedKvLayout(64, 16, rl, KvDataType.F32)
-    pool1 = torch.randn(lay1.floats_total(), generator=gen, device=dev)
-    tab1 = torch.from_numpy(s1.free_order[:32].astype(np.uint32).view(np.int32)).to(dev)
-    k1 = torch.randn(rl, generator=gen, device=dev)
-    v1 = torch.randn(rl, generator=gen, device=dev)
-    q1 = torch.randn(s1.n_head * s1.head_dim, generator=gen, device=dev)
-    o1 = torch.empty_like(q1)
+    if "c1" in parts:  # f32, B=1, 14/2 heads, hd 64, page 16, 511 cached + 1 appended
+        s1 = synth.config1(0)
+        rl = s1.row_len
+        lay1 = PagedKvLayout(64, 16, rl, KvDataType.F32)
+        pool1 = torch.randn(lay1.floats_total(), generator=gen, device=dev)
+        tab1 = torch.from_numpy(s1.free_order[:32].astype(np.uint32).view(np.int32)).to(dev)
+        k1 = torch.randn(rl, generator=gen, device=dev)
+        v1 = torch.randn(rl, generator=gen, device=dev)
+        q1 = torch.randn(s1.n_head * s1.head_dim, generator=gen, device=dev)
+        o1 = torch.empty_like(q1)
 
-    def step1(st):
-        kv.append_kv(st, lay1, pool1, k1, v1, tab1, 511, 1)
-        pa.launch_flash_decoding(st, q1, pool1, tab1, o1, s1.n_head, s1.n_head_kv, s1.head_dim,
-                                 16, 512, 511, True)
-    us1 = graph_time_us(step1, 20)
-    emit({"config": 1, "what": "append 1 token + flash-decoding attention, f32, B=1, 14/2 heads, "
-          "hd 64, ctx 512", "latency_us": round(us1, 2),
-          "kv_bytes": 512 * rl * 2 * 4, "GB/s": round(512 * rl * 2 * 4 / us1 / 1e3, 1)})
+        def step1(st):
+            kv.append_kv(st, lay1, pool1, k1, v1, tab1, 511, 1)
+            pa.launch_flash_decoding(st, q1, pool1, tab1, o1, s1.n_head, s1.n_head_kv,
+                                     s1.head_dim, 16, 512, 511, True)
+        us1 = graph_time_us(step1, 20)
+        emit({"config": 1, "what": "append 1 token + flash-decoding attention, f32, B=1, 14/2 "
+              "heads, hd 64, ctx 512", "latency_us": round(us1, 2),
+              "kv_bytes": 512 * rl * 2 * 4, "GB/s": round(512 * rl * 2 * 4 / us1 / 1e3, 1)})
 
-    def step1f(st):
-        pa.append_flash_decoding(st, k1, v1, q1, pool1, tab1, o1, s1.n_head, s1.n_head_kv,
-                                 s1.head_dim, 16, 511)
-    us1f = graph_time_us(step1f, 20)
-    emit({"config": 1, "what": "the same step in one launch (eh_append_flash_decoding)",
-          "latency_us": round(us1f, 2), "kv_bytes": 512 * rl * 2 * 4,
-          "GB/s": round(512 * rl * 2 * 4 / us1f / 1e3, 1)})
+        def step1f(st):
+            pa.append_flash_decoding(st, k1, v1, q1, pool1, tab1, o1, s1.n_head, s1.n_head_kv,
+                                     s1.head_dim, 16, 511)
+        us1f = graph_time_us(step1f, 20)
+        emit({"config": 1, "what": "the same step in one launch (eh_append_flash_decoding)",
+              "latency_us": round(us1f, 2), "kv_bytes": 512 * rl * 2 * 4,
+              "GB/s": round(512 * rl * 2 * 4 / us1f / 1e3, 1)})
 
-    # ---- append / gather at config 2's shape (one layer)
     s2 = synth.config2(0, extra_tokens=1)
     tab2 = synth.block_tables(s2, extra_tokens=1)
-    lay2 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.F16)
-    pool2 = torch.randn(lay2.floats_total(), generator=gen, device=dev, dtype=torch.float16)
     dtab2 = torch.from_numpy(tab2.view(np.int32)).to(dev)
-    nk2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
-    nv2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
-    cu2 = torch.arange(33, dtype=torch.int32, device=dev)
-    st2 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
-    us_app = graph_time_us(lambda st: kv.append_kv_batched(st, lay2, pool2, nk2, nv2, dtab2, cu2,
-                                                           st2, 32), 20)
-    app_bytes = 32 * 2 * s2.row_len * 2 * 2
-    emit({"config": 2, "what": "batched append of one token per sequence (32 x 1 KiB rows), f16",
-          "latency_us": round(us_app, 2), "GB/s": round(app_bytes / us_app / 1e3, 2)})
-    L0 = int(s2.ctx_lens[0])
-    gout = torch.empty((L0, s2.row_len), dtype=torch.float16, device=dev)
-    tab_row = dtab2[0].contiguous()
-    us_g = graph_time_us(lambda st: kv.read_keys(st, lay2, pool2, tab_row, gout, 0, L0), 20)
-    g_bytes = L0 * s2.row_len * 2 * 2
-    emit({"config": 2, "what": f"gather of one sequence's K rows ({L0} tokens x 512 B), f16",
-          "latency_us": round(us_g, 2), "GB/s": round(g_bytes / us_g / 1e3, 1)})
-    del pool2
+    if "append" in parts:  # append / gather at config 2's shape (one layer)
+        lay2 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.F16)
+        pool2 = torch.randn(lay2.floats_total(), generator=gen, device=dev, dtype=torch.float16)
+        nk2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
+        nv2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
+        cu2 = torch.arange(33, dtype=torch.int32, device=dev)
+        st2 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
+        us_app = graph_time_us(lambda st: kv.append_kv_batched(st, lay2, pool2, nk2, nv2, dtab2,
+                                                               cu2, st2, 32), 20)
+        app_bytes = 32 * 2 * s2.row_len * 2 * 2
+        emit({"config": 2, "what": "batched append of one token per sequence (32 x 1 KiB rows), "
+              "f16", "latency_us": round(us_app, 2), "GB/s": round(app_bytes / us_app / 1e3, 2)})
+        L0 = int(s2.ctx_lens[0])
+        gout = torch.empty((L0, s2.row_len), dtype=torch.float16, device=dev)
+        tab_row = dtab2[0].contiguous()
+        us_g = graph_time_us(lambda st: kv.read_keys(st, lay2, pool2, tab_row, gout, 0, L0), 20)
+        g_bytes = L0 * s2.row_len * 2 * 2
+        emit({"config": 2, "what": f"gather of one sequence's K rows ({L0} tokens x 512 B), f16",
+              "latency_us": round(us_g, 2), "GB/s": round(g_bytes / us_g / 1e3, 1)})
+        del pool2
 
-    # ---- config 2's decode over E4M3 pages (per-kv-head scales): 16 distinct
-    # pools rotated through the captured calls, so the 256 MB MALL cannot hold them
-    lay8 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.FP8)
-    pools8 = [torch.randint(0, 0x7E, (lay8.floats_total(),), generator=gen, device=dev,
-                            dtype=torch.uint8) for _ in range(16)]
-    q8 = torch.randn((32, 12, 128), generator=gen, device=dev)
-    o8 = torch.empty_like(q8)
-    ks8 = torch.full((2,), 0.01, device=dev)
-    vs8 = torch.full((2,), 0.02, device=dev)
-    lens8 = torch.from_numpy((s2.ctx_lens + 1).astype(np.int32)).to(dev)
-    plan8 = PagedAttention.plan(32, 12, 2, 128, 16, int(s2.ctx_lens.max()) + 1, 0, KvDataType.FP8)
-    ws8 = PagedAttention.workspace(plan8)
-    turn = [0]
+    if "e4m3" in parts:  # config 2's decode over E4M3 pages, 16 rotated pools (> the 256 MB MALL)
+        lay8 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.FP8)
+        pools8 = [torch.randint(0, 0x7E, (lay8.floats_total(),), generator=gen, device=dev,
+                                dtype=torch.uint8) for _ in range(16)]
+        q8 = torch.randn((32, 12, 128), generator=gen, device=dev)
+        o8 = torch.empty_like(q8)
+        ks8 = torch.full((2,), 0.01, device=dev)
+        vs8 = torch.full((2,), 0.02, device=dev)
+        lens8 = torch.from_numpy((s2.ctx_lens + 1).astype(np.int32)).to(dev)
+        plan8 = PagedAttention.plan(32, 12, 2, 128, 16, int(s2.ctx_lens.max()) + 1, 0,
+                                    KvDataType.FP8)
+        ws8 = PagedAttention.workspace(plan8)
+        stride2 = int(tab2.shape[1])
+        sched8 = PagedAttention.schedule_buffer(32, stride2, 16, plan8)
+        pa.build_schedule(None, lay8, dtab2, lens8, 0, plan8, sched8)
+        turn = [0]
+        b8 = int((s2.ctx_lens + 1).sum()) * 2 * 128 * 2 * 1
 
-    def dec8(st):
-        p = pools8[turn[0] % len(pools8)]
-        turn[0] += 1
-        pa.decode_batched_e4m3(st, q8, p, dtab2, lens8, o8, 12, 2, 128, 16, ks8, vs8, plan8, ws8)
-    us8 = graph_time_us(dec8, 20, 32)
-    b8 = int((s2.ctx_lens + 1).sum()) * 2 * 128 * 2 * 1
-    emit({"config": 2, "what": "decode over E4M3 pages (fp8 KV, per-kv-head scales), B=32, 12/2 "
-          "heads, hd 128, one layer", "latency_us": round(us8, 2), "kv_bytes": b8,
-          "GB/s": round(b8 / us8 / 1e3, 1), "hbm_frac_of_8TB/s": round(b8 / us8 / 1e3 / 8000.0, 4),
-          "kernel": PagedAttention.kernel_name(12, 2, 128, 16, KvDataType.FP8) +
-          " + eh_decode_tiles_merge"})
+        def dec8(st):
+            p = pools8[turn[0] % len(pools8)]
+            turn[0] += 1
+            pa.decode_batched_e4m3(st, q8, p, dtab2, lens8, o8, 12, 2, 128, 16, ks8, vs8, plan8,
+                                   ws8)
+        us8 = graph_time_us(dec8, 20, 32)
+        emit({"config": 2, "what": "decode over E4M3 pages (fp8 KV, per-kv-head scales), B=32, "
+              "12/2 heads, hd 128, one layer (self-scheduled)", "latency_us": round(us8, 2),
+              "kv_bytes": b8, "GB/s": round(b8 / us8 / 1e3, 1),
+              "hbm_frac_of_8TB/s": round(b8 / us8 / 1e3 / 8000.0, 4)})
 
-    # the same step with the appended f32 rows quantised inside the decode launch
-    pos8 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
-    nk8 = torch.randn((32, s2.row_len), generator=gen, device=dev)
-    nv8 = torch.randn((32, s2.row_len), generator=gen, device=dev)
+        def dec8s(st):
+            p = pools8[turn[0] % len(pools8)]
+            turn[0] += 1
+            pa.append_decode_scheduled(st, lay8, p, None, None, sched8, stride2, q8, o8, 12, 128,
+                                       plan8, ws8, ks8, vs8)
+        us8s = graph_time_us(dec8s, 20, 32)
+        emit({"config": 2, "what": "the same E4M3 decode from a step schedule (built once)",
+              "latency_us": round(us8s, 2), "kv_bytes": b8, "GB/s": round(b8 / us8s / 1e3, 1),
+              "hbm_frac_of_8TB/s": round(b8 / us8s / 1e3 / 8000.0, 4),
+              "kernel": PagedAttention.kernel_name(12, 2, 128, 16, KvDataType.FP8) +
+              "_sched + eh_decode_tiles_merge_sched"})
+        # the fused step: the appended f32 rows quantised inside the decode launch
+        pos8 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
+        nk8 = torch.randn((32, s2.row_len), generator=gen, device=dev)
+        nv8 = torch.randn((32, s2.row_len), generator=gen, device=dev)
+        sched8f = PagedAttention.schedule_buffer(32, stride2, 16, plan8)
+        pa.build_schedule(None, lay8, dtab2, pos8, 1, plan8, sched8f)
 
-    def step8(st):
-        p = pools8[turn[0] % len(pools8)]
-        turn[0] += 1
-        pa.append_decode_batched_e4m3(st, lay8, p, nk8, nv8, dtab2, pos8, q8, o8, 12, 128, plan8,
-                                      ws8, ks8, vs8)
-    us8f = graph_time_us(step8, 20, 32)
-    emit({"config": 2, "what": "fused E4M3 decode step (quantising append of the 32 new f32 rows "
-          "+ decode in one launch), B=32, 12/2 heads, hd 128, one layer",
-          "latency_us": round(us8f, 2), "kv_bytes": b8, "GB/s": round(b8 / us8f / 1e3, 1),
-          "kernel": PagedAttention.kernel_name(12, 2, 128, 16, KvDataType.FP8) +
-          " + eh_decode_tiles_merge"})
-    del pools8
+        def step8(st):
+            p = pools8[turn[0] % len(pools8)]
+            turn[0] += 1
+            pa.append_decode_scheduled(st, lay8, p, nk8, nv8, sched8f, stride2, q8, o8, 12, 128,
+                                       plan8, ws8, ks8, vs8)
+        us8f = graph_time_us(step8, 20, 32)
+        emit({"config": 2, "what": "fused E4M3 decode step from a step schedule (quantising "
+              "append of the 32 new f32 rows + decode in one launch), B=32, 12/2 heads, hd 128, "
+              "one layer", "latency_us": round(us8f, 2), "kv_bytes": b8,
+              "GB/s": round(b8 / us8f / 1e3, 1)})
+        del pools8
 
-    # ---- config 3: bf16 chunked prefill, B=8, 512 new tokens on 2048 cached, 32/8 heads
-    s3 = synth.config3(0)
-    tab3 = synth.block_tables(s3, extra_tokens=512)
-    lay3 = PagedKvLayout(s3.n_blocks, 16, s3.row_len, KvDataType.BF16)
-    pool3 = torch.randn(lay3.floats_total(), generator=gen, device=dev, dtype=torch.bfloat16)
-    dtab3 = torch.from_numpy(tab3.view(np.int32)).to(dev)
-    T3 = 8 * 512
-    k3 = torch.randn((T3, s3.row_len), generator=gen, device=dev, dtype=torch.bfloat16)
-    v3 = torch.randn((T3, s3.row_len), generator=gen, device=dev, dtype=torch.bfloat16)
-    q3 = torch.randn((T3, 32, 128), generator=gen, device=dev)
-    o3 = torch.empty_like(q3)
-    cu3 = torch.arange(0, T3 + 1, 512, dtype=torch.int32, device=dev)
-    sp3 = torch.full((8,), 2048, dtype=torch.int32, device=dev)
-    us_a3 = graph_time_us(lambda st: kv.append_kv_batched(st, lay3, pool3, k3, v3, dtab3, cu3, sp3,
-                                                          T3), 10)
-    us_p3 = graph_time_us(lambda st: fa.launch_batched(st, q3, pool3, dtab3, cu3, sp3, o3, 32, 8,
-                                                       128, 16, 512, kv_dtype=KvDataType.BF16), 5, 4)
-    flops = 8 * 32 * 4 * 128 * sum(2048 + i + 1 for i in range(512))
-    emit({"config": 3, "what": "chunked prefill (causal, MFMA), bf16 KV, B=8, 512 on 2048, 32/8 "
-          "heads, hd 128", "prefill_us": round(us_p3, 2), "flop": flops,
-          "TFLOP/s": round(flops / us_p3 / 1e6, 1),
-          "mfma_frac_of_2.5PF": round(flops / us_p3 / 1e6 / 2500.0, 4),
-          "append_us": round(us_a3, 2),
-          "append_GB/s": round(T3 * 2 * s3.row_len * 2 * 2 / us_a3 / 1e3, 1)})
-    # config 3's prefill over E4M3 pages (per-kv-head scales)
-    lay3e = PagedKvLayout(s3.n_blocks, 16, s3.row_len, KvDataType.FP8)
-    pool3e = torch.randint(0, 0x7E, (lay3e.floats_total(),), generator=gen, device=dev,
-                           dtype=torch.uint8)
-    sc3 = torch.full((8,), 0.01, device=dev)
-    us_p3e = graph_time_us(lambda st: fa.launch_batched_e4m3(st, q3, pool3e, dtab3, cu3, sp3, o3,
-                                                             32, 8, 128, 16, 512, sc3, sc3), 5, 4)
-    emit({"config": 3, "what": "chunked prefill (causal, MFMA) over E4M3 pages (fp8 KV, per-kv-head "
-          "scales), B=8, 512 on 2048, 32/8 heads, hd 128", "prefill_us": round(us_p3e, 2),
-          "flop": flops, "TFLOP/s": round(flops / us_p3e / 1e6, 1),
-          "mfma_frac_of_2.5PF": round(flops / us_p3e / 1e6 / 2500.0, 4)})
-    del pool3, pool3e, k3, v3, q3, o3
+    if "c3" in parts:  # bf16 chunked prefill, B=8, 512 new tokens on 2048 cached, 32/8 heads
+        s3 = synth.config3(0)
+        tab3 = synth.block_tables(s3, extra_tokens=512)
+        lay3 = PagedKvLayout(s3.n_blocks, 16, s3.row_len, KvDataType.BF16)
+        pool3 = torch.randn(lay3.floats_total(), generator=gen, device=dev, dtype=torch.bfloat16)
+        dtab3 = torch.from_numpy(tab3.view(np.int32)).to(dev)
+        T3 = 8 * 512
+        k3 = torch.randn((T3, s3.row_len), generator=gen, device=dev, dtype=torch.bfloat16)
+        v3 = torch.randn((T3, s3.row_len), generator=gen, device=dev, dtype=torch.bfloat16)
+        q3 = torch.randn((T3, 32, 128), generator=gen, device=dev)
+        o3 = torch.empty_like(q3)
+        cu3 = torch.arange(0, T3 + 1, 512, dtype=torch.int32, device=dev)
+        sp3 = torch.full((8,), 2048, dtype=torch.int32, device=dev)
+        us_a3 = graph_time_us(lambda st: kv.append_kv_batched(st, lay3, pool3, k3, v3, dtab3, cu3,
+                                                              sp3, T3), 10)
+        us_p3 = graph_time_us(lambda st: fa.launch_batched(st, q3, pool3, dtab3, cu3, sp3, o3, 32,
+                                                           8, 128, 16, 512,
+                                                           kv_dtype=KvDataType.BF16), 5, 4)
+        flops = 8 * 32 * 4 * 128 * sum(2048 + i + 1 for i in range(512))
+        emit({"config": 3, "what": "chunked prefill (causal, MFMA), bf16 KV staged as f16, B=8, "
+              "512 on 2048, 32/8 heads, hd 128", "prefill_us": round(us_p3, 2), "flop": flops,
+              "TFLOP/s": round(flops / us_p3 / 1e6, 1),
+              "mfma_frac_of_2.5PF": round(flops / us_p3 / 1e6 / 2500.0, 4),
+              "append_us": round(us_a3, 2),
+              "append_GB/s": round(T3 * 2 * s3.row_len * 2 * 2 / us_a3 / 1e3, 1)})
+        pool3h = pool3.to(torch.float16)
+        us_p3h = graph_time_us(lambda st: fa.launch_batched(st, q3, pool3h, dtab3, cu3, sp3, o3,
+                                                            32, 8, 128, 16, 512,
+                                                            kv_dtype=KvDataType.F16), 5, 4)
+        emit({"config": 3, "what": "the same prefill over f16 pages", "prefill_us": round(us_p3h, 2),
+              "TFLOP/s": round(flops / us_p3h / 1e6, 1),
+              "mfma_frac_of_2.5PF": round(flops / us_p3h / 1e6 / 2500.0, 4)})
+        del pool3h
+        lay3e = PagedKvLayout(s3.n_blocks, 16, s3.row_len, KvDataType.FP8)
+        pool3e = torch.randint(0, 0x7E, (lay3e.floats_total(),), generator=gen, device=dev,
+                               dtype=torch.uint8)
+        sc3 = torch.full((8,), 0.01, device=dev)
+        us_p3e = graph_time_us(lambda st: fa.launch_batched_e4m3(st, q3, pool3e, dtab3, cu3, sp3,
+                                                                 o3, 32, 8, 128, 16, 512, sc3,
+                                                                 sc3), 5, 4)
+        emit({"config": 3, "what": "chunked prefill (causal, MFMA) over E4M3 pages (fp8 KV, "
+              "per-kv-head scales), B=8, 512 on 2048, 32/8 heads, hd 128",
+              "prefill_us": round(us_p3e, 2), "flop": flops,
+              "TFLOP/s": round(flops / us_p3e / 1e6, 1),
+              "mfma_frac_of_2.5PF": round(flops / us_p3e / 1e6 / 2500.0, 4)})
+        del pool3, pool3e, k3, v3, q3, o3
 
-    # ---- config 4: prefix-shared CoW + eviction + compaction (page moves on the GPU)
-    from titan_amd.prefix_share import PrefixShareScenario, run_on_gpu
-    scn = PrefixShareScenario(seed=0)
-    plan4 = scn.plan()
-    pool4, _, _, lay4 = run_on_gpu(scn, plan4)
-    src = torch.from_numpy(np.asarray(plan4.compaction.src, np.uint32).view(np.int32)).to(dev)
-    dst = torch.from_numpy(np.asarray(plan4.compaction.dst, np.uint32).view(np.int32)).to(dev)
-    npairs = int(src.numel())
-    # compaction moves each survivor once; replays re-copy the same bytes
-    us4 = graph_time_us(lambda st: kv.copy_pages(st, lay4, pool4, src, dst), 10) if npairs else 0.0
-    page = lay4.page_bytes()
-    emit({"config": 4, "what": "gather-compaction of surviving pages after prefix-shared "
-          "CoW + 25% LRU eviction (64 seqs, 8 kv heads, hd 128, f16)",
-          "pages_moved": npairs, "cow_copies": plan4.cow_pairs, "compaction_us": round(us4, 2),
-          "GB/s": round(2 * npairs * page / us4 / 1e3, 1) if us4 else None})
-    del pool4
+    if "c4" in parts:  # prefix-shared CoW + eviction + compaction (page moves on the GPU)
+        from titan_amd.prefix_share import PrefixShareScenario, run_on_gpu
+        scn = PrefixShareScenario(seed=0)
+        plan4 = scn.plan()
+        pool4, _, _, lay4 = run_on_gpu(scn, plan4)
+        src = torch.from_numpy(np.asarray(plan4.compaction.src, np.uint32).view(np.int32)).to(dev)
+        dst = torch.from_numpy(np.asarray(plan4.compaction.dst, np.uint32).view(np.int32)).to(dev)
+        npairs = int(src.numel())
+        # compaction moves each survivor once; replays re-copy the same bytes
+        us4 = graph_time_us(lambda st: kv.copy_pages(st, lay4, pool4, src, dst), 10) if npairs \
+            else 0.0
+        page = lay4.page_bytes()
+        emit({"config": 4, "what": "gather-compaction of surviving pages after prefix-shared "
+              "CoW + 25% LRU eviction (64 seqs, 8 kv heads, hd 128, f16)",
+              "pages_moved": npairs, "cow_copies": plan4.cow_pairs, "compaction_us": round(us4, 2),
+              "GB/s": round(2 * npairs * page / us4 / 1e3, 1) if us4 else None})
+        del pool4
 
-    # ---- config 5: B=4 at 32768 tokens, 32/8 heads, f16, pool ~90% of free HBM
-    torch.cuda.empty_cache()
-    free, _ = torch.cuda.mem_get_info()
-    s5 = synth.config5(0, n_blocks=int(args.c5_pool_frac * free) // (16 * 2 * 1024 * 2))
-    tab5 = synth.block_tables(s5, extra_tokens=1)
-    lay5 = PagedKvLayout(s5.n_blocks, 16, s5.row_len, KvDataType.F16)
-    pool5 = torch.empty(lay5.floats_total(), device=dev, dtype=torch.float16)
-    # fill only the pages the tables use (values do not change the timing)
-    used = torch.from_numpy(tab5[tab5 != 0xFFFFFFFF].astype(np.int64)).to(dev)
-    pg = pool5.view(s5.n_blocks, -1)
-    pg[used] = torch.randn((used.numel(), pg.shape[1]), generator=gen, device=dev,
-                           dtype=torch.float16)
-    dtab5 = torch.from_numpy(tab5.view(np.int32)).to(dev)
-    q5 = torch.randn((4, 32, 128), generator=gen, device=dev)
-    o5 = torch.empty_like(q5)
-    nk5 = torch.randn((4, s5.row_len), generator=gen, device=dev, dtype=torch.float16)
-    nv5 = torch.randn((4, s5.row_len), generator=gen, device=dev, dtype=torch.float16)
-    st5 = torch.from_numpy(s5.ctx_lens.astype(np.int32)).to(dev)
-    plan5 = PagedAttention.plan(4, 32, 8, 128, 16, 32769)
-    ws5 = PagedAttention.workspace(plan5)
-    # evicts the 256 MB MALL by reading 1 GiB of other data: a write-based flush (memset)
-    # would leave dirty lines whose write-back competes with the timed reads
-    flush = torch.ones(1024 * 1024 * 1024 // 4, device=dev)
-    stream = torch.cuda.Stream()
-    times = []
-    with torch.cuda.stream(stream):
-        for it in range(12):
-            flush.sum()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            pa.append_decode_batched(stream, lay5, pool5, nk5, nv5, dtab5, st5, q5, o5, 32, 128,
-                                     plan5, ws5)
-            b.record(stream)
-            torch.cuda.synchronize()
-            if it >= 2:
-                times.append(a.elapsed_time(b) * 1e3)
-    us5 = float(np.median(times))
-    b5 = 4 * 32769 * 8 * 128 * 2 * 2
-    emit({"config": 5, "what": "fused append + decode, B=4 x 32768 ctx, 32/8 heads, hd 128, f16, "
-          f"pool {lay5.bytes_total() / 1e9:.0f} GB ({s5.n_blocks} pages, scattered), MALL "
-          "evicted (1 GiB read) before each timed call", "latency_us": round(us5, 2), "kv_bytes": b5,
-          "GB/s": round(b5 / us5 / 1e3, 1), "frac_of_8TB/s": round(b5 / us5 / 1e3 / 8000.0, 4),
-          "kernel": PagedAttention.kernel_name(32, 8, 128, 16, KvDataType.F16)})
+    if "c5" in parts:  # B=4 at 32768 tokens, 32/8 heads, f16, pool ~90% of free HBM
+        torch.cuda.empty_cache()
+        free, _ = torch.cuda.mem_get_info()
+        s5 = synth.config5(0, n_blocks=int(args.c5_pool_frac * free) // (16 * 2 * 1024 * 2))
+        tab5 = synth.block_tables(s5, extra_tokens=1)
+        lay5 = PagedKvLayout(s5.n_blocks, 16, s5.row_len, KvDataType.F16)
+        pool5 = torch.empty(lay5.floats_total(), device=dev, dtype=torch.float16)
+        # fill only the pages the tables use (values do not change the timing)
+        used = torch.from_numpy(tab5[tab5 != 0xFFFFFFFF].astype(np.int64)).to(dev)
+        pg = pool5.view(s5.n_blocks, -1)
+        pg[used] = torch.randn((used.numel(), pg.shape[1]), generator=gen, device=dev,
+                               dtype=torch.float16)
+        dtab5 = torch.from_numpy(tab5.view(np.int32)).to(dev)
+        q5 = torch.randn((4, 32, 128), generator=gen, device=dev)
+        o5 = torch.empty_like(q5)
+        nk5 = torch.randn((4, s5.row_len), generator=gen, device=dev, dtype=torch.float16)
+        nv5 = torch.randn((4, s5.row_len), generator=gen, device=dev, dtype=torch.float16)
+        st5 = torch.from_numpy(s5.ctx_lens.astype(np.int32)).to(dev)
+        plan5 = PagedAttention.plan(4, 32, 8, 128, 16, 32769)
+        ws5 = PagedAttention.workspace(plan5)
+        stride5 = int(tab5.shape[1])
+        sched5 = PagedAttention.schedule_buffer(4, stride5, 16, plan5)
+        pa.build_schedule(None, lay5, dtab5, st5, 1, plan5, sched5)
+        # evicts the 256 MB MALL by reading 1 GiB of other data: a write-based flush
+        # (memset) would leave dirty lines whose write-back competes with the timed reads
+        flush = torch.ones(1024 * 1024 * 1024 // 4, device=dev)
+        stream = torch.cuda.Stream()
+        b5 = 4 * 32769 * 8 * 128 * 2 * 2
+        for label, call in (
+                ("fused append + decode (self-scheduled)",
+                 lambda: pa.append_decode_batched(stream, lay5, pool5, nk5, nv5, dtab5, st5, q5,
+                                                  o5, 32, 128, plan5, ws5)),
+                ("fused append + decode from a step schedule",
+                 lambda: pa.append_decode_scheduled(stream, lay5, pool5, nk5, nv5, sched5,
+                                                    stride5, q5, o5, 32, 128, plan5, ws5))):
+            times = []
+            with torch.cuda.stream(stream):
+                for it in range(12):
+                    flush.sum()
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    call()
+                    b.record(stream)
+                    torch.cuda.synchronize()
+                    if it >= 2:
+                        times.append(a.elapsed_time(b) * 1e3)
+            us5 = float(np.median(times))
+            emit({"config": 5, "what": f"{label}, B=4 x 32768 ctx, 32/8 heads, hd 128, f16, pool "
+                  f"{lay5.bytes_total() / 1e9:.0f} GB ({s5.n_blocks} pages, scattered), MALL "
+                  "evicted (1 GiB read) before each timed call", "latency_us": round(us5, 2),
+                  "kv_bytes": b5, "GB/s": round(b5 / us5 / 1e3, 1),
+                  "frac_of_8TB/s": round(b5 / us5 / 1e3 / 8000.0, 4),
+                  "kernel": PagedAttention.kernel_name(32, 8, 128, 16, KvDataType.F16)})
+        del pool5, flush
+
 
 def cpu_child(args):
     """The CPU baseline itself (runs in the pinned child, never touches a GPU):
