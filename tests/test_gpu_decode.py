@@ -469,6 +469,42 @@ def test_fused_step_errors(dev):
     assert torch.all(torch.isfinite(out))
 
 
+@pytest.mark.parametrize("case", ["none_entry", "past_pool", "past_table"])
+def test_fused_step_masked_page_device_position(dev, case):
+    """eh_append_flash_decoding with a device position whose page is masked
+    (table entry 0xFFFFFFFF, a page id past the pool, or a position past the
+    table): EH_OK, the pool is unchanged, and q attends the tokens 0..pos that
+    sit on valid pages."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl = n_kv * hd
+    rng = np.random.default_rng(41)
+    nb = 6
+    table = rng.permutation(nb)[:4].astype(np.uint32)
+    pos = {"none_entry": 40, "past_pool": 20, "past_table": 64}[case]
+    if case == "none_entry":
+        table[2] = 0xFFFFFFFF
+    elif case == "past_pool":
+        table[1] = nb + 3
+    base = rng.standard_normal(nb * bt * 2 * rl).astype(np.float32)
+    pool = torch.from_numpy(base).half().to(dev)
+    pool_f32 = torch.from_numpy(base).half().float().numpy()
+    before = pool.clone()
+    k = torch.from_numpy(rng.standard_normal(rl).astype(np.float32)).half().to(dev)
+    v = torch.from_numpy(rng.standard_normal(rl).astype(np.float32)).half().to(dev)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    out = torch.full((n_head * hd,), float("nan"), device=dev)
+    PagedAttention(0).append_flash_decoding(None, k, v, torch.from_numpy(q).to(dev), pool,
+                                            i32(table, dev), out, n_head, n_kv, hd, bt, 0,
+                                            i32([pos], dev), KvDataType.F16)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.view(torch.int16), before.view(torch.int16)), "row written"
+    valid = [j for j in range(pos // bt + 1) if j < len(table) and table[j] < nb]
+    assert valid == list(range(len(valid))), "masked pages are the trailing ones"
+    n = min(pos + 1, bt * len(valid))
+    ref = orc.sdpa_decode(pool_f32, table[:len(valid)], bt, n, q, n_head, n_kv, hd, True, n - 1)
+    check_close(out.cpu().numpy(), ref, KvDataType.F16)
+
+
 def test_graph_replay_split_count_follows_device_position(dev):
     """The reference sizes its split grid on the host from seq_tokens and
     freezes it at capture (forward_driver.rs:2230-2243), and drops tokens

@@ -200,6 +200,72 @@ def fused_case(dev, dtype, starts, shape, seed, grid=None):
     check_close(out.cpu().numpy(), ref)
 
 
+def valid_token_reference(pool_f32, tab, n_tok, q, nb, bt, n_head, n_kv, hd):
+    """Attention of q over the tokens 0..n_tok-1 of one sequence that sit on
+    valid pages (inside the table, below the pool size), the masked pages
+    being the trailing ones: the valid pages as a contiguous sequence."""
+    pages = pool_f32.reshape(nb, bt * 2 * n_kv * hd)
+    keep, n = [], 0
+    for j in range((n_tok + bt - 1) // bt):
+        p = int(tab[j]) if j < len(tab) else NONE
+        if p < nb:
+            keep.append(p)
+            n += min(bt, n_tok - bt * j)
+    sub = np.concatenate([pages[p] for p in keep])
+    ident = np.arange(len(keep), dtype=np.uint32)
+    return orc.sdpa_decode_batched(sub, ident[None], np.array([n], np.uint32), bt, q[None],
+                                   n_head, n_kv, hd)
+
+
+@pytest.mark.parametrize("scheduled", [False, True], ids=["self", "sched"])
+def test_fused_append_on_masked_page(dev, scheduled):
+    """The fused step when the appended token's page is masked: the table
+    entry is 0xFFFFFFFF (sequence 0), names a page past the pool (1), or the
+    position lies past the table (2).  The row is not written, the call
+    succeeds, and the sequence attends the tokens on its valid pages;
+    sequence 3 appends normally."""
+    n_head, n_kv, hd, bt, stride = 12, 2, 128, 16, 4
+    rl = n_kv * hd
+    rng = np.random.default_rng(31)
+    starts = np.array([40, 20, 64, 33], np.int64)
+    B = len(starts)
+    nb = B * stride + 3
+    tab = rng.permutation(nb)[:B * stride].astype(np.uint32).reshape(B, stride)
+    tab[0, 2] = NONE
+    tab[1, 1] = nb + 7
+    pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)
+    newk = torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).half()
+    newv = torch.from_numpy(rng.standard_normal((B, rl)).astype(np.float32)).half()
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    layout = PagedKvLayout(nb, bt, rl, KvDataType.F16)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(starts.max()) + 1, 0, KvDataType.F16)
+    ws = PagedAttention.workspace(plan)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    pa = PagedAttention(0)
+    dq, dtab, dpos = torch.from_numpy(q).to(dev), i32(tab, dev), i32(starts, dev)
+    if scheduled:
+        sched = PagedAttention.schedule_buffer(B, stride, bt, plan)
+        pa.build_schedule(None, layout, dtab, dpos, 1, plan, sched)
+        pa.append_decode_scheduled(None, layout, pool, newk.to(dev), newv.to(dev), sched, stride,
+                                   dq, out, n_head, hd, plan, ws)
+    else:
+        pa.append_decode_batched(None, layout, pool, newk.to(dev), newv.to(dev), dtab, dpos, dq,
+                                 out, n_head, hd, plan, ws)
+    torch.cuda.synchronize()
+    # only sequence 3's row lands in the pool
+    p = pool_f32.reshape(nb, bt, 2, rl)
+    s3 = int(starts[3])
+    p[tab[3, s3 // bt], s3 % bt, 0] = newk[3].float().numpy()
+    p[tab[3, s3 // bt], s3 % bt, 1] = newv[3].float().numpy()
+    want = torch.from_numpy(pool_f32).half()
+    assert torch.equal(pool.cpu().view(torch.int16), want.view(torch.int16)), "pool bytes"
+    got = out.cpu().numpy()
+    for b in range(B):
+        ref = valid_token_reference(pool_f32, tab[b], int(starts[b]) + 1, q[b], nb, bt, n_head,
+                                    n_kv, hd)
+        check_close(got[b:b + 1], ref, what=f"masked append page, sequence {b}")
+
+
 @pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
 @pytest.mark.parametrize("shape", [(12, 2, 128, 16), (32, 8, 128, 16), (8, 1, 128, 32)],
                          ids=lambda s: "x".join(map(str, s)))
