@@ -54,6 +54,11 @@ constexpr float RESCALE_LOG2 = 8.0f;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+// Native vectors for staged K/V words: HIP's uint4 / uint2 are structs, whose
+// copies the compiler keeps as memory (a private array it then places in
+// LDS or scratch) instead of registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <int DT> struct op_t;
 template <> struct op_t<DT_F16> {
@@ -158,12 +163,12 @@ struct geo<DT_FP8, HD> : geo<DT_F16, HD> {};
 
 // Eight E4M3 codes (two dwords, lowest byte first) as eight f16 (four dwords);
 // exact: every E4M3 value is an f16.
-__device__ __forceinline__ uint4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
-    return make_uint4(
+__device__ __forceinline__ u32x4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
+    return u32x4{
         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
-        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true)));
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
 }
 
 struct lds_hdr {
@@ -178,9 +183,9 @@ struct lds_hdr {
 // sends such a tile to the exact bf16 path).  In-range values convert
 // exactly; the rounding mode only matters below 2^-14 (f16 subnormals).
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint4 bf16x8_to_f16(uint4 w, u16x2& emax) {
+__device__ __forceinline__ u32x4 bf16x8_to_f16(u32x4 w, u16x2& emax) {
     uint32_t r[4];
-    const uint32_t in[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t in[4] = {w[0], w[1], w[2], w[3]};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float lo = __builtin_bit_cast(float, in[i] << 16);
@@ -188,7 +193,7 @@ __device__ __forceinline__ uint4 bf16x8_to_f16(uint4 w, u16x2& emax) {
         r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
         emax = __builtin_elementwise_max(emax, __builtin_bit_cast(u16x2, in[i] & 0x7F807F80u));
     }
-    return make_uint4(r[0], r[1], r[2], r[3]);
+    return u32x4{r[0], r[1], r[2], r[3]};
 }
 constexpr unsigned short BF16_F16_LIMIT = 143u << 7;  // exponent field of 2^16
 
@@ -302,7 +307,7 @@ __device__ __forceinline__ void prefill(
     constexpr int CT = (F8 || B2H) ? DT_F16 : DT;  // MFMA operand type
     constexpr uint32_t SE = F8 ? 1u : (uint32_t)Gm::ELT;  // stored element bytes
     const uint32_t head_off = hk * HD * SE + part * (16 / Gm::ELT) * SE;
-    uint4 kr[4], vr[4];
+    u32x4 kr[4], vr[4];
     uint32_t okbits = 0;  // bit j: key 4*kg+j loadable; bit 4+j: key <= kmax with a bad page
 
     const uint32_t slot_bytes = 2u * row_bytes;
@@ -336,13 +341,13 @@ __device__ __forceinline__ void prefill(
                 okbits |= (live && pv ? 1u : 0u) << j;
                 okbits |= (live && !pv ? 1u : 0u) << (4 + j);
                 if constexpr (F8) {
-                    const uint2 a = *reinterpret_cast<const uint2*>(p + j * step);
-                    const uint2 b = *reinterpret_cast<const uint2*>(p + j * step + (pv ? row_bytes : 0u));
-                    kr[j] = make_uint4(a.x, a.y, 0u, 0u);
-                    vr[j] = make_uint4(b.x, b.y, 0u, 0u);
+                    const u32x2 a = *reinterpret_cast<const u32x2*>(p + j * step);
+                    const u32x2 b = *reinterpret_cast<const u32x2*>(p + j * step + row_bytes);
+                    kr[j] = u32x4{a[0], a[1], 0u, 0u};
+                    vr[j] = u32x4{b[0], b[1], 0u, 0u};
                 } else {
-                    kr[j] = *reinterpret_cast<const uint4*>(p + j * step);
-                    vr[j] = *reinterpret_cast<const uint4*>(p + j * step + (pv ? row_bytes : 0u));
+                    kr[j] = *reinterpret_cast<const u32x4*>(p + j * step);
+                    vr[j] = *reinterpret_cast<const u32x4*>(p + j * step + row_bytes);
                 }
             }
         } else {
@@ -360,13 +365,13 @@ __device__ __forceinline__ void prefill(
                 const uint8_t* p = pool + (uint64_t)(pv ? phys[j] : 0u) * page_bytes +
                                    (uint64_t)(pv ? slot * slot_bytes + head_off : 0u);
                 if constexpr (F8) {
-                    const uint2 a = *reinterpret_cast<const uint2*>(p);
-                    const uint2 b = *reinterpret_cast<const uint2*>(p + (pv ? row_bytes : 0u));
-                    kr[j] = make_uint4(a.x, a.y, 0u, 0u);
-                    vr[j] = make_uint4(b.x, b.y, 0u, 0u);
+                    const u32x2 a = *reinterpret_cast<const u32x2*>(p);
+                    const u32x2 b = *reinterpret_cast<const u32x2*>(p + row_bytes);
+                    kr[j] = u32x4{a[0], a[1], 0u, 0u};
+                    vr[j] = u32x4{b[0], b[1], 0u, 0u};
                 } else {
-                    kr[j] = *reinterpret_cast<const uint4*>(p);
-                    vr[j] = *reinterpret_cast<const uint4*>(p + (pv ? row_bytes : 0u));
+                    kr[j] = *reinterpret_cast<const u32x4*>(p);
+                    vr[j] = *reinterpret_cast<const u32x4*>(p + row_bytes);
                 }
             }
         }
@@ -378,8 +383,8 @@ __device__ __forceinline__ void prefill(
         if constexpr (F8) {  // codes -> f16, then the f16 staging below
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                kr[j] = e4m3x8_to_f16(kr[j].x, kr[j].y);
-                vr[j] = e4m3x8_to_f16(vr[j].x, vr[j].y);
+                kr[j] = e4m3x8_to_f16(kr[j][0], kr[j][1]);
+                vr[j] = e4m3x8_to_f16(vr[j][0], vr[j][1]);
             }
         }
         if constexpr (B2H) {
@@ -397,28 +402,25 @@ __device__ __forceinline__ void prefill(
         for (int j = 0; j < 4; ++j) {
             if (okbits != 0xFu) {  // rare: keys past the window or on a bad page
                 const bool z = !((okbits >> j) & 1u);
-                vr[j].x = z ? 0u : vr[j].x;
-                vr[j].y = z ? 0u : vr[j].y;
-                vr[j].z = z ? 0u : vr[j].z;
-                vr[j].w = z ? 0u : vr[j].w;
+                vr[j] = z ? u32x4{0u, 0u, 0u, 0u} : vr[j];
             }
-            *reinterpret_cast<uint4*>(ks + (4 * kg + j) * Gm::KPITCH + part * 16) = kr[j];
+            *reinterpret_cast<u32x4*>(ks + (4 * kg + j) * Gm::KPITCH + part * 16) = kr[j];
         }
         if constexpr (Gm::VROWM) {  // V rows like K rows
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<uint4*>(vs + (4 * kg + j) * Gm::VRPITCH + part * 16) = vr[j];
+                *reinterpret_cast<u32x4*>(vs + (4 * kg + j) * Gm::VRPITCH + part * 16) = vr[j];
         } else {
-            const uint32_t w[4][4] = {{vr[0].x, vr[0].y, vr[0].z, vr[0].w},
-                                      {vr[1].x, vr[1].y, vr[1].z, vr[1].w},
-                                      {vr[2].x, vr[2].y, vr[2].z, vr[2].w},
-                                      {vr[3].x, vr[3].y, vr[3].z, vr[3].w}};
+            const uint32_t w[4][4] = {{vr[0][0], vr[0][1], vr[0][2], vr[0][3]},
+                                      {vr[1][0], vr[1][1], vr[1][2], vr[1][3]},
+                                      {vr[2][0], vr[2][1], vr[2][2], vr[2][3]},
+                                      {vr[3][0], vr[3][1], vr[3][2], vr[3][3]}};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int d = part * 4 + i;
                 const int col = (kg ^ (part & Gm::GMASK)) * Gm::GBYTES;  // d >> 2 == part
-                *reinterpret_cast<uint4*>(vs + d * Gm::VPITCH + col) =
-                    make_uint4(w[0][i], w[1][i], w[2][i], w[3][i]);
+                *reinterpret_cast<u32x4*>(vs + d * Gm::VPITCH + col) =
+                    u32x4{w[0][i], w[1][i], w[2][i], w[3][i]};
             }
         }
         if (part == 0) {
@@ -599,8 +601,8 @@ __device__ __forceinline__ void prefill(
                         const uint8_t* vp = vtr + (sb * 32 + 16 * st) * Gm::VRPITCH + db * 64;
                         const uint64_t r0 = lds_read_tr(vp);
                         const uint64_t r1 = lds_read_tr(vp + 8 * Gm::VRPITCH);
-                        const uint4 w = make_uint4((uint32_t)r0, (uint32_t)(r0 >> 32), (uint32_t)r1,
-                                                   (uint32_t)(r1 >> 32));
+                        const u32x4 w = u32x4{(uint32_t)r0, (uint32_t)(r0 >> 32), (uint32_t)r1,
+                                              (uint32_t)(r1 >> 32)};
                         if (B2H && big) {  // uniform; P as hi + lo bf16, packed per step (rare path)
                             typename OB::v pbh, pbl;
                             pack8<DT_BF16>(p + 8 * st, pbh, pbl);
