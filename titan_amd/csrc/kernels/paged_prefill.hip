@@ -46,7 +46,7 @@ namespace {
 enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_FP8 = 3 };
 
 constexpr int NT = 512;           // threads per workgroup (8 waves)
-constexpr int NL = 256;           // threads (waves 0-3) that stage the K/V tiles
+constexpr int NL = 256;           // f32 pages: threads (waves 0-3) that stage the K/V tiles
 constexpr uint32_t ROWS = NT / 2;  // query rows per workgroup: 32 per wave
 constexpr uint32_t SLICE = 1024;  // block-table entries staged in LDS at once
 constexpr float RESCALE_LOG2 = 8.0f;
@@ -132,14 +132,20 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint3
     return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
-// Geometry per (type, head_dim): one load item = 4 consecutive keys x 16
-// bytes of a head row; N keys per tile so that the NL staging threads own one item each.
+// Geometry per (type, head_dim): one load item = KPI consecutive keys x 16
+// bytes of a head row; N keys per tile so that the NLOAD staging threads own
+// one item each.  bf16 pages: every thread stages 2 keys, so the bf16 -> f16
+// widening is spread over all 8 waves (measured 8.7 % faster than waves 0-3
+// staging 4 keys each, which stays faster for f16, E4M3 and f32 pages:
+// for f32, an item is one 16-byte V^T group of 4 keys).
 template <int DT, int HD>
 struct geo {
     static constexpr int ELT = op_t<DT>::ELT;
     static constexpr int EPC = 16 / ELT;          // elements per 16-byte chunk
     static constexpr int PARTS = HD / EPC;        // chunks per head row
-    static constexpr int N = 4 * NL / PARTS;      // keys per tile
+    static constexpr int KPI = DT == DT_BF16 ? 2 : 4;  // keys per load item
+    static constexpr int NLOAD = DT == DT_BF16 ? NT : NL;
+    static constexpr int N = KPI * NLOAD / PARTS;  // keys per tile
     static constexpr int SUB = N / 32;            // 32-key sub-blocks per tile
     static constexpr int KPITCH = HD * ELT + 16;  // bytes per K row in LDS
     static constexpr int VPITCH = N * ELT + (ELT == 4 ? 16 : 8);  // bytes per V^T row
@@ -307,11 +313,12 @@ __device__ __forceinline__ void prefill(
     constexpr int CT = (F8 || B2H) ? DT_F16 : DT;  // MFMA operand type
     constexpr uint32_t SE = F8 ? 1u : (uint32_t)Gm::ELT;  // stored element bytes
     const uint32_t head_off = hk * HD * SE + part * (16 / Gm::ELT) * SE;
-    u32x4 kr[4], vr[4];
-    uint32_t okbits = 0;  // bit j: key 4*kg+j loadable; bit 4+j: key <= kmax with a bad page
+    constexpr int KPI = Gm::KPI;
+    u32x4 kr[KPI], vr[KPI];
+    uint32_t okbits = 0;  // bit j: key KPI*kg+j loadable; bit KPI+j: key <= kmax with a bad page
 
     const uint32_t slot_bytes = 2u * row_bytes;
-    const bool page4 = (block_tokens & 3u) == 0u;  // 4 aligned keys share a page
+    const bool pagek = block_tokens % KPI == 0u;  // an item's KPI aligned keys share a page
     // page id of table entry e: from the LDS slice, or (direct) from the
     // global table with the slice's bounds checks -- the re-stage of a tile
     // runs after the slice may have moved on to the next tile
@@ -325,9 +332,9 @@ __device__ __forceinline__ void prefill(
         return v;
     };
     auto issue = [&](uint32_t t, bool direct = false) {
-        const uint32_t key0 = t * N + 4 * kg;
+        const uint32_t key0 = t * N + KPI * kg;
         okbits = 0;
-        if (page4) {
+        if (pagek) {
             const uint32_t e = entry_of(key0);
             const uint32_t phys = page_of(e, direct);
             const uint32_t slot = key0 - e * block_tokens;
@@ -336,10 +343,10 @@ __device__ __forceinline__ void prefill(
                                (uint64_t)(pv ? slot * slot_bytes + head_off : 0u);
             const uint32_t step = pv ? slot_bytes : 0u;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < KPI; ++j) {
                 const bool live = key0 + j <= kmax;
                 okbits |= (live && pv ? 1u : 0u) << j;
-                okbits |= (live && !pv ? 1u : 0u) << (4 + j);
+                okbits |= (live && !pv ? 1u : 0u) << (KPI + j);
                 if constexpr (F8) {
                     const u32x2 a = *reinterpret_cast<const u32x2*>(p + j * step);
                     const u32x2 b = *reinterpret_cast<const u32x2*>(p + j * step + row_bytes);
@@ -351,17 +358,17 @@ __device__ __forceinline__ void prefill(
                 }
             }
         } else {
-            uint32_t phys[4];
+            uint32_t phys[KPI];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) phys[j] = page_of(entry_of(key0 + j), direct);
+            for (int j = 0; j < KPI; ++j) phys[j] = page_of(entry_of(key0 + j), direct);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < KPI; ++j) {
                 const uint32_t key = key0 + j;
                 const uint32_t slot = key - entry_of(key) * block_tokens;
                 const bool live = key <= kmax;
                 const bool pv = phys[j] != 0xFFFFFFFFu;
                 okbits |= (live && pv ? 1u : 0u) << j;
-                okbits |= (live && !pv ? 1u : 0u) << (4 + j);
+                okbits |= (live && !pv ? 1u : 0u) << (KPI + j);
                 const uint8_t* p = pool + (uint64_t)(pv ? phys[j] : 0u) * page_bytes +
                                    (uint64_t)(pv ? slot * slot_bytes + head_off : 0u);
                 if constexpr (F8) {
@@ -382,7 +389,7 @@ __device__ __forceinline__ void prefill(
         uint8_t* vs = ks + Gm::KBYTES;
         if constexpr (F8) {  // codes -> f16, then the f16 staging below
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < KPI; ++j) {
                 kr[j] = e4m3x8_to_f16(kr[j][0], kr[j][1]);
                 vr[j] = e4m3x8_to_f16(vr[j][0], vr[j][1]);
             }
@@ -391,7 +398,7 @@ __device__ __forceinline__ void prefill(
             if (!raw) {  // bf16 -> f16; a value beyond f16's range flags the tile
                 u16x2 emax = {0, 0};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < KPI; ++j) {
                     kr[j] = bf16x8_to_f16(kr[j], emax);
                     vr[j] = bf16x8_to_f16(vr[j], emax);
                 }
@@ -399,18 +406,19 @@ __device__ __forceinline__ void prefill(
             }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (okbits != 0xFu) {  // rare: keys past the window or on a bad page
+        for (int j = 0; j < KPI; ++j) {
+            if (okbits != (1u << KPI) - 1u) {  // rare: keys past the window or on a bad page
                 const bool z = !((okbits >> j) & 1u);
                 vr[j] = z ? u32x4{0u, 0u, 0u, 0u} : vr[j];
             }
-            *reinterpret_cast<u32x4*>(ks + (4 * kg + j) * Gm::KPITCH + part * 16) = kr[j];
+            *reinterpret_cast<u32x4*>(ks + (KPI * kg + j) * Gm::KPITCH + part * 16) = kr[j];
         }
         if constexpr (Gm::VROWM) {  // V rows like K rows
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<u32x4*>(vs + (4 * kg + j) * Gm::VRPITCH + part * 16) = vr[j];
+            for (int j = 0; j < KPI; ++j)
+                *reinterpret_cast<u32x4*>(vs + (KPI * kg + j) * Gm::VRPITCH + part * 16) = vr[j];
         } else {
+            static_assert(Gm::VROWM || KPI == 4, "a V^T group is 4 keys of one item");
             const uint32_t w[4][4] = {{vr[0][0], vr[0][1], vr[0][2], vr[0][3]},
                                       {vr[1][0], vr[1][1], vr[1][2], vr[1][3]},
                                       {vr[2][0], vr[2][1], vr[2][2], vr[2][3]},
@@ -426,10 +434,13 @@ __device__ __forceinline__ void prefill(
         if (part == 0) {
             uint32_t f = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) f |= ((okbits >> j) & 1u) << (8 * j);
-            *reinterpret_cast<uint32_t*>(kflag + buf * N + 4 * kg) = f;
+            for (int j = 0; j < KPI; ++j) f |= ((okbits >> j) & 1u) << (8 * j);
+            if constexpr (KPI == 4)
+                *reinterpret_cast<uint32_t*>(kflag + buf * N + 4 * kg) = f;
+            else
+                *reinterpret_cast<uint16_t*>(kflag + buf * N + 2 * kg) = (uint16_t)f;
         }
-        if (okbits >> 4) hdr->tile_bad[buf] = t;
+        if (okbits >> KPI) hdr->tile_bad[buf] = t;
     };
 
     // ---- Q operands for this lane's row: contraction index mapping
@@ -476,7 +487,7 @@ __device__ __forceinline__ void prefill(
     }
     stage_slice(0);
     __syncthreads();
-    const bool loader = tid < NL;  // uniform per wave
+    const bool loader = tid < Gm::NLOAD;  // uniform per wave
     if (loader) issue(0);
 
     for (uint32_t j = 0; j < n_tiles; ++j) {
