@@ -517,10 +517,13 @@ __device__ __forceinline__ void prefill(
         const uint8_t* ks = stage + buf * Gm::STAGE;
         const uint8_t* vs = ks + Gm::KBYTES;
         const bool bad = hdr->tile_bad[buf] == j;
+        // all score blocks of the tile first, one running-max update per tile,
+        // then per block the weights and O^T += V^T P^T (one basic block: the
+        // next block's weights can interleave with this block's MFMAs)
+        f32x16 sv[Gm::SUB];
 #pragma unroll
         for (int sb = 0; sb < Gm::SUB; ++sb) {
             const uint32_t kb = j * N + sb * 32;
-            if (kb > wave_max) break;
             // S^T (32 keys x 32 rows) = K Q^T
             f32x16 s = f32x16{};
             const uint8_t* krow = ks + (sb * 32 + l32) * Gm::KPITCH;
@@ -573,9 +576,14 @@ __device__ __forceinline__ void prefill(
                     }
                 }
             }
-            float mx = s[0];
+            sv[sb] = s;
+        }
+        {
+            float mx = sv[0][0];
 #pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            for (int sb = 0; sb < Gm::SUB; ++sb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sv[sb][r]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             if (__builtin_amdgcn_ballot_w64(mx > m_run + RESCALE_LOG2)) {
                 const float mn = fmaxf(m_run, mx);
@@ -585,6 +593,10 @@ __device__ __forceinline__ void prefill(
                 for (int i = 0; i < HD / 32; ++i) acc[i] *= alpha;
                 m_run = mn;
             }
+        }
+#pragma unroll
+        for (int sb = 0; sb < Gm::SUB; ++sb) {
+            const f32x16 s = sv[sb];
             float p[16];
             float ps = 0.f;
 #pragma unroll
