@@ -262,6 +262,31 @@ def test_host_reserve_batch_all_or_nothing():
         assert [(p.table(s), p.L.eh_kvcache_token_count(p.h, s)) for s in range(4)] == before
 
 
+def test_host_reserve_of_a_huge_count_is_exhaustion():
+    """A token count near 2^64 must not wrap the page arithmetic into a small
+    request: it cannot fit the pool, so PoolExhausted, with nothing changed."""
+    nb, bt = 6, 4
+    p = HostCache(nb, bt, 1, 2)
+    for _ in range(2):
+        p.L.eh_kvcache_new_sequence(p.h)
+    p.reserve(0, 5)
+    before = [(p.table(s), p.L.eh_kvcache_token_count(p.h, s)) for s in range(2)]
+    huge = (1 << 64) - 3                           # 5 + huge + 3 wraps to 5 in 64 bits
+    start = C.c_uint64(0)
+    with pytest.raises(KvCacheError) as e:
+        check(p.L.eh_kvcache_reserve(p.h, 0, huge, C.byref(start)), host=True)
+    assert e.value.kind == "PoolExhausted"
+    seqs = np.array([1, 0], np.uint64)
+    counts = np.array([1, huge], np.uint64)
+    starts = np.zeros(2, np.uint64)
+    with pytest.raises(KvCacheError) as e:
+        check(p.L.eh_kvcache_reserve_batch(p.h, seqs.ctypes.data, 2, counts.ctypes.data,
+                                           starts.ctypes.data), host=True)
+    assert e.value.kind == "PoolExhausted"
+    assert [(p.table(s), p.L.eh_kvcache_token_count(p.h, s)) for s in range(2)] == before
+    assert p.L.eh_kvcache_blocks_used(p.h) == 2
+
+
 def test_host_truncate_restores_free_list_order():
     p, q = HostCache(12, 4, 1, 2), HostCache(12, 4, 1, 2)
     for c in (p, q):

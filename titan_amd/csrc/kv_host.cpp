@@ -119,16 +119,22 @@ int64_t eh_kvcache_block_table(const eh_kvcache* c, uint64_t seq, uint32_t* out,
     return (int64_t)t.size();
 }
 
+// Pages sequence `seq` holds after n_tokens more tokens, in 128 bits so that
+// an absurd n_tokens cannot wrap around to a small count.
+static unsigned __int128 pages_after(const eh_kvcache* c, uint64_t seq, uint64_t n_tokens) {
+    const unsigned __int128 bt = c->block_tokens;
+    return ((unsigned __int128)c->tokens[seq] + n_tokens + bt - 1) / bt;
+}
+
 eh_status eh_kvcache_reserve(eh_kvcache* c, uint64_t seq, uint64_t n_tokens, uint64_t* start_pos) {
     // The bookkeeping half of cache.rs:153-192 for n tokens: a fresh page is
     // popped whenever the position crosses a page boundary.  All or nothing:
     // on exhaustion nothing changes (for n = 1 this is the reference's rule).
     if (seq >= c->tables.size()) return invalid("unknown sequence id");
     const uint64_t pos = c->tokens[seq];
-    const uint64_t bt = c->block_tokens;
     const uint64_t have = c->tables[seq].size();
-    const uint64_t need = (pos + n_tokens + bt - 1) / bt;
-    const uint64_t fresh = need > have ? need - have : 0;
+    const unsigned __int128 need = pages_after(c, seq, n_tokens);
+    const unsigned __int128 fresh = need > have ? need - have : 0;
     if (fresh > c->free_list.size()) {
         g_used = eh_kvcache_blocks_used(c);
         g_total = c->n_blocks;
@@ -153,17 +159,18 @@ eh_status eh_kvcache_reserve_batch(eh_kvcache* c, const uint64_t* seqs, uint64_t
     // would pop them.
     if (!c) return invalid("cache is null");
     if (n_seqs && (!seqs || !n_tokens)) return invalid("seqs / n_tokens is null");
-    const uint64_t bt = c->block_tokens;
-    uint64_t fresh = 0;
+    unsigned __int128 fresh = 0;  // clamped at free + 1: exhausted either way
     std::vector<uint8_t> seen(c->tables.size(), 0);
     for (uint64_t i = 0; i < n_seqs; ++i) {
         const uint64_t s = seqs[i];
         if (s >= c->tables.size()) return invalid("unknown sequence id");
         if (seen[s]) return invalid("sequence listed twice");
         seen[s] = 1;
-        const uint64_t need = (c->tokens[s] + n_tokens[i] + bt - 1) / bt;
+        const unsigned __int128 need = pages_after(c, s, n_tokens[i]);
         const uint64_t have = c->tables[s].size();
-        fresh += need > have ? need - have : 0;
+        const unsigned __int128 add = need > have ? need - have : 0;
+        fresh += add;
+        if (fresh > c->free_list.size()) fresh = (unsigned __int128)c->free_list.size() + 1;
     }
     if (fresh > c->free_list.size()) {
         g_used = eh_kvcache_blocks_used(c);
