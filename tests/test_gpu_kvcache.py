@@ -208,9 +208,12 @@ def test_batch_exhaustion_mid_batch_changes_nothing(dev):
     assert e.value.kind == "PoolExhausted" and (e.value.blocks_used, e.value.blocks_total) == (4, 5)
     assert [(c.seq_block_table(s), c.token_count(s)) for s in seqs] == before
     assert c.blocks_used() == 4
-    # shapes are checked before any page moves
+    # shapes and counts are checked before any page moves
     with pytest.raises(KvCacheError):
         c.append_batch(seqs, one[:2], one)
+    with pytest.raises(KvCacheError) as e:
+        c.extend_batch(seqs, [2, -1, 2], one, one)
+    assert e.value.msg == "token counts must not be negative"
     assert [(c.seq_block_table(s), c.token_count(s)) for s in seqs] == before
     same_pool(c, o)
 

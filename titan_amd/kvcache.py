@@ -225,8 +225,12 @@ class PagedKvCache:
         counts = [int(n) for n in counts]
         if len(counts) != B:
             raise KvCacheError("InvalidArgs", "one count per sequence")
+        if any(n < 0 for n in counts):
+            raise KvCacheError("InvalidArgs", "token counts must not be negative")
         m = self._cfg.row_len()
         total = sum(counts)
+        if total >= 1 << 31:
+            raise KvCacheError("InvalidArgs", "at most 2^31 - 1 rows per launch")
         want = TORCH_DTYPE[self.dtype]
         for t in (keys, values):
             if tuple(t.shape) != (total, m):
