@@ -347,10 +347,12 @@ __device__ __forceinline__ void decode_tiles(
         const u32x4 h = sv.hdr[w];
         const u32x4* it = sv.items + (uint64_t)w * cap;
         dsc = lane < cap ? it[lane] : u32x4{NO_PAGE, 0u, 0u, 1u};
-        n_items = uni(h[0]);
+        // a schedule is trusted only as far as memory safety needs: counts
+        // within the run's item capacity, sequences within the batch
+        n_items = uni(h[0]) < cap ? uni(h[0]) : cap;
         b0 = uni(h[1]);
         b_last = uni(h[2]);
-        if (n_items == 0) return;
+        if (n_items == 0 || b0 > b_last || b_last >= batch) return;
         if (n_items > 64) dsc_next = lane + 64 < n_items ? it[lane + 64] : u32x4{NO_PAGE, 0u, 0u, 1u};
     } else {
         // tile prefix over the batch (wave 0), from the live lengths
@@ -471,15 +473,21 @@ __device__ __forceinline__ void decode_tiles(
         constexpr int D = decltype(Dc)::value;
         const uint32_t li = k & 63u;
         const u32x4& src = dsc;
-        const uint32_t phys = uni((uint32_t)__builtin_amdgcn_readlane((int)src[0], (int)li));
-        const uint32_t ib = uni((uint32_t)__builtin_amdgcn_readlane((int)src[1], (int)li));
-        const uint32_t tok0 = uni((uint32_t)__builtin_amdgcn_readlane((int)src[2], (int)li));
-        const uint32_t info = uni((uint32_t)__builtin_amdgcn_readlane((int)src[3], (int)li));
+        const uint32_t praw = uni((uint32_t)__builtin_amdgcn_readlane((int)src[0], (int)li));
+        const uint32_t braw = uni((uint32_t)__builtin_amdgcn_readlane((int)src[1], (int)li));
+        const uint32_t tok0 = uni((uint32_t)__builtin_amdgcn_readlane((int)src[2], (int)li)) & ~(uint32_t)(TILE - 1);
+        const uint32_t iraw = uni((uint32_t)__builtin_amdgcn_readlane((int)src[3], (int)li));
+        // memory safety whatever the descriptor holds: pages inside the pool,
+        // the sequence inside the run's range, at most TILE tokens at a tile
+        // boundary (a well-formed descriptor passes unchanged)
+        const bool pok = (uint64_t)praw < n_blocks;
+        const uint32_t phys = pok ? praw : NO_PAGE;
+        const uint32_t ib = braw < b0 ? b0 : braw > b_last ? b_last : braw;
+        const uint32_t info = (iraw & 31u) > (uint32_t)TILE ? (iraw & ~31u) | (uint32_t)TILE : iraw;
         physp[D] = phys;
         tokp[D] = tok0;
         infop[D] = info;
         seqp[D] = ib;
-        const bool pok = phys != NO_PAGE;
         const uint8_t* base = pool + (uint64_t)(pok ? phys : 0u) * page_bytes +
                               (uint64_t)(tok0 & slot_mask) * slot_bytes + kv_off;
         const uint32_t nvalid = info & 31u;
@@ -829,6 +837,7 @@ __device__ __forceinline__ void merge_body(
         w0 = uni(r[0]);
         w1 = uni(r[1]);
         empty = uni(r[3]) == 0u;
+        if (w0 > w1 || w1 >= P) w1 = w0;  // a span outside the runs: nothing to merge
     } else {
         uint32_t tot = 0, before = 0, mine = 0;
         for (uint32_t j = lane; j < batch; j += 64) {
