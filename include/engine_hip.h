@@ -339,7 +339,9 @@ eh_status eh_decode_schedule(eh_context* ctx, eh_stream stream, const eh_kv_layo
  * eh_paged_decode_batched / eh_paged_decode_batched_e4m3).  E4M3 pages take
  * f32 rows and both scales.  layout, bt_stride, batch and grid must be those
  * the schedule was built with; the pool may differ per layer (same layout).
- * Outputs equal the self-scheduled forms'; workspace as eh_decode_plan. */
+ * Outputs equal the self-scheduled forms'; workspace as eh_decode_plan.  A
+ * schedule built for other values is not detected: the kernels still stay
+ * inside the pool, q, out and the workspace, but the results are unspecified. */
 eh_status eh_append_decode_scheduled(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
                                      void* pool, uint64_t pool_bytes, const void* keys,
                                      uint64_t keys_bytes, const void* values,
