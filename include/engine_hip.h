@@ -123,6 +123,21 @@ eh_status eh_append_kv_e4m3_batched(eh_context* ctx, eh_stream stream, const eh_
                                     const uint32_t* start_pos, uint32_t batch,
                                     uint64_t total_tokens, uint32_t head_dim,
                                     const float* k_scale, const float* v_scale);
+/* Dynamic per-head scales for the E4M3 pool (extension: the "dynamic
+ * per-head scaling factors" of specs/kv-compression/spec.md:9, one f32 scale
+ * per head as design.md:5 allows), computed on the device from f32 rows
+ * keys/values [n_rows, row_len] (a prompt, or a calibration sample):
+ * k_scale[h] = max(amax / 448, FLT_MIN), amax = the largest finite |x| of
+ * head h's K elements (inf and NaN ignored), 1 for a head with no finite
+ * nonzero element; v_scale likewise from values.  448 is E4M3's largest
+ * value, so the rows measured use the whole code range; later rows beyond
+ * it saturate.  The scales are the device arrays every E4M3 entry point
+ * reads; one launch, nothing allocated. */
+eh_status eh_kv_e4m3_scales(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                            const float* keys, uint64_t keys_bytes, const float* values,
+                            uint64_t values_bytes, uint64_t n_rows, uint32_t head_dim,
+                            float* k_scale, uint64_t k_scale_bytes, float* v_scale,
+                            uint64_t v_scale_bytes);
 /* Dequantising read (PagedKvGpu::read_keys / read_values, paged_kv.rs:331-470,
  * of an FP8 pool): out [n_tokens, row_len] f32; `scale` is k_scale or v_scale. */
 eh_status eh_gather_kv_e4m3(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,

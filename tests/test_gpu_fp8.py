@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import orc
-from titan_amd import KvDataType, PagedAttention, PagedKvGpu, PagedKvLayout
+from titan_amd import HipError, KvDataType, PagedAttention, PagedKvGpu, PagedKvLayout
 
 import parity
 from e4m3_data import all_codes, gauss_codes
@@ -212,6 +212,122 @@ def test_e4m3_cosine_vs_f16(dev):
     cos = (a * b).sum(1) / (a.norm(dim=1) * b.norm(dim=1))
     assert cos.mean().item() >= 0.998 and cos.min().item() >= 0.99, (cos.mean().item(),
                                                                       cos.min().item())
+
+
+def e4m3_scales_np(rows, n_kv, hd):
+    """The dynamic per-head scale rule: max(amax / 448, FLT_MIN) over the
+    finite elements of each head, 1 when none is nonzero (all in f32)."""
+    out = np.empty(n_kv, np.float32)
+    for h in range(n_kv):
+        a = np.abs(rows[:, h * hd:(h + 1) * hd].astype(np.float32))
+        a = a[np.isfinite(a)]
+        m = np.float32(a.max()) if a.size else np.float32(0)
+        out[h] = max(m / np.float32(448), np.float32(np.finfo(np.float32).tiny)) if m > 0 else 1.0
+    return out
+
+
+def test_e4m3_dynamic_scales_exact(dev):
+    """eh_kv_e4m3_scales: per kv head, max(amax / 448, FLT_MIN) over the finite
+    elements, bit for bit; NaN and infinities ignored, an all-zero head gets 1,
+    a head of tiny values gets the FLT_MIN floor."""
+    rng = np.random.default_rng(71)
+    n_kv, hd, n = 5, 128, 777
+    rl = n_kv * hd
+    k = (rng.standard_normal((n, rl)) * 3).astype(np.float32)
+    v = rng.standard_normal((n, rl)).astype(np.float32)
+    k[123, 0 * hd + 7] = 913.25          # head 0's amax
+    k[5, 1 * hd + 3] = np.nan            # ignored
+    k[6, 1 * hd + 4] = -np.inf           # ignored
+    k[:, 2 * hd:3 * hd] = 0.0            # all zero: scale 1
+    v[:, 3 * hd:4 * hd] *= 1e-38         # amax / 448 below FLT_MIN: the floor
+    v[400, 4 * hd + 127] = -1.5e7        # the sign does not matter
+    layout = PagedKvLayout(4, 16, rl, KvDataType.FP8)
+    ks, vs = torch.full((n_kv,), -1.0, device=dev), torch.full((n_kv,), -1.0, device=dev)
+    PagedKvGpu(0).e4m3_scales(None, layout, torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                              hd, ks, vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(ks.cpu().numpy().view(np.uint32), e4m3_scales_np(k, n_kv, hd).view(np.uint32))
+    assert np.array_equal(vs.cpu().numpy().view(np.uint32), e4m3_scales_np(v, n_kv, hd).view(np.uint32))
+    assert ks[2].item() == 1.0 and vs[3].item() == np.finfo(np.float32).tiny
+
+
+def test_e4m3_dynamic_scales_end_to_end(dev):
+    """The FP8 spec's flow (specs/kv-compression/spec.md:8-14): scales from the
+    prompt's own K/V on the device, the quantising append with them, E4M3
+    decode against the same K/V in f16.  Pool bytes equal the oracle's
+    quantisation with those scales; output cosine as test_e4m3_cosine_vs_f16
+    (i.i.d. data, no model weights here); and the spec's memory bound for its
+    scenario -- Llama 3.2 3B (28 layers, 8 kv heads, head_dim 128), 4096
+    tokens -- holds for the E4M3 layout (<= 300 MB)."""
+    n_layers, kv3b, hd3b, ctx = 28, 8, 128, 4096
+    per_layer = PagedKvLayout(ctx // 16, 16, kv3b * hd3b, KvDataType.FP8).bytes_total()
+    assert n_layers * per_layer <= 300 * 10**6
+
+    rng = np.random.default_rng(72)
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl = n_kv * hd
+    lens = rng.integers(200, 2049, 6).astype(np.int64)
+    B, T = len(lens), int(lens.sum())
+    tab, nb = make_tables(rng, lens, bt)
+    k = (rng.standard_normal((T, rl)) * 2).astype(np.float32)
+    v = rng.standard_normal((T, rl)).astype(np.float32)
+    layout = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
+    dk, dv = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+    ks, vs = torch.empty(n_kv, device=dev), torch.empty(n_kv, device=dev)
+    kvg = PagedKvGpu(0)
+    kvg.e4m3_scales(None, layout, dk, dv, hd, ks, vs)
+    pool = torch.zeros(layout.bytes_total(), dtype=torch.uint8, device=dev)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    kvg.append_kv_e4m3_batched(None, layout, pool, dk, dv, i32(tab, dev), i32(cu, dev),
+                               i32(np.zeros(B), dev), T, hd, ks, vs)
+    torch.cuda.synchronize()
+    ksn, vsn = ks.cpu().numpy(), vs.cpu().numpy()
+    assert np.array_equal(ksn.view(np.uint32), e4m3_scales_np(k, n_kv, hd).view(np.uint32))
+    # oracle pool: each token's row quantised with the device scales at its page slot
+    want = np.zeros((nb, bt, 2, n_kv, hd), np.uint8)
+    for b in range(B):
+        for t in range(int(lens[b])):
+            r = cu[b] + t
+            for h in range(n_kv):
+                want[tab[b, t // bt], t % bt, 0, h] = orc.f32_to_e4m3(k[r, h * hd:(h + 1) * hd], ksn[h])
+                want[tab[b, t // bt], t % bt, 1, h] = orc.f32_to_e4m3(v[r, h * hd:(h + 1) * hd], vsn[h])
+    assert np.array_equal(pool.cpu().numpy(), want.reshape(-1)), "pool bytes"
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    pa = PagedAttention(0)
+    dq, dl, dt = torch.from_numpy(q).to(dev), i32(lens, dev), i32(tab, dev)
+    p8 = PagedAttention.plan(B, n_head, n_kv, hd, bt, 2048, 0, KvDataType.FP8)
+    o8 = torch.empty((B, n_head, hd), device=dev)
+    pa.decode_batched_e4m3(None, dq, pool, dt, dl, o8, n_head, n_kv, hd, bt, ks, vs, p8,
+                           PagedAttention.workspace(p8))
+    # the same rows as f16 pages
+    f16 = np.zeros((nb, bt, 2, rl), np.float16)
+    for b in range(B):
+        for t in range(int(lens[b])):
+            f16[tab[b, t // bt], t % bt, 0] = k[cu[b] + t]
+            f16[tab[b, t // bt], t % bt, 1] = v[cu[b] + t]
+    p16 = PagedAttention.plan(B, n_head, n_kv, hd, bt, 2048, 0, KvDataType.F16)
+    o16 = torch.empty_like(o8)
+    pa.decode_batched(None, dq, torch.from_numpy(f16.reshape(-1)).to(dev), dt, dl, o16, n_head,
+                      n_kv, hd, bt, KvDataType.F16, p16, PagedAttention.workspace(p16))
+    torch.cuda.synchronize()
+    a, c = o8.cpu().double().reshape(-1, hd), o16.cpu().double().reshape(-1, hd)
+    cos = (a * c).sum(1) / (a.norm(dim=1) * c.norm(dim=1))
+    assert cos.mean().item() >= 0.998 and cos.min().item() >= 0.99, (cos.mean().item(),
+                                                                      cos.min().item())
+
+
+def test_e4m3_dynamic_scales_errors(dev):
+    rl, hd = 256, 128
+    layout = PagedKvLayout(4, 16, rl, KvDataType.FP8)
+    rows = torch.zeros((8, rl), device=dev)
+    sc = torch.empty(2, device=dev)
+    kvg = PagedKvGpu(0)
+    with pytest.raises(HipError):                         # scale arrays shorter than n_kv
+        kvg.e4m3_scales(None, layout, rows, rows, hd, sc[:1], sc)
+    with pytest.raises(HipError):                         # not an FP8 layout
+        kvg.e4m3_scales(None, PagedKvLayout(4, 16, rl, KvDataType.F16), rows, rows, hd, sc, sc)
+    with pytest.raises(HipError):                         # head_dim must divide row_len
+        kvg.e4m3_scales(None, layout, rows, rows, 96, sc, sc)
 
 
 def test_e4m3_entry_rejects_other_paths(dev):

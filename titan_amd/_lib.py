@@ -45,6 +45,8 @@ _SIGS = {
                                         u64, u32, vp, vp, u32, u64, u32, vp, vp]),
     "eh_gather_kv_e4m3": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, u64, u64, i32,
                                 u32, vp]),
+    "eh_kv_e4m3_scales": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, u64, u32, vp, u64, vp,
+                                u64]),
     "eh_copy_pages": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, vp, u32]),
     "eh_remap_block_tables": (i32, [vp, vp, vp, u64, vp, u32]),
     "eh_page_refcounts": (i32, [vp, vp, vp, u32, vp, u32, vp, u32]),

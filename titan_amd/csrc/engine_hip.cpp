@@ -800,6 +800,31 @@ eh_status eh_append_kv_e4m3_batched(eh_context* c, eh_stream stream, const eh_kv
                   head_dim, (uint32_t)l->block_tokens, (uint64_t)l->n_blocks, k_scale, v_scale);
 }
 
+eh_status eh_kv_e4m3_scales(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                            const float* keys, uint64_t keys_bytes, const float* values,
+                            uint64_t values_bytes, uint64_t n_rows, uint32_t head_dim,
+                            float* k_scale, uint64_t k_scale_bytes, float* v_scale,
+                            uint64_t v_scale_bytes) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    eh_status st = check_e4m3(l, head_dim, k_scale, v_scale);
+    if (st) return st;
+    const uint64_t n_kv = l->row_len / head_dim;
+    if (k_scale_bytes < n_kv * 4) return invalid_size(n_kv * 4, k_scale_bytes, "k_scale");
+    if (v_scale_bytes < n_kv * 4) return invalid_size(n_kv * 4, v_scale_bytes, "v_scale");
+    if (n_kv > 65535) return invalid_size(65535, n_kv, "kv heads");
+    const uint64_t kv_expected = n_rows * l->row_len * 4;
+    if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
+    if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
+    if (n_rows && (!keys || !values)) return fail(EH_INVALID_ARGS, "keys/values are null");
+    if (((uintptr_t)keys | (uintptr_t)values) % 16)
+        return fail(EH_UNSUPPORTED, "alignment (keys/values 16 B)");
+    if (n_rows > 0xFFFFFFFFull) return invalid_size(0xFFFFFFFFull, n_rows, "rows");
+    st = bind(c);
+    if (st) return st;
+    return launch(c, c->mod_kv, "eh_kv_e4m3_scales", dim3((uint32_t)n_kv, 2), dim3(256), stream,
+                  keys, values, (uint32_t)n_rows, (uint32_t)l->row_len, head_dim, k_scale, v_scale);
+}
+
 eh_status eh_gather_kv_e4m3(eh_context* c, eh_stream stream, const eh_kv_layout* l,
                             const void* pool, uint64_t pool_bytes, const uint32_t* bt,
                             uint64_t bt_bytes, float* out, uint64_t out_bytes, uint64_t start_token,

@@ -192,6 +192,44 @@ extern "C" __global__ __launch_bounds__(256) void eh_append_kv_e4m3(
     }
 }
 
+// Dynamic per-head E4M3 scales from data (the FP8 KV design's per-head f32
+// scale): scale[h] = max(amax_h / 448, FLT_MIN), amax_h = the largest finite
+// magnitude among head h's elements of rows [n_rows, row_len], so those
+// elements span the whole code range (448 is E4M3's largest value); a head
+// with no finite nonzero element gets 1.  Grid (n_kv, 2): y = 0 reads keys
+// into k_scale, y = 1 values into v_scale; 256 threads; head_dim % 4 == 0.
+extern "C" __global__ __launch_bounds__(256) void eh_kv_e4m3_scales(
+    const float* keys, const float* values, uint32_t n_rows, uint32_t row_len, uint32_t head_dim,
+    float* k_scale, float* v_scale) {
+    __shared__ float wmax[4];
+    const uint32_t h = blockIdx.x;
+    const float* src = (blockIdx.y ? values : keys) + (uint64_t)h * head_dim;
+    const uint32_t qph = head_dim / 4;  // float4s per head row
+    const uint64_t total = (uint64_t)n_rows * qph;
+    float m = 0.0f;
+    for (uint64_t i = threadIdx.x; i < total; i += blockDim.x) {
+        const uint64_t r = i / qph;
+        const float4 x = *reinterpret_cast<const float4*>(src + r * row_len + 4 * (i - r * qph));
+        const float a[4] = {__builtin_fabsf(x.x), __builtin_fabsf(x.y), __builtin_fabsf(x.z),
+                            __builtin_fabsf(x.w)};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (a[k] <= 3.40282347e38f) m = a[k] > m ? a[k] : m;  // finite only: NaN and inf fail
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float y = __shfl_xor(m, o, 64);
+        m = y > m ? y : m;
+    }
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; ++w) m = wmax[w] > m ? wmax[w] : m;
+        const float s = m / 448.0f;
+        (blockIdx.y ? v_scale : k_scale)[h] = m > 0.0f ? (s > 1.17549435e-38f ? s : 1.17549435e-38f) : 1.0f;
+    }
+}
+
 // Dequantising gather of one sequence's K (is_value = 0) or V rows:
 // out [n_tokens, row_len] f32 = decode(code) * scale of the element's head;
 // rows whose block-table entry is missing are left untouched.

@@ -126,6 +126,22 @@ class PagedKvGpu:
             bb, int(stride), buf(cu_seqlens)[0], buf(start_pos)[0], int(batch), int(total_tokens),
             int(head_dim), buf(k_scale)[0], buf(v_scale)[0]))
 
+    def e4m3_scales(self, stream, layout, keys, values, head_dim, k_scale, v_scale):
+        """Dynamic per-kv-head scales of an E4M3 pool from f32 rows keys/values
+        [n, row_len] (a prompt or a calibration sample): scale = max(amax / 448,
+        FLT_MIN) per head over the finite elements, 1 for a head with none
+        nonzero; written to the device tensors k_scale / v_scale [n_kv] that
+        the E4M3 entry points read (the per-head scales of the FP8 KV design,
+        openspec/archive/2026-08-28-fp8-kv-cache-quantization/specs/
+        kv-compression/spec.md:9)."""
+        kp, kb = buf(keys)
+        vp, vb = buf(values)
+        ksp, ksb = buf(k_scale)
+        vsp, vsb = buf(v_scale)
+        check(self._L.eh_kv_e4m3_scales(self._ctx.handle, stream_handle(stream),
+                                        C.byref(layout.c()), kp, kb, vp, vb, int(keys.shape[0]),
+                                        int(head_dim), ksp, ksb, vsp, vsb))
+
     def read_e4m3(self, stream, layout, pool, block_table, out, start_token, n_tokens, is_value,
                   head_dim, scale):
         """read_keys / read_values of an E4M3 pool, dequantised: out [n, row_len]
