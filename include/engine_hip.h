@@ -181,7 +181,8 @@ eh_status eh_paged_attention(eh_context* ctx, eh_stream stream, uint32_t kv_dtyp
  * split-K decode using the context's scratch.  Unlike the reference, every
  * token is attended (no 32-split cap) and the split count follows the
  * device-side position when pos_ptr is given (grid sized from the block
- * table's capacity).  Calls sharing one context must not overlap in time. */
+ * table's capacity).  Calls sharing one context must not overlap in time
+ * (eh_flash_decoding_ws takes a workspace of its own instead). */
 eh_status eh_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
                             const float* q, uint64_t q_bytes, const void* pool,
                             uint64_t pool_bytes, const uint32_t* block_table, uint64_t bt_bytes,
@@ -209,6 +210,41 @@ eh_status eh_append_flash_decoding(eh_context* ctx, eh_stream stream, uint32_t k
                                    uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
                                    uint64_t block_tokens, uint64_t query_pos,
                                    const uint32_t* pos_ptr);
+
+/* ---- The three single-sequence calls above with a caller-owned workspace
+ * (extension): the split-K partials go to `workspace` instead of the
+ * context's scratch, so calls on different streams may overlap in time (one
+ * workspace per concurrent call).  Arguments and results are those of the
+ * call without _ws.  The split grows until its partials fit workspace_bytes;
+ * eh_single_decode_workspace_bytes() (the context scratch's size) always
+ * suffices, and a context that fits one pass needs none (0 bytes).  A
+ * workspace too small for the longest split is EH_INVALID_SIZE (expected =
+ * the least that fits).  16-byte aligned. */
+uint64_t eh_single_decode_workspace_bytes(void);
+eh_status eh_paged_attention_ws(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                                const float* q, uint64_t q_bytes, const void* pool,
+                                uint64_t pool_bytes, const uint32_t* block_table,
+                                uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                                uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                                uint64_t block_tokens, uint64_t seq_tokens, uint64_t query_pos,
+                                int causal, const uint32_t* pos_ptr, void* workspace,
+                                uint64_t workspace_bytes);
+eh_status eh_flash_decoding_ws(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                               const float* q, uint64_t q_bytes, const void* pool,
+                               uint64_t pool_bytes, const uint32_t* block_table, uint64_t bt_bytes,
+                               float* out, uint64_t out_bytes, uint64_t n_head, uint64_t n_head_kv,
+                               uint64_t head_dim, uint64_t block_tokens, uint64_t seq_tokens,
+                               uint64_t query_pos, int causal, const uint32_t* pos_ptr,
+                               void* workspace, uint64_t workspace_bytes);
+eh_status eh_append_flash_decoding_ws(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
+                                      const void* keys, uint64_t keys_bytes, const void* values,
+                                      uint64_t values_bytes, const float* q, uint64_t q_bytes,
+                                      void* pool, uint64_t pool_bytes,
+                                      const uint32_t* block_table, uint64_t bt_bytes, float* out,
+                                      uint64_t out_bytes, uint64_t n_head, uint64_t n_head_kv,
+                                      uint64_t head_dim, uint64_t block_tokens, uint64_t query_pos,
+                                      const uint32_t* pos_ptr, void* workspace,
+                                      uint64_t workspace_bytes);
 
 /* ---- Batched decode (extension: B sequences in one launch).
  * eh_decode_plan picks the kernel and its launch shape for contexts up to

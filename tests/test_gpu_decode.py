@@ -505,6 +505,84 @@ def test_fused_step_masked_page_device_position(dev, case):
     check_close(out.cpu().numpy(), ref, KvDataType.F16)
 
 
+def test_single_sequence_calls_with_own_workspace(dev):
+    """The _ws forms of eh_paged_attention / eh_flash_decoding /
+    eh_append_flash_decoding: with a workspace of the context scratch's size
+    they equal the shared-scratch calls bit for bit; with a smaller one the
+    split grows and the result stays within the bar of the oracle; a
+    workspace too small for the longest split is InvalidSize naming the
+    least that fits; calls on two streams with their own workspaces overlap
+    and both match the oracle."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl = n_kv * hd
+    rng = np.random.default_rng(57)
+    n = 20000
+    nb = n // bt + 8
+    table = rng.permutation(nb)[:n // bt + 1].astype(np.uint32)
+    base = rng.standard_normal(nb * bt * 2 * rl).astype(np.float32)
+    pool = torch.from_numpy(base).half().to(dev)
+    pf = torch.from_numpy(base).half().float().numpy()
+    dt = i32(table, dev)
+    pa = PagedAttention(0)
+    full = torch.empty(PagedAttention.single_workspace_bytes() // 4, device=dev)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    dq = torch.from_numpy(q).to(dev)
+    ref = orc.sdpa_decode(pf, table, bt, n, q, n_head, n_kv, hd, True, n - 1)
+    for call in ("launch_flash_decoding", "launch_with_pos_ptr"):
+        a = torch.empty(n_head * hd, device=dev)
+        b = torch.empty_like(a)
+        args = (None, dq, pool, dt)
+        tail = (n_head, n_kv, hd, bt, n, n - 1, True)
+        if call == "launch_flash_decoding":
+            pa.launch_flash_decoding(*args, a, *tail, kv_dtype=KvDataType.F16)
+            pa.launch_flash_decoding(*args, b, *tail, kv_dtype=KvDataType.F16, workspace=full)
+        else:
+            pa.launch_with_pos_ptr(*args, a, *tail, None, KvDataType.F16)
+            pa.launch_with_pos_ptr(*args, b, *tail, None, KvDataType.F16, workspace=full)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), call
+        check_close(b.cpu().numpy(), ref, KvDataType.F16, call + " _ws")
+    # a small workspace: longer splits, same result within the bar
+    small = torch.empty(12 * 1024, device=dev)
+    c = torch.empty(n_head * hd, device=dev)
+    pa.launch_flash_decoding(None, dq, pool, dt, c, n_head, n_kv, hd, bt, n, n - 1, True,
+                             kv_dtype=KvDataType.F16, workspace=small)
+    torch.cuda.synchronize()
+    check_close(c.cpu().numpy(), ref, KvDataType.F16, "flash_decoding small workspace")
+    with pytest.raises(HipError) as e:
+        pa.launch_flash_decoding(None, dq, pool, dt, c, n_head, n_kv, hd, bt, n, n - 1, True,
+                                 kv_dtype=KvDataType.F16, workspace=torch.empty(16, device=dev))
+    assert e.value.kind == "InvalidSize" and e.value.actual == 64 and e.value.expected > 64
+    # the fused step: same pool bytes and output with and without a workspace
+    p0, p1 = pool.clone(), pool.clone()
+    k = torch.from_numpy(rng.standard_normal(rl).astype(np.float32)).half().to(dev)
+    v = torch.from_numpy(rng.standard_normal(rl).astype(np.float32)).half().to(dev)
+    o0, o1 = torch.empty(n_head * hd, device=dev), torch.empty(n_head * hd, device=dev)
+    pa.append_flash_decoding(None, k, v, dq, p0, dt, o0, n_head, n_kv, hd, bt, n, None,
+                             KvDataType.F16)
+    pa.append_flash_decoding(None, k, v, dq, p1, dt, o1, n_head, n_kv, hd, bt, n, None,
+                             KvDataType.F16, workspace=full)
+    torch.cuda.synchronize()
+    assert torch.equal(p0.view(torch.int16), p1.view(torch.int16))
+    assert torch.equal(o0.view(torch.int32), o1.view(torch.int32))
+    # two streams, one workspace each, no synchronisation between the calls
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    w1, w2 = torch.empty_like(full), torch.empty_like(full)
+    q2 = rng.standard_normal(n_head * hd).astype(np.float32)
+    dq2 = torch.from_numpy(q2).to(dev)
+    r1, r2 = torch.empty(n_head * hd, device=dev), torch.empty(n_head * hd, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        pa.launch_flash_decoding(s1, dq, pool, dt, r1, n_head, n_kv, hd, bt, n, n - 1, True,
+                                 kv_dtype=KvDataType.F16, workspace=w1)
+        pa.launch_flash_decoding(s2, dq2, pool, dt, r2, n_head, n_kv, hd, bt, n - 1000, n - 1001,
+                                 True, kv_dtype=KvDataType.F16, workspace=w2)
+    torch.cuda.synchronize()
+    check_close(r1.cpu().numpy(), ref, KvDataType.F16, "stream 1")
+    ref2 = orc.sdpa_decode(pf, table, bt, n - 1000, q2, n_head, n_kv, hd, True, n - 1001)
+    check_close(r2.cpu().numpy(), ref2, KvDataType.F16, "stream 2")
+
+
 def test_graph_replay_split_count_follows_device_position(dev):
     """The reference sizes its split grid on the host from seq_tokens and
     freezes it at capture (forward_driver.rs:2230-2243), and drops tokens

@@ -73,6 +73,7 @@ def test_launches_do_not_allocate(dev):
     q1 = q[0].contiguous()
     o1 = out[0].contiguous()
     pos1 = pos[:1].contiguous()
+    sws = torch.empty(1 << 16, device=dev)   # caller-owned single-sequence workspace
 
     calls = {
         "eh_append_kv": lambda: kv.append_kv(None, lay16, pool16, k16[:1], v16[:1], row_tab, 499, 1),
@@ -98,6 +99,14 @@ def test_launches_do_not_allocate(dev):
         "eh_append_flash_decoding": lambda: pa.append_flash_decoding(
             None, k16[0].contiguous(), v16[0].contiguous(), q1, pool16, row_tab, o1, nh, nkv, hd,
             bt, 499, kv_dtype=KvDataType.F16),
+        "eh_paged_attention_ws": lambda: pa.launch_with_pos_ptr(
+            None, q1, pool32, row_tab, o1, nh, nkv, hd, bt, 500, 499, True, None, workspace=sws),
+        "eh_flash_decoding_ws": lambda: pa.launch_flash_decoding(
+            None, q1, pool16, row_tab, o1, nh, nkv, hd, bt, 500, 499, True, pos1,
+            kv_dtype=KvDataType.F16, workspace=sws),
+        "eh_append_flash_decoding_ws": lambda: pa.append_flash_decoding(
+            None, k16[0].contiguous(), v16[0].contiguous(), q1, pool16, row_tab, o1, nh, nkv, hd,
+            bt, 499, kv_dtype=KvDataType.F16, workspace=sws),
         "eh_paged_decode_batched (balanced)": lambda: pa.decode_batched(
             None, q, pool16, d_tab, lens, out, nh, nkv, hd, bt, KvDataType.F16, plan, ws),
         "eh_paged_decode_batched (fixed splits)": lambda: pa.decode_batched(

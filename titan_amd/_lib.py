@@ -56,6 +56,13 @@ _SIGS = {
                                 u64, u64, u64, i32, vp]),
     "eh_append_flash_decoding": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp,
                                        u64, u64, u64, u64, u64, u64, vp]),
+    "eh_single_decode_workspace_bytes": (u64, []),
+    "eh_paged_attention_ws": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64, u64,
+                                    u64, u64, u64, i32, vp, vp, u64]),
+    "eh_flash_decoding_ws": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64, u64,
+                                   u64, u64, u64, i32, vp, vp, u64]),
+    "eh_append_flash_decoding_ws": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64,
+                                          vp, u64, u64, u64, u64, u64, u64, vp, vp, u64]),
     "eh_decode_plan": (i32, [u32, u32, u32, u32, u32, u32, u32, u32, P(u32), P(u32), P(u64)]),
     "eh_decode_kernel_name": (i32, [u32, u32, u32, u32, u32, C.c_char_p, u64]),
     "eh_paged_decode_batched": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, u32, vp, u32, vp, u64,

@@ -910,8 +910,15 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
                                       uint64_t n_head_kv, uint64_t head_dim, uint64_t block_tokens,
                                       uint64_t seq_tokens, uint64_t query_pos, int causal,
                                       const uint32_t* pos_ptr, bool single_pass,
-                                      const void* new_k = nullptr, const void* new_v = nullptr) {
+                                      const void* new_k = nullptr, const void* new_v = nullptr,
+                                      bool own_ws = false, void* ws = nullptr,
+                                      uint64_t ws_bytes = 0) {
     if (!c) return fail(EH_INVALID_ARGS, "null context");
+    // partials: the caller's workspace (own_ws) or the context's scratch
+    if (own_ws && ws_bytes && (!ws || (uintptr_t)ws % 16))
+        return fail(EH_INVALID_ARGS, "workspace is null or not 16-byte aligned");
+    float* const part = own_ws ? (float*)ws : c->scratch;
+    const uint64_t part_floats = own_ws ? ws_bytes / 4 : c->scratch_floats;
     eh_status st = validate_attention(kv_dtype, q_bytes, pool_bytes, bt_bytes, out_bytes, n_head,
                                       n_head_kv, head_dim, block_tokens, seq_tokens, query_pos);
     if (st) return st;
@@ -946,16 +953,21 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
     uint64_t tps = auto_tps(1, dk.units, cap, block_tokens, chunk, dk.slots ? 512 : 1024);
     if (single_pass && cap <= max_tps(block_tokens, chunk))
         tps = std::max<uint64_t>(div_ceil(cap, chunk), 1) * chunk;
-    // Grow the split until the partials fit the context's scratch.
+    // Grow the split until the partials fit the scratch (or workspace).
     while (div_ceil(cap, tps) > 1 &&
-           decode_ws_floats(n_head, div_ceil(cap, tps), head_dim) > c->scratch_floats)
+           decode_ws_floats(n_head, div_ceil(cap, tps), head_dim) > part_floats)
         tps *= 2;
+    if (own_ws && tps > max_tps(block_tokens, chunk)) {
+        const uint64_t least = decode_ws_floats(n_head, div_ceil(cap, max_tps(block_tokens, chunk)),
+                                                head_dim) * 4;
+        return invalid_size(least, ws_bytes, "workspace");
+    }
     if (tps > max_tps(block_tokens, chunk) || div_ceil(cap, tps) > kMaxSplits)
         return invalid_size(max_tps(block_tokens, chunk) * kMaxSplits, cap, "context too long");
     a.tps = (uint32_t)tps;
     a.max_splits = (uint32_t)div_ceil(cap, tps);
-    a.part_acc = c->scratch;
-    a.part_ml = c->scratch + n_head * a.max_splits * head_dim;
+    a.part_acc = part;
+    a.part_ml = part + n_head * a.max_splits * head_dim;
     a.new_k = new_k;
     a.new_v = new_v;
     return run_decode(c, stream, a);
@@ -983,14 +995,15 @@ eh_status eh_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype, 
                                 query_pos, causal, pos_ptr, false);
 }
 
-eh_status eh_append_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype,
-                                   const void* keys, uint64_t keys_bytes, const void* values,
-                                   uint64_t values_bytes, const float* q, uint64_t q_bytes,
-                                   void* pool, uint64_t pool_bytes, const uint32_t* bt,
-                                   uint64_t bt_bytes, float* out, uint64_t out_bytes,
-                                   uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
-                                   uint64_t block_tokens, uint64_t query_pos,
-                                   const uint32_t* pos_ptr) {
+static eh_status append_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                       const void* keys, uint64_t keys_bytes, const void* values,
+                                       uint64_t values_bytes, const float* q, uint64_t q_bytes,
+                                       void* pool, uint64_t pool_bytes, const uint32_t* bt,
+                                       uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                                       uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                                       uint64_t block_tokens, uint64_t query_pos,
+                                       const uint32_t* pos_ptr, bool own_ws, void* ws,
+                                       uint64_t ws_bytes) {
     if (kv_dtype == EH_KV_FP8) return fail(EH_UNSUPPORTED, "FP8 pages: fused single-sequence step");
     if (!keys || !values) return fail(EH_INVALID_ARGS, "keys / values are null");
     const uint64_t row = n_head_kv * head_dim * elt_bytes(kv_dtype);
@@ -1004,7 +1017,66 @@ eh_status eh_append_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_
         return invalid_size((query_pos / block_tokens + 1) * 4, bt_bytes, "block_table");
     return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
                                 out_bytes, n_head, n_head_kv, head_dim, block_tokens, query_pos + 1,
-                                query_pos, 1, pos_ptr, false, keys, values);
+                                query_pos, 1, pos_ptr, false, keys, values, own_ws, ws, ws_bytes);
+}
+
+eh_status eh_append_flash_decoding(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                   const void* keys, uint64_t keys_bytes, const void* values,
+                                   uint64_t values_bytes, const float* q, uint64_t q_bytes,
+                                   void* pool, uint64_t pool_bytes, const uint32_t* bt,
+                                   uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                                   uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                                   uint64_t block_tokens, uint64_t query_pos,
+                                   const uint32_t* pos_ptr) {
+    return append_flash_decoding(c, stream, kv_dtype, keys, keys_bytes, values, values_bytes, q,
+                                 q_bytes, pool, pool_bytes, bt, bt_bytes, out, out_bytes, n_head,
+                                 n_head_kv, head_dim, block_tokens, query_pos, pos_ptr, false,
+                                 nullptr, 0);
+}
+
+// ---- The single-sequence calls with a caller-owned workspace (no shared
+// scratch: calls on different streams may overlap).
+uint64_t eh_single_decode_workspace_bytes(void) { return kScratchFloats * sizeof(float); }
+
+eh_status eh_paged_attention_ws(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
+                                uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                                const uint32_t* bt, uint64_t bt_bytes, float* out,
+                                uint64_t out_bytes, uint64_t n_head, uint64_t n_head_kv,
+                                uint64_t head_dim, uint64_t block_tokens, uint64_t seq_tokens,
+                                uint64_t query_pos, int causal, const uint32_t* pos_ptr,
+                                void* workspace, uint64_t workspace_bytes) {
+    return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
+                                out_bytes, n_head, n_head_kv, head_dim, block_tokens, seq_tokens,
+                                query_pos, causal, pos_ptr, true, nullptr, nullptr, true, workspace,
+                                workspace_bytes);
+}
+
+eh_status eh_flash_decoding_ws(eh_context* c, eh_stream stream, uint32_t kv_dtype, const float* q,
+                               uint64_t q_bytes, const void* pool, uint64_t pool_bytes,
+                               const uint32_t* bt, uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                               uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                               uint64_t block_tokens, uint64_t seq_tokens, uint64_t query_pos,
+                               int causal, const uint32_t* pos_ptr, void* workspace,
+                               uint64_t workspace_bytes) {
+    return single_seq_attention(c, stream, kv_dtype, q, q_bytes, pool, pool_bytes, bt, bt_bytes, out,
+                                out_bytes, n_head, n_head_kv, head_dim, block_tokens, seq_tokens,
+                                query_pos, causal, pos_ptr, false, nullptr, nullptr, true, workspace,
+                                workspace_bytes);
+}
+
+eh_status eh_append_flash_decoding_ws(eh_context* c, eh_stream stream, uint32_t kv_dtype,
+                                      const void* keys, uint64_t keys_bytes, const void* values,
+                                      uint64_t values_bytes, const float* q, uint64_t q_bytes,
+                                      void* pool, uint64_t pool_bytes, const uint32_t* bt,
+                                      uint64_t bt_bytes, float* out, uint64_t out_bytes,
+                                      uint64_t n_head, uint64_t n_head_kv, uint64_t head_dim,
+                                      uint64_t block_tokens, uint64_t query_pos,
+                                      const uint32_t* pos_ptr, void* workspace,
+                                      uint64_t workspace_bytes) {
+    return append_flash_decoding(c, stream, kv_dtype, keys, keys_bytes, values, values_bytes, q,
+                                 q_bytes, pool, pool_bytes, bt, bt_bytes, out, out_bytes, n_head,
+                                 n_head_kv, head_dim, block_tokens, query_pos, pos_ptr, true,
+                                 workspace, workspace_bytes);
 }
 
 eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uint32_t n_head_kv,

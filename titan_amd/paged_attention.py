@@ -37,47 +37,64 @@ class PagedAttention:
 
     def launch_with_pos_ptr(self, stream, q, pool, block_table, out, n_head, n_head_kv, head_dim,
                             block_tokens, seq_tokens, query_pos, causal, pos_ptr,
-                            kv_dtype=KvDataType.F32):
-        """paged_attention.rs:177-345 (single pass per kv head)."""
+                            kv_dtype=KvDataType.F32, workspace=None):
+        """paged_attention.rs:177-345 (single pass per kv head).  With a
+        workspace tensor the split-K partials go there instead of the
+        context's shared scratch (calls on other streams may overlap)."""
         self._call(self._L.eh_paged_attention, stream, q, pool, block_table, out, n_head,
                    n_head_kv, head_dim, block_tokens, seq_tokens, query_pos, causal, pos_ptr,
-                   kv_dtype)
+                   kv_dtype, workspace, self._L.eh_paged_attention_ws)
 
     def launch_flash_decoding(self, stream, q, pool, block_table, out, n_head, n_head_kv,
                               head_dim, block_tokens, seq_tokens, query_pos, causal, pos_ptr=None,
-                              kv_dtype=KvDataType.F32):
-        """paged_attention.rs:352-490 (split-K + log-sum-exp merge)."""
+                              kv_dtype=KvDataType.F32, workspace=None):
+        """paged_attention.rs:352-490 (split-K + log-sum-exp merge); workspace
+        as launch_with_pos_ptr."""
         self._call(self._L.eh_flash_decoding, stream, q, pool, block_table, out, n_head,
                    n_head_kv, head_dim, block_tokens, seq_tokens, query_pos, causal, pos_ptr,
-                   kv_dtype)
+                   kv_dtype, workspace, self._L.eh_flash_decoding_ws)
+
+    @staticmethod
+    def single_workspace_bytes():
+        """A workspace size that suffices for every single-sequence call."""
+        return int(_lib.load().eh_single_decode_workspace_bytes())
 
     def append_flash_decoding(self, stream, keys, values, q, pool, block_table, out, n_head,
                               n_head_kv, head_dim, block_tokens, query_pos, pos_ptr=None,
-                              kv_dtype=KvDataType.F32):
+                              kv_dtype=KvDataType.F32, workspace=None):
         """One decode step of one sequence in one launch: keys/values [row_len]
         land at position *pos_ptr (or query_pos), then q attends tokens 0..that
         position (PagedKvGpu.append_kv, paged_kv.rs:200-327, followed by
-        launch_flash_decoding, paged_attention.rs:352-490)."""
+        launch_flash_decoding, paged_attention.rs:352-490); workspace as
+        launch_with_pos_ptr."""
         kp, kb = buf(keys)
         vp_, vb = buf(values)
         qp, qb = buf(q)
         pp, pb = buf(pool)
         bp, bb = buf(block_table)
         op, ob = buf(out)
-        check(self._L.eh_append_flash_decoding(
-            self._ctx.handle, stream_handle(stream), int(kv_dtype), kp, kb, vp_, vb, qp, qb, pp, pb,
-            bp, bb, op, ob, int(n_head), int(n_head_kv), int(head_dim), int(block_tokens),
-            int(query_pos), buf(pos_ptr)[0]))
+        args = (self._ctx.handle, stream_handle(stream), int(kv_dtype), kp, kb, vp_, vb, qp, qb, pp,
+                pb, bp, bb, op, ob, int(n_head), int(n_head_kv), int(head_dim), int(block_tokens),
+                int(query_pos), buf(pos_ptr)[0])
+        if workspace is None:
+            check(self._L.eh_append_flash_decoding(*args))
+        else:
+            check(self._L.eh_append_flash_decoding_ws(*args, *buf(workspace)))
 
     def _call(self, fn, stream, q, pool, block_table, out, n_head, n_head_kv, head_dim,
-              block_tokens, seq_tokens, query_pos, causal, pos_ptr, kv_dtype):
+              block_tokens, seq_tokens, query_pos, causal, pos_ptr, kv_dtype, workspace=None,
+              fn_ws=None):
         qp, qb = buf(q)
         pp, pb = buf(pool)
         bp, bb = buf(block_table)
         op, ob = buf(out)
-        check(fn(self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
-                 op, ob, int(n_head), int(n_head_kv), int(head_dim), int(block_tokens),
-                 int(seq_tokens), int(query_pos), 1 if causal else 0, buf(pos_ptr)[0]))
+        args = (self._ctx.handle, stream_handle(stream), int(kv_dtype), qp, qb, pp, pb, bp, bb,
+                op, ob, int(n_head), int(n_head_kv), int(head_dim), int(block_tokens),
+                int(seq_tokens), int(query_pos), 1 if causal else 0, buf(pos_ptr)[0])
+        if workspace is None:
+            check(fn(*args))
+        else:
+            check(fn_ws(*args, *buf(workspace)))
 
     # ---- batched extension ---------------------------------------------------
     @staticmethod
