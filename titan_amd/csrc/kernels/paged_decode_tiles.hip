@@ -1067,9 +1067,12 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_mass(
 }
 
 // One wave per kv head; at most 8 waves per workgroup; two waves per SIMD
-// (256 VGPRs, no AGPR copies, which would wait for the loads they copy); 2
-// tiles in flight per wave (measured faster than 4: deeper queues slow the
-// random page reads).
+// (256 VGPRs, no AGPR copies, which would wait for the loads they copy).
+// Tiles in flight per wave: 2 for 16-bit pages, 1 for E4M3 pages (half the
+// bytes per tile).  Measured at config 2: 16-bit 1 / 2 / 3 tiles 26.0 / 25.0
+// / 26.5 us per call; E4M3 1 / 2 / 3 / 4 tiles 18.1 / 19.2 / 19.8 / 20.3 us
+// -- deeper queues slow the random page reads.
+constexpr int tiles_depth(int dt) { return dt == DT_FP8 ? 1 : 2; }
 #define EH_TILES_ONE(NAME, DT, G, EXT, SCHED)                                                       \
     extern "C" __global__ __launch_bounds__(512, 1) void NAME(                                     \
         const float* q, uint8_t* pool, uint64_t n_blocks, const uint32_t* bt, uint32_t bt_stride,  \
@@ -1079,7 +1082,7 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_mass(
         uint32_t n_runs, uint32_t sink, uint32_t window, float* tile_rec, float* fin,              \
         uint32_t rec_row, const float* k_scale, const float* v_scale, const u32x4* sched,          \
         uint32_t cap) {                                                                            \
-        decode_tiles<DT, G, 2, 16, EXT, SCHED>(q, pool, n_blocks, bt, bt_stride, lens, lens_add,   \
+        decode_tiles<DT, G, tiles_depth(DT), 16, EXT, SCHED>(q, pool, n_blocks, bt, bt_stride, lens, lens_add,   \
                                                new_k, new_v, batch, out, part_acc, part_ml, n_head, \
                                                n_head_kv, block_tokens, bt_shift, scale_log2,      \
                                                n_runs, sink, window, tile_rec, fin, rec_row,       \
