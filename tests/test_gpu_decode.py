@@ -553,6 +553,19 @@ def test_single_sequence_calls_with_own_workspace(dev):
         pa.launch_flash_decoding(None, dq, pool, dt, c, n_head, n_kv, hd, bt, n, n - 1, True,
                                  kv_dtype=KvDataType.F16, workspace=torch.empty(16, device=dev))
     assert e.value.kind == "InvalidSize" and e.value.actual == 64 and e.value.expected > 64
+    # no workspace at all (null, 0 bytes): a context that one pass covers needs
+    # no partials; a longer one is InvalidSize
+    short = 300
+    a1 = torch.empty(n_head * hd, device=dev)
+    pa.launch_with_pos_ptr(None, dq, pool, dt, a1, n_head, n_kv, hd, bt, short, short - 1, True,
+                           None, KvDataType.F16, workspace=(0, 0))
+    torch.cuda.synchronize()
+    ref_s = orc.sdpa_decode(pf, table, bt, short, q, n_head, n_kv, hd, True, short - 1)
+    check_close(a1.cpu().numpy(), ref_s, KvDataType.F16, "single pass, no workspace")
+    with pytest.raises(HipError) as e:
+        pa.launch_flash_decoding(None, dq, pool, dt, c, n_head, n_kv, hd, bt, n, n - 1, True,
+                                 kv_dtype=KvDataType.F16, workspace=(0, 0))
+    assert e.value.kind == "InvalidSize" and e.value.actual == 0
     # the fused step: same pool bytes and output with and without a workspace
     p0, p1 = pool.clone(), pool.clone()
     k = torch.from_numpy(rng.standard_normal(rl).astype(np.float32)).half().to(dev)
