@@ -145,19 +145,30 @@ __device__ __forceinline__ uint32_t uni(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
 
-// Even cut of T tiles over P workgroups: T = q P + r, workgroup w < r takes
-// q + 1 tiles, the others q (empty workgroups, when T < P, come last).
+// Even cut of T tiles over at most P runs.  The largest run holds
+// k = ceil(T / P) tiles whatever the cut, so the cut uses the fewest runs
+// that keep it at k, P' = ceil(T / k): every used run holds k or k - 1 tiles
+// (config 2: 890 runs of 5 and one of 4, instead of 358 of 5 and 666 of 4),
+// and fewer runs leave fewer partial states -- measured 2 % faster per call.
+// T = q P' + r: run w < r takes q + 1 tiles, the others q; runs P' .. P - 1
+// are empty (first() is clamped to T).
 struct tile_split {
-    uint32_t q, r;
-    __device__ __forceinline__ uint32_t first(uint32_t w) const { return w * q + (w < r ? w : r); }
-    // workgroup holding tile f
+    uint32_t q, r, T;
+    __device__ __forceinline__ uint32_t first(uint32_t w) const {
+        const uint64_t f = (uint64_t)w * q + (w < r ? w : r);
+        return f < T ? (uint32_t)f : T;
+    }
+    // run holding tile f < T
     __device__ __forceinline__ uint32_t owner(uint32_t f) const {
         const uint32_t big = r * (q + 1);
         return f < big ? f / (q + 1) : r + (f - big) / q;
     }
 };
 __device__ __forceinline__ tile_split make_split(uint32_t T, uint32_t P) {
-    return tile_split{T / P, T % P};
+    if (T == 0u || P == 0u) return tile_split{0u, 0u, 0u};
+    const uint32_t k = T / P + (T % P != 0u);
+    const uint32_t pe = T / k + (T % k != 0u);
+    return tile_split{T / pe, T % pe, T};
 }
 
 // Tokens a decode query attends out of the n of its sequence: all of them,
@@ -317,7 +328,7 @@ __device__ __forceinline__ void decode_tiles(
     // dsc (current batch of 64) and dsc_next (the following one)
     uint32_t n_items, b0, b_last;
     u32x4 dsc, dsc_next = u32x4{NO_PAGE, 0u, 0u, 0u};
-    tile_split ts{0u, 0u};
+    tile_split ts{0u, 0u, 0u};
     uint32_t F0 = 0;
     auto make_desc = [&](uint32_t kb) -> u32x4 {  // self-scheduled: item kb + lane
         const uint32_t k = kb + lane;
@@ -373,7 +384,7 @@ __device__ __forceinline__ void decode_tiles(
             if (lane == 0) cum[0] = 0;
         }
         lds_barrier();
-        // T = q P + r: runs 0..r-1 take q+1 tiles, the rest q
+        // the runs' cut of the T tiles (make_split; runs past the used ones are empty)
         const uint32_t T = cum[batch];
         ts = make_split(T, P);
         F0 = w < P ? ts.first(w) : T;
