@@ -306,10 +306,12 @@ def main():
 
 
 
-def graph_time_us(fn, iters=20, per_graph=20, stream=None):
+def graph_time_us(fn, iters=20, per_graph=20, stream=None, warm_s=0.05):
     """Capture per_graph back-to-back calls fn(stream) in one graph, replay it
-    iters times between two events on the capture stream; mean microseconds
-    per call (graph launch cost amortised over per_graph calls)."""
+    for warm_s seconds (the compute clock settles under sustained load: short
+    runs of the MFMA-bound prefill measured up to 18 % slower), then iters
+    times between two events on the capture stream; mean microseconds per
+    call (graph launch cost amortised over per_graph calls)."""
     import torch
     s = stream or torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -321,8 +323,14 @@ def graph_time_us(fn, iters=20, per_graph=20, stream=None):
             for _ in range(per_graph):
                 fn(s)
     torch.cuda.synchronize()
+    t_end = time.perf_counter() + warm_s
+    while True:
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() >= t_end:
+            break
     with torch.cuda.stream(s):
-        g.replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(s)
         for _ in range(iters):
