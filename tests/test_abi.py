@@ -31,6 +31,15 @@ def test_library_exports_every_declared_symbol():
     assert declared_symbols() == set(_lib.EXPORTED)
 
 
+def test_rust_binding_declares_every_entry_point():
+    """The integration guide's complete extern block names exactly the
+    functions the headers declare (the Rust side a maintainer would add)."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text[text.index("## Appendix: the complete `extern \"C\"` block"):]
+    declared_in_rust = set(re.findall(r"pub fn (eh_\w+)\(", block))
+    assert declared_in_rust == declared_symbols()
+
+
 def test_code_objects_contain_launched_kernels():
     kv = open(os.path.join(_lib.LIB_DIR, "paged_kv.hsaco"), "rb").read()
     for ch in (16, 8, 4, 2):
