@@ -685,3 +685,56 @@ def test_scheduled_tables_shorter_than_lengths(dev):
     ref = orc.sdpa_decode_batched(pool_f32, tab, np.minimum(lens, 32).astype(np.uint32), bt,
                                   q.cpu().numpy(), n_head, n_kv, hd)
     check_close(out.cpu().numpy(), ref, what="scheduled, short tables")
+
+
+def _random_sched_case(seed):
+    """One seeded random shape of the scheduled fused step: 16-bit pages,
+    1/2/4/8 kv heads, 1-8 q heads per kv head, pages of 16/32/64 tokens,
+    1-24 sequences whose positions mix zeros, page boundaries and long
+    contexts, and a planner or forced grid."""
+    rng = np.random.default_rng(10_000 + seed)
+    dtype = (KvDataType.F16, KvDataType.BF16)[int(rng.integers(2))]
+    n_kv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 3, 4, 6, 7, 8]))
+    bt = int(rng.choice([16, 32, 64]))
+    B = int(rng.integers(1, 25))
+    kind = rng.integers(0, 3, B)
+    pos = np.where(kind == 0, rng.integers(0, 40, B),
+                   np.where(kind == 1, rng.integers(40, 1500, B),
+                            rng.choice([0, bt - 1, bt, 2 * bt - 1, 2 * bt], B)))
+    grid = None if rng.integers(2) else int(rng.choice([1, 2, 7, 64, 333]))
+    return dtype, (g * n_kv, n_kv, 128, bt), pos.astype(np.int64), grid
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_scheduled_step_random_sweep(dev, seed):
+    """The bench's path on random shapes: one schedule, one fused append +
+    decode launch.  Pool bytes equal the batched append kernel's, bit for
+    bit; outputs match sdpa_decode on the appended pool."""
+    dtype, shape, pos, grid = _random_sched_case(seed)
+    n_head, n_kv, hd, bt = shape
+    B = len(pos)
+    print(f"[sweep {seed}] {dtype.name} heads {n_head}/{n_kv} page {bt} B {B} grid {grid} "
+          f"max pos {int(pos.max())}", flush=True)
+    pa = PagedAttention(0)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, dtype)
+    assert plan[0] == 0
+    if grid is not None:
+        plan = (0, grid, plan[2])
+    tab, nb, pool, k, v, q = sched_case(dev, shape, pos, 20_000 + seed, dtype)
+    layout = PagedKvLayout(nb, bt, n_kv * hd, dtype)
+    dtab, dpos = i32(tab, dev), i32(pos, dev)
+    sched = PagedAttention.schedule_buffer(B, tab.shape[1], bt, plan)
+    pa.build_schedule(None, layout, dtab, dpos, 1, plan, sched)
+    ws = PagedAttention.workspace(plan)
+    pool_ref = pool.clone()
+    cu = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    PagedKvGpu(0).append_kv_batched(None, layout, pool_ref, k, v, dtab, cu, dpos, B)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    pa.append_decode_scheduled(None, layout, pool, k, v, sched, tab.shape[1], q, out, n_head, hd,
+                               plan, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.view(torch.int16), pool_ref.view(torch.int16))
+    ref = orc.sdpa_decode_batched(pool.float().cpu().numpy(), tab, pos.astype(np.uint32) + 1, bt,
+                                  q.cpu().numpy(), n_head, n_kv, hd)
+    check_close(out.cpu().numpy(), ref, what=f"scheduled sweep {seed}")
