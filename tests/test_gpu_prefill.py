@@ -336,3 +336,53 @@ def test_e4m3_prefill_rejects_other_entries(dev):
     with pytest.raises(HipError):
         FlashAttention2(0).launch_batched(None, q, pool, tab, cu, st, out, 8, 2, 128, 16, 4,
                                           kv_dtype=KvDataType.FP8)
+
+
+def _random_prefill_case(seed):
+    """One seeded random batched prefill: f32/f16/bf16 pages, head_dim 64 or
+    128, 1/2/4/8 kv heads with 1-8 q heads each (at most 16 q heads, so the
+    oracle stays fast), pages of 16/32/64 tokens, 1-4 sequences with chunks of
+    1-200 tokens on contexts of 0-800."""
+    rng = np.random.default_rng(30_000 + seed)
+    dtype = (KvDataType.F32, KvDataType.F16, KvDataType.BF16)[int(rng.integers(3))]
+    hd = int(rng.choice([64, 128]))
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([g for g in (1, 2, 3, 4, 7, 8) if g * nkv <= 16]))
+    bt = int(rng.choice([16, 32, 64]))
+    B = int(rng.integers(1, 5))
+    starts = rng.choice([0, 0, bt - 1, bt, int(rng.integers(1, 800))], B).astype(np.int64)
+    lens = rng.integers(1, 201, B).astype(np.int64)
+    return dtype, (g * nkv, nkv, hd, bt), starts, lens
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_random_sweep(dev, seed):
+    """The batched prefill on random shapes against the oracle's causal
+    prefill, sequence by sequence."""
+    dtype, (nh, nkv, hd, bt), starts, lens = _random_prefill_case(seed)
+    print(f"[prefill sweep {seed}] {dtype.name} heads {nh}/{nkv} hd {hd} page {bt} "
+          f"starts {starts.tolist()} lens {lens.tolist()}", flush=True)
+    rng = np.random.default_rng(40_000 + seed)
+    pages = [-(-(int(s) + int(n)) // bt) for s, n in zip(starts, lens)]
+    stride = max(pages) + 1
+    n_pages = sum(pages) + 2
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    tables = np.full((len(starts), stride), 0xFFFFFFFF, np.uint32)
+    o = 0
+    for b, k in enumerate(pages):
+        tables[b, :k] = perm[o:o + k]
+        o += k
+    dpool, hpool = make_pool(rng, n_pages, bt, nkv, hd, dtype, dev)
+    total = int(lens.sum())
+    q = rng.standard_normal((total, nh, hd)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    out = torch.full((total, nh, hd), float("nan"), device=dev)
+    FlashAttention2(0).launch_batched(None, torch.from_numpy(q).to(dev), dpool, i32(tables, dev),
+                                      i32(cu, dev), i32(starts.astype(np.uint32), dev), out,
+                                      nh, nkv, hd, bt, int(lens.max()), kv_dtype=dtype)
+    torch.cuda.synchronize()
+    g = out.cpu().numpy()
+    for b, (s, n) in enumerate(zip(starts, lens)):
+        ref = orc.prefill_causal(hpool, tables[b, :pages[b]], bt, q[cu[b]:cu[b + 1]], int(n),
+                                 int(s), nh, nkv, hd)
+        check_close(g[cu[b]:cu[b + 1]], ref, dtype, f"prefill sweep {seed} seq {b}")
