@@ -505,3 +505,50 @@ def test_e4m3_fused_step_errors(dev):
                                       ws, None, None)
     with pytest.raises(HipError):       # FP8 pools only through the scale-aware fused step
         pa.append_decode_batched(None, lay, pool, keys, keys, tab, pos, q, out, 12, hd, plan, ws)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_e4m3_scheduled_step_random_sweep(dev, seed):
+    """The scheduled E4M3 step (quantising append + decode in one launch, the
+    split read from a step schedule) on random shapes: 1/2/4/8 kv heads with
+    1-8 q heads each, pages of 16/32/64 tokens, 1-24 sequences mixing zeros,
+    page boundaries and long contexts.  The pool equals the quantising
+    append's bit for bit; outputs match sdpa_decode on the dequantised pool."""
+    rng = np.random.default_rng(50_000 + seed)
+    n_kv = int(rng.choice([1, 2, 4, 8]))
+    n_head = n_kv * int(rng.choice([1, 2, 3, 4, 6, 7, 8]))
+    hd, bt = 128, int(rng.choice([16, 32, 64]))
+    B = int(rng.integers(1, 25))
+    kind = rng.integers(0, 3, B)
+    pos = np.where(kind == 0, rng.integers(0, 40, B),
+                   np.where(kind == 1, rng.integers(40, 1500, B),
+                            rng.choice([0, bt - 1, bt, 2 * bt - 1], B))).astype(np.uint32)
+    print(f"[e4m3 sweep {seed}] heads {n_head}/{n_kv} page {bt} B {B} max pos {int(pos.max())}",
+          flush=True)
+    rl = n_kv * hd
+    tab, nb = make_tables(rng, pos + 1, bt)
+    codes, ks, vs = gauss_codes(rng, nb, bt, n_kv, hd)
+    newk = rng.standard_normal((B, rl)).astype(np.float32)
+    newv = rng.standard_normal((B, rl)).astype(np.float32)
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, KvDataType.FP8)
+    assert plan[0] == 0
+    lay = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    dks, dvs, dtab, dpos = t(ks), t(vs), i32(tab, dev), i32(pos, dev)
+    pool_a = t(codes.copy())
+    PagedKvGpu(0).append_kv_e4m3_batched(None, lay, pool_a, t(newk), t(newv), dtab,
+                                         i32(np.arange(B + 1), dev), dpos, B, hd, dks, dvs)
+    pa = PagedAttention(0)
+    sched = PagedAttention.schedule_buffer(B, tab.shape[1], bt, plan)
+    pa.build_schedule(None, lay, dtab, dpos, 1, plan, sched)
+    pool_b = t(codes.copy())
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    pa.append_decode_scheduled(None, lay, pool_b, t(newk), t(newv), sched, tab.shape[1], t(q), out,
+                               n_head, hd, plan, PagedAttention.workspace(plan), dks, dvs)
+    torch.cuda.synchronize()
+    pa_np, pb_np = pool_a.cpu().numpy(), pool_b.cpu().numpy()
+    assert np.array_equal(pa_np, pb_np), np.argwhere(pa_np != pb_np)[:4]
+    ref = orc.sdpa_decode_batched(dequant_pool(pb_np, nb, bt, n_kv, hd, ks, vs), tab, pos + 1, bt,
+                                  q, n_head, n_kv, hd)
+    check_close(out.cpu().numpy(), ref)
