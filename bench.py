@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
-    p.add_argument("--roofline-iters", type=int, default=10)
+    p.add_argument("--roofline-iters", type=int, default=20)
     p.add_argument("--fuse", type=int, default=1,
                    help="one fused append+decode launch per layer when the balanced kernel applies")
     p.add_argument("--sched", type=int, default=1,
@@ -54,8 +54,9 @@ def parse():
                         "(1, 3, 4, 5) and append/gather, one JSON line each")
     p.add_argument("--c5-pool-frac", type=float, default=0.9,
                    help="config 5 pool size as a fraction of free HBM")
-    p.add_argument("--parts", default="c1,append,e4m3,c3,c4,c5",
-                   help="suite parts to run (comma list of c1, append, e4m3, c3, c4, c5)")
+    p.add_argument("--parts", default="c1,append,e4m3,ceiling,c3,c4,c5",
+                   help="suite parts to run (comma list of c1, append, e4m3, ceiling, c3, c4, "
+                        "c5)")
     return p.parse_args()
 
 
@@ -96,6 +97,7 @@ def start_cpu_baseline(args):
     cmd = ([taskset, "-c", str(cpu)] + cmd) if taskset else cmd
     env = dict(os.environ, HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="",
                ROCR_VISIBLE_DEVICES="", TITAN_CPU_PIN=str(cpu),
+               TITAN_CPU_AVAIL=str(len(os.sched_getaffinity(0))),
                TITAN_CPU_PINNER="taskset" if taskset else "sched_setaffinity")
     return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
                             env=env)
@@ -210,15 +212,18 @@ def main():
 
     ctx_before = int(start.sum().item())
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # one event between consecutive steps: the first-to-last interval is the
+    # timed region, the consecutive pairs give per-step times for the median
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
+    ev[0].record()
+    for k in range(args.steps):
         runner()
-    e1.record()
+        ev[k + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = e0.elapsed_time(e1)
+    gpu_ms = ev[0].elapsed_time(ev[-1])
+    step_ms = [ev[k].elapsed_time(ev[k + 1]) for k in range(args.steps)]
     elapsed = max(gpu_ms / 1e3, 1e-9)
     # KV bytes the decode reads: every attended row once per kv head (K and V).
     kv_bytes = 0
@@ -254,15 +259,17 @@ def main():
                     pa.decode_batched(dstream, qs[i], pools[i], d_tab, lens, outs[i], NQ, NKV, HD,
                                       BT, KvDataType.F16, plan, ws)
     torch.cuda.synchronize()
-    ra, rb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    rev = [torch.cuda.Event(enable_timing=True) for _ in range(args.roofline_iters + 1)]
     with torch.cuda.stream(dstream):  # replay() launches on the current stream
         dgraph.replay()  # warm
-        ra.record(dstream)
-        for _ in range(args.roofline_iters):
+        rev[0].record(dstream)
+        for k in range(args.roofline_iters):
             dgraph.replay()
-        rb.record(dstream)
+            rev[k + 1].record(dstream)
     torch.cuda.synchronize()
-    avg_ms = ra.elapsed_time(rb) / (args.roofline_iters * L)
+    avg_ms = rev[0].elapsed_time(rev[-1]) / (args.roofline_iters * L)
+    med_ms = float(np.median([rev[k].elapsed_time(rev[k + 1])
+                              for k in range(args.roofline_iters)])) / L
     attended = int(lens.sum().item())
     # KV rows read once per kv head; a fused launch also reads and writes the
     # appended rows (B x 2 rows)
@@ -284,6 +291,10 @@ def main():
                 (kname + (" + eh_decode_tiles_merge" if balanced else " + eh_decode_merge")
                  + (" (fused append)" if fused else "")),
                 "avg_launch_us": round(avg_ms * 1e3, 2),
+                "median_launch_us": round(med_ms * 1e3, 2),
+                "timing": f"HIP events on the graph's stream around each of {args.roofline_iters} "
+                          f"replays of {L} calls (+ one schedule build); avg = total / calls, "
+                          "median over the replays",
                 "algorithmic_bytes_per_launch": per_launch_bytes}
 
     cpu = finish_cpu_baseline(cpu_proc) if cpu_proc is not None else None
@@ -291,6 +302,8 @@ def main():
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(float(np.median(step_ms)), 4),
+        "ms_per_step_min_max": [round(min(step_ms), 4), round(max(step_ms), 4)],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded N(0,1) K/V/Q, seeded U[128,4096] contexts, shuffled free list)",
         "config": {"workload": "config2: batch-32 GQA paged decode step, 12/2 heads, hd 128, "
@@ -487,6 +500,85 @@ def suite(args, dev):
               "GB/s": round(b8 / us8f / 1e3, 1)})
         del pools8
 
+    if "ceiling" in parts:
+        # The read floor of the headline call: config 2's decode (schedule +
+        # fused append + decode, 28 rotated pools as the headline step) and a
+        # pure read of the same pages through the same tables (whole 16 KiB
+        # pages, sequence-major as the decode walks them) over the same 28
+        # pools, each as a graph of 28 calls replayed between events.
+        L = 28
+        lay2 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.F16)
+        pools = [torch.randn(lay2.floats_total(), generator=gen, device=dev, dtype=torch.float16)
+                 for _ in range(L)]
+        pos2 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
+        n_tok = s2.ctx_lens.astype(np.int64) + 1
+        ids = np.concatenate([tab2[b, :(int(n_tok[b]) + 15) // 16] for b in range(32)])
+        dids = torch.from_numpy(ids.astype(np.uint32).view(np.int32)).to(dev)
+        page_b = lay2.page_bytes()
+        plan2 = PagedAttention.plan(32, 12, 2, 128, 16, int(n_tok.max()))
+        ws2 = PagedAttention.workspace(plan2)
+        stride2 = int(tab2.shape[1])
+        sched2 = PagedAttention.schedule_buffer(32, stride2, 16, plan2)
+        q2 = torch.randn((32, 12, 128), generator=gen, device=dev)
+        o2 = torch.empty_like(q2)
+        nk2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
+        nv2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
+        xo = torch.empty(1024 * 8, dtype=torch.int32, device=dev)
+        dec_bytes = int(n_tok.sum()) * 2 * 128 * 2 * 2 + 2 * 32 * 2 * s2.row_len * 2
+
+        def graph_us(call, reps=20):
+            """µs per call: 28 calls (one per pool) in one graph, median of
+            `reps` replays after 50 ms of warm replays."""
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.current_stream())
+            call(None, pools[0])
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(st):
+                with torch.cuda.graph(g, stream=st):
+                    for i in range(L):
+                        call(st, pools[i])
+            torch.cuda.synchronize()
+            t_end = time.perf_counter() + 0.05
+            while time.perf_counter() < t_end:
+                with torch.cuda.stream(st):
+                    g.replay()
+                torch.cuda.synchronize()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+            with torch.cuda.stream(st):
+                ev[0].record(st)
+                for k in range(reps):
+                    g.replay()
+                    ev[k + 1].record(st)
+            torch.cuda.synchronize()
+            return float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)])) * 1e3 / L
+
+        pa.build_schedule(None, lay2, dtab2, pos2, 1, plan2, sched2)
+        us_dec = graph_us(lambda st, p: pa.append_decode_scheduled(
+            st, lay2, p, nk2, nv2, sched2, stride2, q2, o2, 12, 128, plan2, ws2))
+        best = None
+        sweep = {}
+        for depth in (1, 2):
+            for grid in (256, 512, 1024):
+                us = graph_us(lambda st, p: kv.stream_pages(st, lay2, p, dids, xo, depth, grid))
+                sweep[f"d{depth}_g{grid}"] = round(us, 2)
+                if best is None or us < best[0]:
+                    best = (us, depth, grid)
+        st_bytes = len(ids) * page_b
+        emit({"config": 2, "what": "read ceiling: the decode's pages (whole 16 KiB pages through "
+              "the same tables, sequence-major) streamed once per call by eh_stream_pages, 28 "
+              "rotated pools as the headline step; the decode call (schedule + fused append + "
+              "decode) timed the same way in the same process",
+              "pages": int(len(ids)), "stream_bytes": st_bytes, "decode_bytes": dec_bytes,
+              "ceiling_us": round(best[0], 2), "ceiling_depth": best[1], "ceiling_grid": best[2],
+              "ceiling_GB/s": round(st_bytes / best[0] / 1e3, 1),
+              "ceiling_frac_of_8TB/s": round(st_bytes / best[0] / 1e3 / 8000.0, 4),
+              "sweep_us": sweep, "decode_us": round(us_dec, 2),
+              "decode_GB/s": round(dec_bytes / us_dec / 1e3, 1),
+              "decode_frac_of_8TB/s": round(dec_bytes / us_dec / 1e3 / 8000.0, 4),
+              "decode_frac_of_ceiling": round((dec_bytes / us_dec) / (st_bytes / best[0]), 4)})
+        del pools
+
     if "c3" in parts:  # bf16 chunked prefill, B=8, 512 new tokens on 2048 cached, 32/8 heads
         s3 = synth.config3(0)
         tab3 = synth.block_tables(s3, extra_tokens=512)
@@ -559,12 +651,21 @@ def suite(args, dev):
         tab5 = synth.block_tables(s5, extra_tokens=1)
         lay5 = PagedKvLayout(s5.n_blocks, 16, s5.row_len, KvDataType.F16)
         pool5 = torch.empty(lay5.floats_total(), device=dev, dtype=torch.float16)
-        # fill only the pages the tables use (values do not change the timing)
-        used = torch.from_numpy(tab5[tab5 != 0xFFFFFFFF].astype(np.int64)).to(dev)
-        pg = pool5.view(s5.n_blocks, -1)
-        pg[used] = torch.randn((used.numel(), pg.shape[1]), generator=gen, device=dev,
-                               dtype=torch.float16)
+        # only the pages the tables use are filled (values do not change the
+        # timing): N(0,1), with 1 % of the K rows scaled by 8 (the
+        # configuration's softmax-range stress)
+        ids5 = tab5.reshape(-1)                    # every entry is used: 2049 pages a sequence
+        assert (ids5 != 0xFFFFFFFF).all()
+        used = torch.from_numpy(ids5.astype(np.int64)).to(dev)
+        pg = pool5.view(s5.n_blocks, 16, 2, s5.row_len)
+        vals = torch.randn((used.numel(), 16, 2, s5.row_len), generator=gen, device=dev,
+                           dtype=torch.float16)
+        hot = torch.rand((used.numel(), 16), generator=gen, device=dev) < 0.01
+        vals[:, :, 0][hot] *= 8
+        pg[used] = vals
+        del vals
         dtab5 = torch.from_numpy(tab5.view(np.int32)).to(dev)
+        dids5 = torch.from_numpy(ids5.view(np.int32)).to(dev)
         q5 = torch.randn((4, 32, 128), generator=gen, device=dev)
         o5 = torch.empty_like(q5)
         nk5 = torch.randn((4, s5.row_len), generator=gen, device=dev, dtype=torch.float16)
@@ -579,14 +680,10 @@ def suite(args, dev):
         # (memset) would leave dirty lines whose write-back competes with the timed reads
         flush = torch.ones(1024 * 1024 * 1024 // 4, device=dev)
         stream = torch.cuda.Stream()
+        xo5 = torch.empty(1024 * 8, dtype=torch.int32, device=dev)
         b5 = 4 * 32769 * 8 * 128 * 2 * 2
-        for label, call in (
-                ("fused append + decode (self-scheduled)",
-                 lambda: pa.append_decode_batched(stream, lay5, pool5, nk5, nv5, dtab5, st5, q5,
-                                                  o5, 32, 128, plan5, ws5)),
-                ("fused append + decode from a step schedule",
-                 lambda: pa.append_decode_scheduled(stream, lay5, pool5, nk5, nv5, sched5,
-                                                    stride5, q5, o5, 32, 128, plan5, ws5))):
+
+        def cold_us(call):
             times = []
             with torch.cuda.stream(stream):
                 for it in range(12):
@@ -598,14 +695,74 @@ def suite(args, dev):
                     torch.cuda.synchronize()
                     if it >= 2:
                         times.append(a.elapsed_time(b) * 1e3)
-            us5 = float(np.median(times))
-            emit({"config": 5, "what": f"{label}, B=4 x 32768 ctx, 32/8 heads, hd 128, f16, pool "
-                  f"{lay5.bytes_total() / 1e9:.0f} GB ({s5.n_blocks} pages, scattered), MALL "
-                  "evicted (1 GiB read) before each timed call", "latency_us": round(us5, 2),
-                  "kv_bytes": b5, "GB/s": round(b5 / us5 / 1e3, 1),
+            return float(np.median(times))
+
+        sweep = {}
+        for depth in (1, 2):
+            for grid in (256, 512, 1024):
+                sweep[f"d{depth}_g{grid}"] = round(cold_us(
+                    lambda: kv.stream_pages(stream, lay5, pool5, dids5, xo5, depth, grid)), 2)
+        c_key = min(sweep, key=sweep.get)
+        c_us = sweep[c_key]
+        c_bytes = int(ids5.size) * lay5.page_bytes()
+        emit({"config": 5, "what": "read ceiling: the 8196 used 64 KiB pages streamed once by "
+              "eh_stream_pages through the same tables, MALL evicted (1 GiB read) before each "
+              "timed call", "stream_bytes": c_bytes, "ceiling_us": c_us, "best": c_key,
+              "sweep_us": sweep, "ceiling_GB/s": round(c_bytes / c_us / 1e3, 1),
+              "ceiling_frac_of_8TB/s": round(c_bytes / c_us / 1e3 / 8000.0, 4)})
+        for label, call in (
+                ("fused append + decode (self-scheduled)",
+                 lambda: pa.append_decode_batched(stream, lay5, pool5, nk5, nv5, dtab5, st5, q5,
+                                                  o5, 32, 128, plan5, ws5)),
+                ("fused append + decode from a step schedule",
+                 lambda: pa.append_decode_scheduled(stream, lay5, pool5, nk5, nv5, sched5,
+                                                    stride5, q5, o5, 32, 128, plan5, ws5))):
+            o5.fill_(float("nan"))
+            us5 = cold_us(call)
+            # every timed call rewrote the same rows at position 32768 and
+            # attended the same 32769 tokens: the appended rows bit for bit and
+            # the last call's output against a float64 numpy attention over a
+            # compacted host copy of the used pages (the oracle itself stays
+            # in tests/, where the same check runs at this pool size)
+            host = pg[used].cpu().numpy().reshape(4, 2049 * 16, 2, 8, 128)
+            app_ok = all(np.array_equal(host[b, 32768, 0].reshape(-1).view(np.uint16),
+                                        nk5[b].cpu().numpy().view(np.uint16)) and
+                         np.array_equal(host[b, 32768, 1].reshape(-1).view(np.uint16),
+                                        nv5[b].cpu().numpy().view(np.uint16)) for b in range(4))
+            ref = np_decode_f64(host[:, :32769], q5.cpu().numpy())
+            del host
+            d = np.abs(o5.cpu().numpy().astype(np.float64) - ref)
+            ok = bool(np.isfinite(d).all() and d.max() <= 2e-3 and
+                      (d <= 2e-3 + 1e-3 * np.abs(ref)).all())
+            emit({"config": 5, "what": f"{label}, B=4 x 32768 ctx, 32/8 heads, hd 128, f16, 1 % "
+                  f"of K rows x 8, pool {lay5.bytes_total() / 1e9:.0f} GB ({s5.n_blocks} pages, "
+                  "scattered), MALL evicted (1 GiB read) before each timed call",
+                  "latency_us": round(us5, 2), "kv_bytes": b5, "GB/s": round(b5 / us5 / 1e3, 1),
                   "frac_of_8TB/s": round(b5 / us5 / 1e3 / 8000.0, 4),
+                  "frac_of_ceiling": round((b5 / us5) / (c_bytes / c_us), 4),
+                  "check_vs_numpy_f64": {"max_abs": float(d.max()), "within_bar": ok,
+                                         "appended_rows_bit_exact": bool(app_ok)},
                   "kernel": PagedAttention.kernel_name(32, 8, 128, 16, KvDataType.F16)})
         del pool5, flush
+
+
+def np_decode_f64(kv, q):
+    """Float64 decode attention by numpy: kv [B, T, 2, n_kv, hd] (K then V of
+    every attended token), q [B, n_head, hd]; q head h reads kv head
+    h // (n_head / n_kv); scale 1 / sqrt(hd)."""
+    import numpy as np
+    B, T, _, n_kv, hd = kv.shape
+    n_head = q.shape[1]
+    grp = n_head // n_kv
+    out = np.empty(q.shape, np.float64)
+    for b in range(B):
+        for h in range(n_kv):
+            k = kv[b, :, 0, h].astype(np.float64)
+            v = kv[b, :, 1, h].astype(np.float64)
+            s = k @ q[b, h * grp:(h + 1) * grp].astype(np.float64).T / np.sqrt(hd)
+            w = np.exp(s - s.max(axis=0))
+            out[b, h * grp:(h + 1) * grp] = (w.T @ v) / w.sum(axis=0)[:, None]
+    return out
 
 
 def cpu_child(args):
@@ -654,12 +811,13 @@ def cpu_child(args):
     pin = os.environ.get("TITAN_CPU_PIN", "?")
     print(json.dumps({
         "value": round(kv_bytes / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+        "host_logical_cpus": os.cpu_count(),
         "sample": f"config 2 layer-steps (32 sequences, {int((lens + 1).sum())} attended tokens: "
                   f"append + sdpa_decode over the f32-widened pool), median of {len(times)} "
                   f"({total:.1f} s), 1 thread pinned to CPU {pin} "
-                  f"({os.environ.get('TITAN_CPU_PINNER', '?')}) of {cpu_model()}, "
-                  f"{len(os.sched_getaffinity(0))} CPU(s) in the child's mask; the reference "
-                  f"path is single-threaded",
+                  f"({os.environ.get('TITAN_CPU_PINNER', '?')}) of {cpu_model()}: 1 of "
+                  f"{os.cpu_count()} logical CPUs on the host ({os.environ.get('TITAN_CPU_AVAIL', '?')} "
+                  f"in the benchmark's affinity mask); the reference path is single-threaded",
         "median_layer_step_ms": round(med * 1e3, 2),
         "median_step_ms_28_layers": round(med * 28e3, 1),
         "tok_s": round(B / (28 * med), 3)}), flush=True)

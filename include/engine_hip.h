@@ -390,9 +390,14 @@ eh_status eh_decode_schedule(eh_context* ctx, eh_stream stream, const eh_kv_layo
  * eh_paged_decode_batched / eh_paged_decode_batched_e4m3).  E4M3 pages take
  * f32 rows and both scales.  layout, bt_stride, batch and grid must be those
  * the schedule was built with; the pool may differ per layer (same layout).
- * Outputs equal the self-scheduled forms'; workspace as eh_decode_plan.  A
- * schedule built for other values is not detected: the kernels still stay
- * inside the pool, q, out and the workspace, but the results are unspecified. */
+ * Outputs equal the self-scheduled forms'; workspace as eh_decode_plan.  The
+ * schedule and the workspace must be 16-byte aligned (EH_INVALID_ARGS).
+ * keys/values with a schedule built with lens_add = 0 are not appended (the
+ * schedule's last tiles hold existing tokens, which the append would
+ * overwrite): the pool is left unchanged and q attends the schedule's
+ * tokens.  A schedule built for other shapes is not detected: the kernels
+ * still stay inside the pool, q, out and the workspace, but the results are
+ * unspecified. */
 eh_status eh_append_decode_scheduled(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
                                      void* pool, uint64_t pool_bytes, const void* keys,
                                      uint64_t keys_bytes, const void* values,
@@ -402,6 +407,20 @@ eh_status eh_append_decode_scheduled(eh_context* ctx, eh_stream stream, const eh
                                      uint64_t out_bytes, uint32_t n_head, uint32_t head_dim,
                                      uint32_t grid, void* workspace, uint64_t workspace_bytes,
                                      const float* k_scale, const float* v_scale);
+
+/* ---- Measurement aid (no counterpart in the reference): the read ceiling
+ * of a paged decode.  Streams the n_ids pages listed in ids (page ids of the
+ * pool described by layout; page bytes a multiple of 16 KiB) once, in list
+ * order, with grid workgroups of 8 waves, each wave taking an equal
+ * contiguous share of the pages' 16 KiB items and keeping depth (1 or 2)
+ * items in flight; every word read is folded into one xor per wave, written
+ * to out[grid * 8] (4 bytes per wave, nothing else is written).  Timing it
+ * over a decode's page list gives the cold-read floor the decode is
+ * measured against.  Ids past the pool are skipped. */
+eh_status eh_stream_pages(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                          const void* pool, uint64_t pool_bytes, const uint32_t* ids,
+                          uint64_t ids_bytes, uint32_t n_ids, uint32_t depth, uint32_t grid,
+                          uint32_t* out, uint64_t out_bytes);
 
 /* ---- eh_append_decode_batched without a workspace argument, for callers
  * that cannot allocate device memory (code under HIP graph capture, tight

@@ -16,7 +16,8 @@ import pytest
 import torch
 
 from oracle import orc
-from titan_amd import KvDataType, PagedAttention, PagedKvGpu, PagedKvLayout
+from titan_amd import HipError, KvDataType, PagedAttention, PagedKvGpu, PagedKvLayout
+from titan_amd.errors import KvCacheError
 from titan_amd import synth
 
 import parity
@@ -165,6 +166,38 @@ def test_tiles_workspace_reuse(dev):
         check_close(out.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("kstd", [4.0, 16.0, 64.0])
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
+@pytest.mark.parametrize("shape", [(12, 2, 128, 16), (8, 2, 64, 16)],
+                         ids=["balanced-hd128", "slots-hd64"])
+def test_decode_large_keys_within_f16_range(dev, dtype, kstd, shape):
+    """K of standard deviation 4-64 (inside f16's range) with N(0,1) q and V,
+    under the strict bar, through the balanced MFMA kernel (hd 128) and the
+    fixed-split dot2 kernel (hd 64).  With f16 operands the q lo halves
+    (~2^-11 of q) and the small weights fall into f16's subnormal range,
+    which the MFMA / dot2 operands do not keep: q is scaled by a power of two
+    first and P carries 2^7, else the error grows with |K|."""
+    n_head, n_kv, hd, bt = shape
+    rng = np.random.default_rng(600 + int(kstd) + 10 * int(dtype) + hd)
+    lens = np.array([2900, 1, 700, 16, 1500, 33], np.int64)
+    tab, nb = make_tables(rng, lens, bt)
+    host = rng.standard_normal((nb, bt, 2, n_kv * hd)).astype(np.float32)
+    host[:, :, 0] *= np.float32(kstd)
+    t = torch.from_numpy(host.reshape(-1)).to(TD[dtype])
+    pool, pool_f32 = t.to(dev), t.to(torch.float32).numpy()
+    B = len(lens)
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(lens.max()), 0, dtype)
+    assert (plan[0] == 0) == (hd == 128)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                     i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, plan,
+                                     PagedAttention.workspace(plan))
+    torch.cuda.synchronize()
+    ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
+    check_close(out.cpu().numpy(), ref, f"{dtype.name} K std {kstd:g} hd {hd}")
+
+
 def fused_case(dev, dtype, starts, shape, seed, grid=None):
     n_head, n_kv, hd, bt = shape
     rl = n_kv * hd
@@ -310,6 +343,55 @@ def test_fused_config2_one_layer_full_size(dev):
     ref = orc.sdpa_decode_batched(pool_f32, tab, (s.ctx_lens + 1).astype(np.uint32), 16, q, 12, 2,
                                   128)
     check_close(out.cpu().numpy(), ref)
+
+
+def test_scheduled_config2_full_size_bench_path(dev):
+    """The benchmark's timed path at full size: config 2 (32 sequences, ctx
+    U[128,4096], 12/2 heads, hd 128, page 16, f16), one step schedule built
+    from the device positions (eh_decode_schedule, lens_add 1), then two
+    layers with their own pools sharing it (eh_append_decode_scheduled), for
+    two steps as positions grow by one.  Every layer's output against
+    sdpa_decode_batched on the pool holding the appended rows; the pool
+    bytes bit for bit against the oracle's appended pool."""
+    s = synth.config2(0, extra_tokens=2)
+    rng = np.random.default_rng(21)
+    tab = synth.block_tables(s, extra_tokens=2)
+    stride = int(tab.shape[1])
+    layout = PagedKvLayout(s.n_blocks, 16, s.row_len, KvDataType.F16)
+    plan = PagedAttention.plan(32, 12, 2, 128, 16, int(s.ctx_lens.max()) + 2)
+    assert plan[0] == 0
+    ws = PagedAttention.workspace(plan)
+    sched = PagedAttention.schedule_buffer(32, stride, 16, plan)
+    pa = PagedAttention(0)
+    layers = []
+    for _ in range(2):
+        host = rng.standard_normal(s.n_blocks * 16 * 2 * s.row_len).astype(np.float16)
+        layers.append({"pool": torch.from_numpy(host).to(dev), "ref": host.copy()})
+    dtab = i32(tab, dev)
+    pos = torch.from_numpy(s.ctx_lens.astype(np.int32)).to(dev)
+    for step in range(2):
+        L_now = s.ctx_lens.astype(np.int64) + step
+        pa.build_schedule(None, layout, dtab, pos, 1, plan, sched)
+        for li, lay in enumerate(layers):
+            nk = rng.standard_normal((32, s.row_len)).astype(np.float16)
+            nv = rng.standard_normal((32, s.row_len)).astype(np.float16)
+            q = rng.standard_normal((32, 12, 128)).astype(np.float32)
+            out = torch.full((32, 12, 128), float("nan"), device=dev)
+            pa.append_decode_scheduled(None, layout, lay["pool"], torch.from_numpy(nk).to(dev),
+                                       torch.from_numpy(nv).to(dev), sched, stride,
+                                       torch.from_numpy(q).to(dev), out, 12, 128, plan, ws)
+            torch.cuda.synchronize()
+            p = lay["ref"].reshape(-1, 16, 2, s.row_len)
+            for b in range(32):
+                p[tab[b, L_now[b] // 16], L_now[b] % 16, 0] = nk[b]
+                p[tab[b, L_now[b] // 16], L_now[b] % 16, 1] = nv[b]
+            got = lay["pool"].cpu().numpy()
+            assert np.array_equal(got.view(np.uint16), lay["ref"].view(np.uint16)), \
+                f"step {step} layer {li}: pool bytes"
+            ref = orc.sdpa_decode_batched(lay["ref"].astype(np.float32), tab,
+                                          (L_now + 1).astype(np.uint32), 16, q, 12, 2, 128)
+            check_close(out.cpu().numpy(), ref, f"bench path step {step} layer {li}")
+        pos.add_(1)
 
 
 def test_fused_graph_replay_growing_positions(dev):
@@ -463,6 +545,66 @@ def test_config5_full_size_offsets_past_4gib(dev):
     check_close(out1.cpu().numpy(), ref[2].ravel(), what="config5 flash_decoding seq 2")
 
 
+def test_config5_stated_pool_scheduled(dev):
+    """Benchmark config 5 on its stated pool, as the benchmark times it: a
+    pool of 90 % of free HBM (about 4.2 M pages of 64 KiB on a 288 GB
+    device), 4 sequences of 32768 cached tokens on pages drawn by the seeded
+    permutation over the whole pool (byte offsets up to ~2^38), 1 % of K rows
+    x8; one step schedule, then the fused append of token 32768 + decode
+    (eh_append_decode_scheduled).  The appended rows bit for bit and the
+    output against the oracle on a compacted host copy of the used pages."""
+    torch.cuda.empty_cache()
+    free, _ = torch.cuda.mem_get_info()
+    page_bytes = 16 * 2 * 1024 * 2
+    s = synth.config5(0, n_blocks=int(0.9 * free) // page_bytes)
+    tab = synth.block_tables(s, extra_tokens=1)
+    B, stride = tab.shape
+    assert (B, stride) == (4, 2049) and (tab != NONE).all()
+    print(f"[c5 pool] {s.n_blocks} pages ({s.n_blocks * page_bytes / 1e9:.0f} GB), "
+          f"largest id {int(tab.max())}", flush=True)
+    rng = np.random.default_rng(5005)
+    host = rng.standard_normal((B * stride, 16, 2, 1024), dtype=np.float32).astype(np.float16)
+    hot = rng.random((B * stride, 16)) < 0.01
+    host[:, :, 0][hot] *= np.float16(8)
+    layout = PagedKvLayout(s.n_blocks, 16, 1024, KvDataType.F16)
+    pool = torch.empty(layout.floats_total(), dtype=torch.float16, device=dev)
+    try:
+        pages = pool.view(s.n_blocks, 16, 2, 1024)
+        d_ids = torch.from_numpy(tab.reshape(-1).astype(np.int64)).to(dev)
+        pages[d_ids] = torch.from_numpy(host).to(dev)
+        newk = rng.standard_normal((B, 1024)).astype(np.float16)
+        newv = rng.standard_normal((B, 1024)).astype(np.float16)
+        q = rng.standard_normal((B, 32, 128)).astype(np.float32)
+        plan = PagedAttention.plan(B, 32, 8, 128, 16, 32769)
+        assert plan[0] == 0
+        sched = PagedAttention.schedule_buffer(B, stride, 16, plan)
+        dtab = i32(tab, dev)
+        pa = PagedAttention(0)
+        pa.build_schedule(None, layout, dtab, i32(s.ctx_lens, dev), 1, plan, sched)
+        out = torch.full((B, 32, 128), float("nan"), device=dev)
+        print("[c5 pool] scheduled fused append + decode", flush=True)
+        pa.append_decode_scheduled(None, layout, pool, torch.from_numpy(newk).to(dev),
+                                   torch.from_numpy(newv).to(dev), sched, stride,
+                                   torch.from_numpy(q).to(dev), out, 32, 128, plan,
+                                   PagedAttention.workspace(plan))
+        torch.cuda.synchronize()
+        got = pages[d_ids].cpu().numpy()
+    finally:
+        del pool
+        torch.cuda.empty_cache()
+    want = host
+    for b in range(B):
+        want[(b + 1) * stride - 1, 0, 0] = newk[b]
+        want[(b + 1) * stride - 1, 0, 1] = newv[b]
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), "pool bytes"
+    del got
+    print("[c5 pool] oracle", flush=True)
+    ref = orc.sdpa_decode_batched(want.reshape(-1).astype(np.float32),
+                                  np.arange(B * stride, dtype=np.uint32).reshape(B, stride),
+                                  np.full(B, 32769, np.uint32), 16, q, 32, 8, 128)
+    check_close(out.cpu().numpy(), ref, what="config5 stated pool, scheduled")
+
+
 # ---- step schedule (eh_decode_schedule + eh_append_decode_scheduled) ----------
 
 def sched_case(dev, shape, pos, seed, dtype=KvDataType.F16, spare=3):
@@ -529,6 +671,106 @@ def test_scheduled_step_equals_self_scheduled(dev, dtype, shape):
                                   np.asarray(SCHED_POS, np.uint32) + 1, bt, q.cpu().numpy(),
                                   n_head, n_kv, hd)
     check_close(out_b.cpu().numpy(), ref, what="scheduled")
+
+
+def test_scheduled_validation_errors(dev):
+    """eh_decode_schedule and eh_append_decode_scheduled reject, before any
+    launch, with the error kind and the expected / actual values: a schedule
+    buffer below eh_decode_schedule_bytes, a null or misaligned schedule,
+    batch past 2048, grid 0, bt_stride 0, E4M3 pages without scales, a short
+    or misaligned workspace and keys without values."""
+    shape = (12, 2, 128, 16)
+    pos = [40, 7, 100]
+    B = len(pos)
+    tab, nb, pool, k, v, q = sched_case(dev, shape, pos, 90)
+    layout = PagedKvLayout(nb, 16, 256, KvDataType.F16)
+    plan = PagedAttention.plan(B, 12, 2, 128, 16, 101)
+    stride = int(tab.shape[1])
+    need = PagedAttention.schedule_bytes(B, stride, 16, plan)
+    big = torch.zeros(need // 4 + 64, dtype=torch.int32, device=dev)
+    sched = (big.data_ptr(), need)
+    dtab, dpos = i32(tab, dev), i32(np.asarray(pos), dev)
+    ws = PagedAttention.workspace(plan)
+    out = torch.empty((B, 12, 128), device=dev)
+    pa = PagedAttention(0)
+
+    def err(fn, kind, expected=None, actual=None):
+        # InvalidArgs is KvCacheError::InvalidArgs's counterpart, the others CudaError's
+        with pytest.raises(KvCacheError if kind == "InvalidArgs" else HipError) as e:
+            fn()
+        assert e.value.kind == kind, (e.value.kind, getattr(e.value, "site", e.value))
+        if expected is not None:
+            assert (e.value.expected, e.value.actual) == (expected, actual), e.value.site
+
+    build = pa.build_schedule
+    err(lambda: build(None, layout, dtab, dpos, 1, plan, (big.data_ptr(), need - 16)),
+        "InvalidSize", need, need - 16)
+    err(lambda: build(None, layout, dtab, dpos, 1, plan, (0, need)), "InvalidArgs")
+    err(lambda: build(None, layout, dtab, dpos, 1, plan, (big.data_ptr() + 4, need)),
+        "InvalidArgs")
+    err(lambda: build(None, layout, dtab, dpos, 1, (0, 0, plan[2]), sched), "InvalidSize", 1, 0)
+    wide = torch.zeros((2049, 1), dtype=torch.int32, device=dev)
+    err(lambda: build(None, layout, wide, torch.zeros(2049, dtype=torch.int32, device=dev), 1,
+                      plan, sched), "InvalidSize", 2048, 2049)
+    err(lambda: build(None, layout, torch.zeros((B, 0), dtype=torch.int32, device=dev), dpos, 1,
+                      plan, sched), "InvalidSize", 1, 0)
+    build(None, layout, dtab, dpos, 1, plan, sched)
+
+    run = pa.append_decode_scheduled
+    err(lambda: run(None, layout, pool, k, v, (0, need), stride, q, out, 12, 128, plan, ws),
+        "InvalidArgs")
+    err(lambda: run(None, layout, pool, k, v, (big.data_ptr() + 8, need), stride, q, out, 12, 128,
+                    plan, ws), "InvalidArgs")
+    err(lambda: run(None, layout, pool, k, v, (big.data_ptr(), need - 16), stride, q, out, 12,
+                    128, plan, ws), "InvalidSize", need, need - 16)
+    err(lambda: run(None, layout, pool, k, None, sched, stride, q, out, 12, 128, plan, ws),
+        "InvalidArgs")
+    wneed = 4 * (plan[1] + B) * 12 * (128 + 2)   # (grid + batch) partial slots per q head
+    assert ws.numel() * ws.element_size() >= wneed
+    err(lambda: run(None, layout, pool, k, v, sched, stride, q, out, 12, 128, plan,
+                    (ws.data_ptr(), wneed - 4)), "InvalidSize", wneed, wneed - 4)
+    wbig = torch.empty(wneed // 4 + 16, dtype=torch.float32, device=dev)
+    err(lambda: run(None, layout, pool, k, v, sched, stride, q, out, 12, 128, plan,
+                    (wbig.data_ptr() + 4, wneed)), "InvalidArgs")
+    err(lambda: run(None, layout, pool, k, v, sched, stride, q, out, 12, 128, (0, 0, plan[2]),
+                    ws), "InvalidSize", 1, 0)
+    lay8 = PagedKvLayout(nb, 16, 256, KvDataType.FP8)
+    pool8 = torch.zeros(lay8.floats_total(), dtype=torch.uint8, device=dev)
+    err(lambda: run(None, lay8, pool8, None, None, sched, stride, q, out, 12, 128, plan, ws),
+        "InvalidArgs")
+    run(None, layout, pool, k, v, sched, stride, q, out, 12, 128, plan, ws)
+    torch.cuda.synchronize()
+    assert torch.all(torch.isfinite(out))
+
+
+def test_scheduled_append_skipped_on_decode_schedule(dev):
+    """Rows passed with a schedule built for no append (lens_add 0): the
+    schedule's last tiles hold existing tokens, so the rows are not written
+    (the pool keeps its bytes) and the output equals the decode-only call on
+    the same schedule."""
+    shape = (12, 2, 128, 16)
+    lens = np.array([40, 16, 1, 300, 33], np.int64)
+    B = len(lens)
+    tab, nb, pool, k, v, q = sched_case(dev, shape, lens - 1, 91)
+    layout = PagedKvLayout(nb, 16, 256, KvDataType.F16)
+    plan = PagedAttention.plan(B, 12, 2, 128, 16, int(lens.max()))
+    sched = PagedAttention.schedule_buffer(B, tab.shape[1], 16, plan)
+    pa = PagedAttention(0)
+    pa.build_schedule(None, layout, i32(tab, dev), i32(lens, dev), 0, plan, sched)
+    ws = PagedAttention.workspace(plan)
+    before = pool.clone()
+    o1 = torch.full((B, 12, 128), float("nan"), device=dev)
+    o2 = torch.full((B, 12, 128), float("nan"), device=dev)
+    pa.append_decode_scheduled(None, layout, pool, k, v, sched, tab.shape[1], q, o1, 12, 128,
+                               plan, ws)
+    pa.append_decode_scheduled(None, layout, pool, None, None, sched, tab.shape[1], q, o2, 12,
+                               128, plan, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.view(torch.int16), before.view(torch.int16))
+    assert torch.equal(o1, o2)
+    ref = orc.sdpa_decode_batched(pool.float().cpu().numpy(), tab, lens.astype(np.uint32), 16,
+                                  q.cpu().numpy(), 12, 2, 128)
+    check_close(o1.cpu().numpy(), ref, "append skipped")
 
 
 @pytest.mark.parametrize("grid", [1, 3, 64, 1023])

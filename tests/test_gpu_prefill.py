@@ -4,7 +4,11 @@ The oracle's prefill_causal restates the reference's causal window
 (flash_attention_2.cu:44-68: query i at p0+i attends keys 0..=p0+i) with the
 f64 sdpa of forward_cpu.rs:424-510, on the exactly widened f32 pool.
 Tolerances: f32 KV max-abs 1e-5; f16 and bf16 KV max-abs <= 2e-3 and |gpu - ref| <= 2e-3 +
-1e-3*|ref| (bf16 uses hi+lo operand pairs to meet it).  Shapes: the
+1e-3*|ref|.  Operands: f16 pages run f16 MFMAs with q as hi + lo f16 halves
+for the scores and P one f16; bf16 pages are widened to f16 as they are
+staged (exact below 2^16) and take the same path, and a tile holding a bf16
+value of magnitude 2^16 or more is re-staged raw and run on bf16 MFMAs with q
+and P as hi + lo bf16 pairs.  Shapes: the
 reference's own FA2 test (flash_attention_parity.rs:45-207), ragged chunks on
 scattered pages, GQA groups 1..8, both compiled head sizes, and benchmark
 config 3 (sampled rows at full size).
@@ -148,6 +152,34 @@ def test_bf16_values_beyond_f16_range(dev, hd, nh, nkv):
     g = out.cpu().numpy()
     assert np.abs(ref).max() > 1e3                       # the large values reach the output
     check_close(g, ref, KvDataType.BF16, "bf16 beyond f16 range", stress=True)
+
+
+@pytest.mark.parametrize("kstd", [4.0, 16.0, 64.0])
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
+def test_large_keys_within_f16_range(dev, dtype, kstd):
+    """K of standard deviation 4-64 (every value inside f16's range, so bf16
+    pages take the f16-staged path) with N(0,1) q and V, under the strict
+    bar.  The score error of the f16 operands grows with |K|: q rounded once
+    to f16 reaches 7e-3 at a K deviation of 16; q as hi + lo halves keeps
+    every case near 5e-4."""
+    nh, nkv, hd, bt, p0, nq = 32, 8, 128, 16, 900, 160
+    rng = np.random.default_rng(77 + int(kstd) + 1000 * int(dtype))
+    total = p0 + nq
+    n_pages = -(-total // bt)
+    pool_pages = n_pages + 3
+    table = rng.permutation(pool_pages)[:n_pages].astype(np.uint32)
+    host = rng.standard_normal((pool_pages, bt, 2, nkv, hd)).astype(np.float32)
+    host[:, :, 0] *= np.float32(kstd)
+    t = torch.from_numpy(host.reshape(-1)).to(TD[dtype])
+    dpool, hpool = t.to(dev), t.to(torch.float32).numpy()
+    assert np.abs(hpool).max() < 65504.0
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    out = torch.full((nq, nh, hd), float("nan"), device=dev)
+    FlashAttention2(0).launch(None, torch.from_numpy(q).to(dev), dpool, i32(table, dev), out, nh,
+                              nkv, hd, bt, nq, p0, kv_dtype=dtype)
+    torch.cuda.synchronize()
+    ref = orc.prefill_causal(hpool, table, bt, q, nq, p0, nh, nkv, hd)
+    check_close(out.cpu().numpy(), ref, dtype, f"{dtype.name} K std {kstd:g}")
 
 
 def test_pos_ptr_overrides_offset(dev):

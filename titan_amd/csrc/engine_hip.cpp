@@ -404,6 +404,9 @@ struct tiles_args {
 };
 
 eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const tiles_cfg& t) {
+    // partial states are written and read as 16-byte vectors
+    if (!a.ws || (uintptr_t)a.ws % 16)
+        return fail(EH_INVALID_ARGS, "workspace is null or not 16-byte aligned");
     char name[64];
     const bool f8 = a.kv_dtype == EH_KV_FP8;
     const bool ext = a.window != 0 || a.block_mass != nullptr;  // sinks/window or mass records
@@ -873,6 +876,32 @@ eh_status eh_copy_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l, 
     std::snprintf(name, sizeof name, "eh_copy_pages_c%d", ch);
     return launch(c, c->mod_kv, name, dim3(std::min<uint32_t>(n_pairs, 65535)), dim3(256), stream,
                   (uint8_t*)pool, src_ids, dst_ids, n_pairs, page_bytes, (uint64_t)l->n_blocks);
+}
+
+eh_status eh_stream_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                         const void* pool, uint64_t pool_bytes, const uint32_t* ids,
+                         uint64_t ids_bytes, uint32_t n_ids, uint32_t depth, uint32_t grid,
+                         uint32_t* out, uint64_t out_bytes) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    const uint64_t elt = elt_bytes(l->data_type);
+    if (!elt) return fail(EH_UNSUPPORTED, "data_type");
+    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    if (page_bytes == 0 || page_bytes % 16384)
+        return fail(EH_UNSUPPORTED, "page bytes: a multiple of 16 KiB", 16384, page_bytes);
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    if (depth != 1 && depth != 2) return fail(EH_UNSUPPORTED, "depth: 1 or 2", 2, depth);
+    if (grid < 1) return invalid_size(1, grid, "grid");
+    if (n_ids == 0) return EH_OK;
+    if (!ids || !out || !pool) return fail(EH_INVALID_ARGS, "null pool, ids or out");
+    if (ids_bytes < 4ull * n_ids) return invalid_size(4ull * n_ids, ids_bytes, "ids");
+    const uint64_t out_need = 4ull * grid * 8;
+    if (out_bytes < out_need) return invalid_size(out_need, out_bytes, "out");
+    eh_status st = bind(c);
+    if (st) return st;
+    return launch(c, c->mod_kv, depth == 1 ? "eh_stream_pages_d1" : "eh_stream_pages_d2",
+                  dim3(grid), dim3(512), stream, (const uint8_t*)pool, ids, n_ids, page_bytes,
+                  (uint64_t)l->n_blocks, out);
 }
 
 eh_status eh_remap_block_tables(eh_context* c, eh_stream stream, uint32_t* bt, uint64_t n_entries,
@@ -1468,7 +1497,10 @@ eh_status eh_decode_schedule(eh_context* c, eh_stream stream, const eh_kv_layout
     if (batch == 0) return EH_OK;
     eh_status st = check_sched_shape(l, batch, bt_stride, grid, sched_bytes_given);
     if (st) return st;
-    if (!lens || !bt || !sched) return fail(EH_INVALID_ARGS, "lens / block_tables / schedule is null");
+    if (!lens || !bt) return fail(EH_INVALID_ARGS, "lens / block_tables is null");
+    // the kernels read and write the schedule as 16-byte records
+    if (!sched || (uintptr_t)sched % 16)
+        return fail(EH_INVALID_ARGS, "schedule is null or not 16-byte aligned");
     const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
     if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
     if (l->n_blocks < 1) return fail(EH_INVALID_ARGS, "layout");
@@ -1498,7 +1530,8 @@ eh_status eh_append_decode_scheduled(eh_context* c, eh_stream stream, const eh_k
     if (batch == 0) return EH_OK;
     eh_status st = check_sched_shape(l, batch, bt_stride, grid, sched_bytes_given);
     if (st) return st;
-    if (!sched) return fail(EH_INVALID_ARGS, "schedule is null");
+    if (!sched || (uintptr_t)sched % 16)
+        return fail(EH_INVALID_ARGS, "schedule is null or not 16-byte aligned");
     if ((keys == nullptr) != (values == nullptr)) return fail(EH_INVALID_ARGS, "keys / values");
     if (head_dim < 1 || l->row_len % head_dim) return invalid_size(head_dim, l->row_len % (head_dim ? head_dim : 1));
     const uint64_t n_head_kv = l->row_len / head_dim;

@@ -149,6 +149,16 @@ __device__ __forceinline__ uint32_t split_count(uint32_t n, uint32_t tps, uint32
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The slot kernel's f16 q is scaled by 2^q_exponent(max |q|) before its hi
+// + lo split (largest element in [2^14, 2^15)), so that the lo halves are
+// normal f16 values rather than subnormals holding a few bits above the
+// 2^-24 step, and the scores by the inverse (exact).
+__device__ __forceinline__ int q_exponent(float amax) {
+    if (!(amax > 0.0f) || !(amax < __builtin_inff())) return 0;
+    const int e = 15 - __builtin_amdgcn_frexp_expf(amax);
+    return e < -100 ? -100 : e > 100 ? 100 : e;
+}
+
 // Block-table entries one workgroup stages in LDS: every page its split
 // touches.  The host keeps tokens_per_split <= (BT_SLICE - 2) * block_tokens.
 constexpr uint32_t BT_SLICE = 1024;
@@ -403,9 +413,11 @@ __device__ __forceinline__ void decode_split(
 // wave-uniform and its block-table entry a scalar load.
 //
 // Arithmetic: q.k with packed dot2 and q split into hi + lo 16-bit parts (a
-// single rounded q is too coarse for large scores); f16 P.V pairs two tokens
-// per dot2 (P rounded to f16, well inside the tolerance); bf16 P.V widens V
-// and uses f32 fma.  Invalid tokens enter the softmax as -inf scores.
+// single rounded q is too coarse for large scores; f16: q scaled by a power
+// of two first, see q_exponent); f16 P.V pairs two tokens per dot2 (P
+// rounded to f16, with the weight sums l taken from the same rounded
+// weights, so that acc / l stays a weighted mean); bf16 P.V widens V and
+// uses f32 fma.  Invalid tokens enter the softmax as -inf scores.
 constexpr int SLOT_STEPS = 16;   // unrolled wave steps per chunk (even, power of two <= 64)
 constexpr int SLOT_DEPTH = 4;    // wave steps in flight (even)
 constexpr int SLOT_HMAX = 64;    // q heads one workgroup may serve
@@ -489,16 +501,41 @@ __device__ __forceinline__ void decode_slots(
     // q of this lane's GH heads and EPL dims, pre-scaled into the log2
     // domain, as hi + lo 16-bit pairs (heads past the group are zero).
     uint32_t qa[GH][NP], qb[GH][NP];
+    // f16: one exponent for the wave's q (wave-uniform); scores times qdown
+    float qup = scale_log2, qdown = 1.0f;
+    if constexpr (DT == DT_F16) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            const bool hv = hbase + h < group;
+            const float* qp = q + ((uint64_t)b * n_head + hk * group + (hv ? hbase + h : group - 1)) * HD;
+#pragma unroll
+            for (int e = 0; e < EPL; e += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(qp + slot_dim<HD>(sub, e));
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        const int qe = q_exponent(__builtin_bit_cast(
+            float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, amax))) * scale_log2);
+        qup = __builtin_amdgcn_ldexpf(scale_log2, qe);
+        qdown = __builtin_amdgcn_ldexpf(1.0f, -qe);
+    }
 #pragma unroll
     for (int h = 0; h < GH; ++h) {
         const bool hv = hbase + h < group;
         const uint32_t hh = hv ? hbase + h : group - 1;
-        const float sc = hv ? scale_log2 : 0.0f;
+        const float sc = hv ? qup : 0.0f;
         const float* qp = q + ((uint64_t)b * n_head + hk * group + hh) * HD;
 #pragma unroll
         for (int e = 0; e < EPL; e += 4) {
             const float4 v = *reinterpret_cast<const float4*>(qp + slot_dim<HD>(sub, e));
-            const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+            // each product rounded once, then split (opaque: fused with the
+            // product, hi and lo could come from differently rounded values)
+            float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(x[i]));
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 if constexpr (DT == DT_F16) {
@@ -561,7 +598,7 @@ __device__ __forceinline__ void decode_slots(
                 }
             }
             d = group_sum<8>(d);
-            s[h] = ok ? d : -INFINITY;
+            s[h] = ok ? d * qdown : -INFINITY;
         }
     };
     // Lazy rescale: the running maximum only moves when a score exceeds it by
@@ -628,8 +665,9 @@ __device__ __forceinline__ void decode_slots(
 #pragma unroll
                 for (int h = 0; h < GH; ++h) {
                     const float p0 = fast_exp2(s0[h] - m[h]), p1 = fast_exp2(s1[h] - m[h]);
-                    l[h] += p0 + p1;
                     const half2_v pp = {(_Float16)p0, (_Float16)p1};
+                    l[h] = __builtin_amdgcn_fdot2(pp, half2_v{(_Float16)1.0f, (_Float16)1.0f},
+                                                  l[h], false);
 #pragma unroll
                     for (int e = 0; e < EPL; ++e)
                         acc[h][e] = __builtin_amdgcn_fdot2(pp, __builtin_bit_cast(half2_v, vp[e]),

@@ -23,6 +23,11 @@
 //   * q.k is one MFMA tile per 16 tokens: S[16 tok x 16 heads] =
 //     K[16 x 128] . Q^T with v_mfma_f32_16x16x32 (f16 or bf16), q split into
 //     hi + lo 16-bit halves (two MFMAs per step) so scores keep ~22 bits;
+//     with f16 operands the wave's q is first scaled by a power of two
+//     (largest element in [2^14, 2^15)) so that the lo halves are normal
+//     f16 values rather than subnormals holding a few bits above the 2^-24
+//     step (E4M3 pages fold the K scale into q, ~1e-3), and the scores are
+//     scaled back (exact);
 //   * the score tile leaves lane (g, x) = (lane / 16, lane % 16) with the
 //     scores of tokens 4g..4g+3 for head x; the online softmax runs there in
 //     the log2 domain with a lazy rescale (the running max only moves when a
@@ -30,7 +35,10 @@
 //   * P.V is MFMA too: O^T[16 dims x 16 heads] += V^T . P^T with
 //     v_mfma_f32_16x16x16.  P^T is exactly the score tile each lane holds
 //     (f16 P; bf16 P as hi + lo halves); V^T comes from the V tile staged in
-//     LDS through the gfx950 transposed read ds_read_b64_tr_b16;
+//     LDS through the gfx950 transposed read ds_read_b64_tr_b16; with f16 P
+//     the weight sums l add the rounded f16 weights the MFMAs see, so acc / l
+//     stays a weighted mean (a dominant weight rounded by up to 2^-11 would
+//     otherwise shift the output by that much of its V row);
 //   * every wave keeps DEPTH tiles of K/V loads in flight (16-byte lanes,
 //     K in the MFMA A layout) and fetches its page ids in batches of 64
 //     tiles, read back by v_readlane;
@@ -59,6 +67,14 @@ constexpr int QSEG = 2;          // sequences per run whose q is staged in LDS u
 constexpr float RESCALE = 8.0f;  // lazy-rescale threshold, log2 domain
 constexpr float NEG_BIG = -1e30f;
 constexpr int VROW = 288;        // LDS bytes per V token row (256 + 32: conflict-free transposed reads)
+
+// Exponent e that puts values whose largest magnitude is amax in
+// [2^14, 2^15) once scaled by 2^e (0 for zero or non-finite amax).
+__device__ __forceinline__ int q_exponent(float amax) {
+    if (!(amax > 0.0f) || !(amax < __builtin_inff())) return 0;
+    const int e = 15 - __builtin_amdgcn_frexp_expf(amax);
+    return e < -100 ? -100 : e > 100 ? 100 : e;
+}
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -132,6 +148,10 @@ __device__ __forceinline__ void nested_for(F&& f) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// A value the compiler may not fuse with the operations that made it or
+// use it (an empty asm: no instruction is emitted).
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
 
 // Workgroup barrier ordering LDS only: global loads and stores still in
 // flight (the tile stream, partial writes) are not waited for.
@@ -217,6 +237,10 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     const V2 v = {(S)a, (S)b};
     return __builtin_bit_cast(uint32_t, v);
 }
+// The lo half of a hi + lo 16-bit split of a (a = hi + lo to ~2^-22).  An
+// `a` that is a product must come through opaque(): fused with the product,
+// the backend can form the hi the caller packs and the hi subtracted here
+// from differently rounded products (one f16 step apart where they differ).
 template <int DT>
 __device__ __forceinline__ float lo_part(float a) {
     typedef typename kvt<DT>::s S;
@@ -253,9 +277,10 @@ constexpr uint32_t INFO_WHOLE = 1u << 9;
 constexpr uint32_t NO_PAGE = 0xFFFFFFFFu;
 
 // Step schedule layout (uint32x4 records): P run headers {n_items, b_first,
-// b_last, 0}; P x cap item descriptors (run w's at w * cap); batch sequence
-// records {w0, w1, tokens, tiles} (the runs holding the sequence's first and
-// last tile).
+// b_last, appends} (appends = 1 when the schedule was built with lens_add > 0,
+// so that the tile holding a sequence's last token is the appended one); P x
+// cap item descriptors (run w's at w * cap); batch sequence records {w0, w1,
+// tokens, tiles} (the runs holding the sequence's first and last tile).
 struct sched_view {
     const u32x4* hdr;
     const u32x4* items;
@@ -364,6 +389,13 @@ __device__ __forceinline__ void decode_tiles(
         b0 = uni(h[1]);
         b_last = uni(h[2]);
         if (n_items == 0 || b0 > b_last || b_last >= batch) return;
+        // rows to append with a schedule built for no append (lens_add 0):
+        // its last tiles hold existing tokens, which an append would
+        // overwrite; the rows are dropped and the pool stays as it is
+        if (uni(h[3]) == 0u) {
+            new_k = nullptr;
+            new_v = nullptr;
+        }
         if (n_items > 64) dsc_next = lane + 64 < n_items ? it[lane + 64] : u32x4{NO_PAGE, 0u, 0u, 1u};
     } else {
         // tile prefix over the batch (wave 0), from the live lengths
@@ -420,15 +452,34 @@ __device__ __forceinline__ void decode_tiles(
     // memory; later sequences (runs over many short sequences) load directly.
     V8 qa[KSTEPS], qb[KSTEPS];
     const bool hv = x < group;
+    // f16 operands: q scaled by 2^qe (one exponent for the wave's heads,
+    // wave-uniform) and the scores by qdown = 2^-qe
+    float qdown = 1.0f;
     auto set_q = [&](const float4* a, const float4* c) {
         typedef typename K::s S;
-        const float sc = hv ? scale_log2 * (F8 ? k_scale[kv] : 1.0f) : 0.0f;
+        float sc = hv ? scale_log2 * (F8 ? k_scale[kv] : 1.0f) : 0.0f;
+        if constexpr (CT == DT_F16) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int st = 0; st < KSTEPS; ++st)
+                amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a[st].x), fabsf(a[st].y)),
+                                               fmaxf(fabsf(a[st].z), fabsf(a[st].w))),
+                                         fmaxf(fmaxf(fabsf(c[st].x), fabsf(c[st].y)),
+                                               fmaxf(fabsf(c[st].z), fabsf(c[st].w)))) * sc);
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+            const int qe = q_exponent(__builtin_bit_cast(
+                float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, amax))));
+            sc = __builtin_amdgcn_ldexpf(sc, qe);
+            qdown = __builtin_amdgcn_ldexpf(1.0f, -qe);
+        }
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st) {
             const float v[8] = {a[st].x, a[st].y, a[st].z, a[st].w, c[st].x, c[st].y, c[st].z, c[st].w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float vv = v[e] * sc;
+                float vv = v[e] * sc;
+                opaque(vv);  // rounded once, then split
                 qa[st][e] = (S)vv;
                 qb[st][e] = (S)lo_part<CT>(vv);
             }
@@ -675,6 +726,7 @@ __device__ __forceinline__ void decode_tiles(
             s = K::mma(a, qa[st], s);
             s = K::mma(a, qb[st], s);
         }
+        if constexpr (CT == DT_F16) s *= qdown;
         if constexpr (EXT) {
             if (win) {  // uniform
                 const span sp = make_span(ntok[cb], sink, window);
@@ -741,9 +793,24 @@ __device__ __forceinline__ void decode_tiles(
         }
         const float p0 = fast_exp2(s[0] - m_own), p1 = fast_exp2(s[1] - m_own);
         const float p2 = fast_exp2(s[2] - m_own), p3 = fast_exp2(s[3] - m_own);
-        l_own += (p0 + p1) + (p2 + p3);
+        // P^T operand (tokens 4g..4g+3 of head x) straight from the scores
+        const uint32_t ph0 = pack2<CT>(p0, p1), ph1 = pack2<CT>(p2, p3);
+        const uint64_t ph = (uint64_t)ph0 | ((uint64_t)ph1 << 32);
+        // the tile's weight sum: of the f16 weights the MFMAs see (f16 P),
+        // of the f32 weights (bf16 P as hi + lo, ~16 bits)
+        float pl;
+        if constexpr (CT == DT_F16) {
+            const f16x2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+            pl = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, ph1), one2,
+                                        __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, ph0),
+                                                               one2, 0.0f, false),
+                                        false);
+        } else {
+            pl = (p0 + p1) + (p2 + p3);
+        }
+        l_own += pl;
         if (EXT && tile_rec != nullptr) {  // uniform: this tile's weight sum per head, relative to m_own
-            float e = (p0 + p1) + (p2 + p3);
+            float e = pl;
             e += __shfl_xor(e, 16, 64);
             e += __shfl_xor(e, 32, 64);
             const uint32_t a = tok0 / TILE;
@@ -751,8 +818,6 @@ __device__ __forceinline__ void decode_tiles(
                 reinterpret_cast<float2*>(tile_rec)[((uint64_t)cb * rec_row + a) * n_head +
                                                     kv * group + x] = make_float2(e, m_own);
         }
-        // P^T operand (tokens 4g..4g+3 of head x) straight from the scores
-        const uint64_t ph = (uint64_t)pack2<CT>(p0, p1) | ((uint64_t)pack2<CT>(p2, p3) << 32);
         uint64_t plo = 0;
         if constexpr (CT == DT_BF16)
             plo = (uint64_t)pack2<CT>(lo_part<CT>(p0), lo_part<CT>(p1)) |
@@ -1015,7 +1080,7 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_tiles_schedule(
             const uint32_t f0 = ts.first(i) < T ? ts.first(i) : T;
             const uint32_t f1 = ts.first(i + 1) < T ? ts.first(i + 1) : T;
             const uint32_t n = f1 > f0 ? f1 - f0 : 0u;
-            hdr[i] = u32x4{n, n ? seq_of(f0) : 0u, n ? seq_of(f1 - 1) : 0u, 0u};
+            hdr[i] = u32x4{n, n ? seq_of(f0) : 0u, n ? seq_of(f1 - 1) : 0u, lens_add != 0u ? 1u : 0u};
         }
         if (i < T) {  // item descriptor of tile i
             const uint32_t b = seq_of(i);

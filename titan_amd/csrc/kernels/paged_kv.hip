@@ -316,3 +316,72 @@ extern "C" __global__ __launch_bounds__(256) void eh_fill_u32(uint32_t* p, uint6
          i += (uint64_t)gridDim.x * blockDim.x)
         p[i] = v;
 }
+
+// ---------------------------------------------------------------------------
+// Read ceiling of a paged decode (a measurement aid, not part of the KV
+// path): streams the listed pages once, in list order, and folds every word
+// read into one xor per wave, so no load is dead and nothing but 4 bytes per
+// wave is written.  A page is read as 16 KiB items, one wave per item, 64
+// lanes x 16 B per wave instruction (16 instructions per item); the item
+// list (page-major) is cut into equal contiguous ranges, one per wave, and
+// each wave keeps DEPTH items in flight (the next item is issued as soon as
+// its slot is consumed; issues past the range re-read the range's last item,
+// never folded).  page_bytes is a multiple of 16 KiB; ids past the pool are
+// skipped (read as page 0, not folded).
+namespace {
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+constexpr uint32_t kItemBytes = 16384;
+
+template <int DEPTH>
+__device__ __forceinline__ void stream_pages_body(const uint8_t* __restrict__ pool,
+                                                  const uint32_t* __restrict__ ids,
+                                                  uint32_t n_ids, uint64_t page_bytes,
+                                                  uint64_t n_blocks, uint32_t* __restrict__ out) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wpb = blockDim.x >> 6;
+    const uint32_t W = gridDim.x * wpb;
+    const uint32_t w = blockIdx.x * wpb + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t ipp = (uint32_t)(page_bytes / kItemBytes);  // items per page
+    const uint64_t n_items = (uint64_t)n_ids * ipp;
+    const uint64_t i0 = n_items * w / W, i1 = n_items * (w + 1) / W;
+    u32x4v acc = {0u, 0u, 0u, 0u};
+    if (i0 < i1) {
+        u32x4v r[DEPTH][16];
+        bool ok[DEPTH];
+        auto issue = [&](int d, uint64_t i) {
+            const uint64_t ic = i < i1 ? i : i1 - 1;
+            const uint32_t p = ids[ic / ipp];
+            ok[d] = i < i1 && (uint64_t)p < n_blocks;
+            const uint8_t* src = pool + ((uint64_t)p < n_blocks ? p : 0u) * page_bytes +
+                                 (ic % ipp) * kItemBytes + lane * 16u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) r[d][j] = *reinterpret_cast<const u32x4v*>(src + j * 1024);
+        };
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) issue(d, i0 + d);
+        for (uint64_t base = i0; base < i1; base += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                u32x4v x = r[d][0];
+#pragma unroll
+                for (int j = 1; j < 16; ++j) x ^= r[d][j];
+                acc ^= ok[d] ? x : u32x4v{0u, 0u, 0u, 0u};
+                issue(d, base + d + DEPTH);
+            }
+        }
+    }
+    uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v ^= (uint32_t)__shfl_xor((int)v, o, 64);
+    if (lane == 0) out[w] = v;
+}
+}  // namespace
+
+#define EH_STREAM_PAGES(D)                                                                       \
+    extern "C" __global__ __launch_bounds__(512) void eh_stream_pages_d##D(                      \
+        const uint8_t* pool, const uint32_t* ids, uint32_t n_ids, uint64_t page_bytes,           \
+        uint64_t n_blocks, uint32_t* out) {                                                      \
+        stream_pages_body<D>(pool, ids, n_ids, page_bytes, n_blocks, out);                       \
+    }
+EH_STREAM_PAGES(1)
+EH_STREAM_PAGES(2)

@@ -25,14 +25,16 @@
 //     straight from registers (keys permuted consistently between P and V^T);
 //   * the accumulators are rescaled only when a row maximum grows by more
 //     than 2^8 (exact: every term uses the same stale maximum);
-//   * operands: f16 KV -> f16 MFMA with f16 Q and P; bf16 KV -> widened to
-//     f16 as the tiles are staged (exact: a bf16 significand has 8 bits, and
-//     every finite bf16 below 2^16 in magnitude is an f16, down to 2^-14;
-//     below that the f16 subnormals keep the value to 2^-24), then the f16
-//     path; a staged tile holding a finite bf16 of magnitude >= 2^16 is
-//     re-staged raw and computed on bf16 MFMAs with Q and P each split into
-//     hi + lo bf16 parts (two MFMAs per product, ~16 significant bits);
-//     f32 KV -> f32 MFMA (no operand rounding);
+//   * operands: f16 KV -> f16 MFMA with Q split into hi + lo f16 halves
+//     for the scores (~22 significant bits) and P one f16; bf16 KV ->
+//     widened to f16 as the tiles are staged (exact: a bf16 significand has
+//     8 bits, and every finite bf16 below 2^16 in magnitude is an f16, down
+//     to 2^-14; below that the f16 subnormals keep the value to 2^-24), then
+//     the f16 path; a staged tile holding a finite bf16 of magnitude >= 2^16
+//     is re-staged raw and computed on bf16 MFMAs with Q and P each split
+//     into hi + lo bf16 parts (two MFMAs per product, ~16 significant bits);
+//     E4M3 KV -> widened to f16 (exact), the f16 path; f32 KV -> f32 MFMA
+//     (no operand rounding);
 //   * workgroups are dispatched longest row block first (causal: a later
 //     row block attends more keys), so the second round of workgroups on a
 //     CU fills in behind the first; the row blocks of one (sequence, kv
@@ -53,6 +55,14 @@ constexpr uint32_t ROWS = NT / 2;  // query rows per workgroup: 32 per wave
 constexpr uint32_t SLICE = 1024;  // block-table entries staged in LDS at once
 constexpr float RESCALE_LOG2 = 8.0f;
 
+// Exponent e that puts a row whose largest |element| is amax in
+// [2^14, 2^15) once scaled by 2^e (0 for an all-zero or non-finite row).
+__device__ __forceinline__ int q_exponent(float amax) {
+    if (!(amax > 0.0f) || !(amax < __builtin_inff())) return 0;
+    const int e = 15 - __builtin_amdgcn_frexp_expf(amax);
+    return e < -100 ? -100 : e > 100 ? 100 : e;
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -63,11 +73,24 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <int DT> struct op_t;
+// 16-bit pages (f16, bf16 widened to f16, E4M3 widened to f16): q is split
+// into hi + lo f16 halves for S = K Q^T (two MFMAs per step, ~22-bit scores;
+// one f16 q would carry an error that grows with |K|: 7e-3 max-abs at K of
+// standard deviation 16 against 5e-4 with the split); P stays one f16.
+// q is first scaled by a power of two per wave (largest element in
+// [2^14, 2^15)): a lo half of ~2^-11 of an element is then a normal f16,
+// where unscaled it would often be subnormal and keep only the few bits
+// above f16's absolute step of 2^-24 (with E4M3 pages q carries the K scale
+// and is ~1e-3); the scores are scaled back, exactly.  The row sums l are
+// taken from the same f16-rounded P that feeds the P.V MFMAs, so that
+// acc / l stays a weighted mean: with the unrounded sums, a dominant weight
+// rounded by up to 2^-11 shifts the output by that much of its V row
+// (2.7e-3 measured at K of standard deviation 16).
 template <> struct op_t<DT_F16> {
     typedef f16x8 v;
     static constexpr int KS = 16;  // contraction depth of one MFMA
     static constexpr int ELT = 2;
-    static constexpr bool SPLIT = false;
+    static constexpr bool SPLIT = true;
     static __device__ __forceinline__ f32x16 mma(v a, v b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
@@ -91,14 +114,15 @@ template <> struct op_t<DT_F32> {
     }
 };
 
-// E4M3 pages are staged into LDS as f16 (exact) and use the f16 operands,
-// with q split into hi + lo f16 halves for S (E4M3 keys span 448 / 2^-9, so
-// scores need more than q's 11 bits); P stays single f16 as in decode.
-template <> struct op_t<DT_FP8> : op_t<DT_F16> {
-    static constexpr bool SPLIT = true;
-};
+// E4M3 pages are staged into LDS as f16 (exact) and use the f16 operands.
+template <> struct op_t<DT_FP8> : op_t<DT_F16> {};
 
-// 8 f32 -> MFMA operand (hi part, and lo = x - hi for split types).
+// 8 f32 -> MFMA operand (hi part, and lo = x - hi for split types).  A
+// caller whose x are products must pass them through opaque(): fused with
+// the product, the backend formed the hi that feeds the MFMA and the hi
+// subtracted for lo from two differently rounded products (v_cvt_pk_f16_f32
+// of the rounded product, v_fma_mixlo_f16 of the exact one), and where
+// they differed hi + lo missed x by one f16 step (1e-3-scale score errors).
 template <int DT>
 __device__ __forceinline__ void pack8(const float* x, typename op_t<DT>::v& hi,
                                       typename op_t<DT>::v& lo) {
@@ -121,6 +145,10 @@ __device__ __forceinline__ void pack8(const float* x, typename op_t<DT>::v& hi,
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// A value the compiler may not fuse with the operations that made it or
+// use it (an empty asm: no instruction is emitted).
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
 
 // Transposed LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane
 // 4r + b points at 4 consecutive 16-bit elements of row r (columns 4b..4b+3)
@@ -456,16 +484,39 @@ __device__ __forceinline__ void prefill(
     constexpr int QSTEPS = HD / O::KS;
     const float qscale = scale_log2 * (F8 ? k_scale[hk] : 1.0f);  // E4M3: the K scale folds into q
     opv qa[QSTEPS], qb[O::SPLIT ? QSTEPS : 1];
+    // 16-bit operands: the wave's q is scaled by 2^qe before the split and
+    // its scores by qdown = 2^-qe after the MFMAs (both exact)
+    float qdown = 1.0f;
     {
         const float* qrow = q + ((uint64_t)(qoff + tok) * n_head + head) * HD;
         if constexpr (Gm::ELT == 2) {
+            float4 a[QSTEPS], c[QSTEPS];
+            float amax = 0.0f;
 #pragma unroll
             for (int t = 0; t < QSTEPS; ++t) {
-                const float4 a = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h);
-                const float4 c = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h + 4);
-                const float x[8] = {a.x * qscale, a.y * qscale, a.z * qscale,
-                                    a.w * qscale, c.x * qscale, c.y * qscale,
-                                    c.z * qscale, c.w * qscale};
+                a[t] = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h);
+                c[t] = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h + 4);
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a[t].x), fabsf(a[t].y)),
+                                         fmaxf(fabsf(a[t].z), fabsf(a[t].w))));
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(c[t].x), fabsf(c[t].y)),
+                                         fmaxf(fabsf(c[t].z), fabsf(c[t].w))));
+            }
+            // one exponent for the wave's 32 rows (wave-uniform, so the
+            // scale costs no vector register in the tile loop): a row's lo
+            // halves stay normal down to 2^17 below the wave's largest element
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+            amax = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                                 __builtin_bit_cast(int, amax))) * qscale;
+            const int qe = q_exponent(amax);
+            const float up = __builtin_amdgcn_ldexpf(qscale, qe);
+            qdown = __builtin_amdgcn_ldexpf(1.0f, -qe);
+#pragma unroll
+            for (int t = 0; t < QSTEPS; ++t) {
+                float x[8] = {a[t].x * up, a[t].y * up, a[t].z * up, a[t].w * up,
+                              c[t].x * up, c[t].y * up, c[t].z * up, c[t].w * up};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) opaque(x[e]);  // rounded once, then split
                 pack8<CT>(x, qa[t], qb[O::SPLIT ? t : 0]);
             }
         } else {
@@ -535,17 +586,17 @@ __device__ __forceinline__ void prefill(
             f32x16 s = f32x16{};
             const uint8_t* krow = ks + (sb * 32 + l32) * Gm::KPITCH;
             if constexpr (Gm::ELT == 2) {
-                if (B2H && big) {  // uniform: raw bf16 keys, q's f16 value split hi + lo bf16 (exact)
+                if (B2H && big) {  // uniform: raw bf16 keys, q (f16 hi + lo) split hi + lo bf16
 #pragma unroll
                     for (int t = 0; t < QSTEPS; ++t) {
                         const typename OB::v a = *reinterpret_cast<const typename OB::v*>(krow + (16 * t + 8 * h) * 2);
                         // recomputed per use (kept out of the loop-invariant set:
                         // hoisted for every step it would hold 64 more registers)
-                        opv qt = qa[t];
-                        asm volatile("" : "+v"(qt));
+                        opv qt = qa[t], qu = qb[t];
+                        asm volatile("" : "+v"(qt), "+v"(qu));
                         float x[8];
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) x[e] = (float)qt[e];
+                        for (int e = 0; e < 8; ++e) x[e] = (float)qt[e] + (float)qu[e];
                         typename OB::v qh, ql;
                         pack8<DT_BF16>(x, qh, ql);
                         s = OB::mma(a, qh, s);
@@ -591,7 +642,7 @@ __device__ __forceinline__ void prefill(
             for (int sb = 0; sb < Gm::SUB; ++sb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sv[sb][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * qdown;
             if (__builtin_amdgcn_ballot_w64(mx > m_run + RESCALE_LOG2)) {
                 const float mn = fmaxf(m_run, mx);
                 const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
@@ -605,18 +656,31 @@ __device__ __forceinline__ void prefill(
         for (int sb = 0; sb < Gm::SUB; ++sb) {
             const f32x16 s = sv[sb];
             float p[16];
-            float ps = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                p[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
-                ps += p[r];
-            }
-            l_run += ps;
+            for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf(s[r], qdown, -m_run));
             // O^T (HD x 32 rows) += V^T P^T
             if constexpr (Gm::ELT == 2) {
                 opv pa[2], pb[2];
                 pack8<CT>(p, pa[0], pb[0]);
                 pack8<CT>(p + 8, pa[1], pb[1]);
+                if (B2H && big) {  // uniform: P as hi + lo bf16 pairs (~16 bits), f32 sum
+                    float ps = 0.f;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) ps += p[r];
+                    l_run += ps;
+                } else {  // the sum of the f16 weights the MFMAs see
+                    // (pairs taken lane by lane: reading them through a u32x4
+                    // bit-cast of pa[i] compiled, with ROCm 7.2's hipcc, to
+                    // four dot2s of the first dword)
+                    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+                    const f16x2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            l_run = __builtin_amdgcn_fdot2(f16x2{pa[i][2 * j], pa[i][2 * j + 1]},
+                                                           one2, l_run, false);
+                }
 
                 const uint8_t* vtr = vs + vtr_off;
                 // A = V^T[dims db*32 + l32][keys]: lane (l32, h) takes keys
@@ -642,11 +706,14 @@ __device__ __forceinline__ void prefill(
                         } else {
                             const opv a = __builtin_bit_cast(opv, w);
                             acc[db] = O::mma(a, pa[st], acc[db]);
-                            if constexpr (O::SPLIT && !F8) acc[db] = O::mma(a, pb[st], acc[db]);
                         }
                     }
                 }
             } else {
+                float ps = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ps += p[r];
+                l_run += ps;
 #pragma unroll
                 for (int db = 0; db < HD / 32; ++db) {
                     const int d = db * 32 + l32;

@@ -162,6 +162,19 @@ class PagedKvGpu:
         check(self._L.eh_copy_pages(self._ctx.handle, stream_handle(stream), C.byref(layout.c()),
                                     pp, pb, buf(src_ids)[0], buf(dst_ids)[0], int(n)))
 
+    def stream_pages(self, stream, layout, pool, ids, out, depth=1, grid=256):
+        """Measurement aid (no reference counterpart): reads the pages listed
+        in `ids` once (16 KiB items, `depth` in flight per wave, `grid`
+        workgroups of 8 waves) and writes one xor of the words read per
+        wave into `out` (u32 [grid * 8]): the cold-read floor of a decode
+        over the same pages."""
+        pp, pb = buf(pool)
+        ip, ib = buf(ids)
+        op, ob = buf(out)
+        check(self._L.eh_stream_pages(self._ctx.handle, stream_handle(stream),
+                                      C.byref(layout.c()), pp, pb, ip, ib, int(ids.numel()),
+                                      int(depth), int(grid), op, ob))
+
     def remap_block_tables(self, stream, block_tables, remap):
         """entry = remap[entry] for every entry below len(remap)."""
         check(self._L.eh_remap_block_tables(self._ctx.handle, stream_handle(stream),
