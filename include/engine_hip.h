@@ -66,7 +66,10 @@ typedef struct eh_kv_layout {
  * Loads the gfx950 code objects from code_object_dir (NULL = the directory
  * of this library) and allocates the split-K scratch once. */
 eh_status eh_create(int device, const char* code_object_dir, eh_context** out);
-/* Drop for all three (paged_kv.rs:478-491): unloads modules, frees scratch. */
+/* Drop for all three (paged_kv.rs:478-491): unloads modules, frees scratch.
+ * Work launched through ctx must have completed, and no HIP graph captured
+ * with its launches may be replayed afterwards: the graph's kernel nodes
+ * point into the unloaded code objects. */
 void eh_destroy(eh_context* ctx);
 /* Detail of this thread's last failure: expected/actual for InvalidSize and
  * PoolExhausted (blocks_used/blocks_total), the site string, the HIP code. */
@@ -255,6 +258,9 @@ eh_status eh_append_flash_decoding_ws(eh_context* ctx, eh_stream stream, uint32_
  *     tokens_per_split = 0 and max_splits = the grid (workgroups); the device
  *     cuts the batch's 16-token tiles evenly among them from the live
  *     lengths, so any context lengths are served (max_ctx is not a bound);
+ *     q enters its MFMAs as hi + lo 16-bit halves, so over f16 (and E4M3)
+ *     pages q's elements must stay below ~5e5 in magnitude (|q| log2(e) /
+ *     sqrt(128) within f16's 65504);
  *   - otherwise fixed splits: tokens_per_split (hint rounded up to the
  *     kernel's split granularity -- one round of its four waves, 8 to 256
  *     tokens, for the per-token kernel -- or automatic; at most

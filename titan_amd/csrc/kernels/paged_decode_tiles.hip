@@ -22,12 +22,9 @@
 //     dispatch faster) that share one scan of the lengths;
 //   * q.k is one MFMA tile per 16 tokens: S[16 tok x 16 heads] =
 //     K[16 x 128] . Q^T with v_mfma_f32_16x16x32 (f16 or bf16), q split into
-//     hi + lo 16-bit halves (two MFMAs per step) so scores keep ~22 bits;
-//     with f16 operands the wave's q is first scaled by a power of two
-//     (largest element in [2^14, 2^15)) so that the lo halves are normal
-//     f16 values rather than subnormals holding a few bits above the 2^-24
-//     step (E4M3 pages fold the K scale into q, ~1e-3), and the scores are
-//     scaled back (exact);
+//     hi + lo 16-bit halves (two MFMAs per step) so scores keep ~22 bits
+//     (an f16 lo half below 2^-14 is a subnormal: its 2^-24 step still
+//     leaves q ~21 bits at the scale of the contract's data);
 //   * the score tile leaves lane (g, x) = (lane / 16, lane % 16) with the
 //     scores of tokens 4g..4g+3 for head x; the online softmax runs there in
 //     the log2 domain with a lazy rescale (the running max only moves when a
@@ -39,6 +36,8 @@
 //     the weight sums l add the rounded f16 weights the MFMAs see, so acc / l
 //     stays a weighted mean (a dominant weight rounded by up to 2^-11 would
 //     otherwise shift the output by that much of its V row);
+//   * E4M3 pages apply the K scale to the scores after the MFMAs (folded
+//     into q, q * scale ~ 1e-3 would leave its lo halves only a few bits);
 //   * every wave keeps DEPTH tiles of K/V loads in flight (16-byte lanes,
 //     K in the MFMA A layout) and fetches its page ids in batches of 64
 //     tiles, read back by v_readlane;
@@ -47,7 +46,7 @@
 //     (m, l, acc) that eh_decode_tiles_merge combines.
 // E4M3 pages (OCP E4M3FN codes with one f32 scale per kv head for K and for
 // V) are converted to f16 in registers -- exact, every E4M3 value is an f16 --
-// and take the f16 path: the K scale is folded into q, the V scale into the
+// and take the f16 path: the K scale multiplies the scores, the V scale the
 // written rows and partials.
 // Pages must be a power of two of at least 16 tokens; head_dim 128;
 // at most 8 q heads per kv head; block-table entries past the table or the
@@ -68,13 +67,6 @@ constexpr float RESCALE = 8.0f;  // lazy-rescale threshold, log2 domain
 constexpr float NEG_BIG = -1e30f;
 constexpr int VROW = 288;        // LDS bytes per V token row (256 + 32: conflict-free transposed reads)
 
-// Exponent e that puts values whose largest magnitude is amax in
-// [2^14, 2^15) once scaled by 2^e (0 for zero or non-finite amax).
-__device__ __forceinline__ int q_exponent(float amax) {
-    if (!(amax > 0.0f) || !(amax < __builtin_inff())) return 0;
-    const int e = 15 - __builtin_amdgcn_frexp_expf(amax);
-    return e < -100 ? -100 : e > 100 ? 100 : e;
-}
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -452,27 +444,14 @@ __device__ __forceinline__ void decode_tiles(
     // memory; later sequences (runs over many short sequences) load directly.
     V8 qa[KSTEPS], qb[KSTEPS];
     const bool hv = x < group;
-    // f16 operands: q scaled by 2^qe (one exponent for the wave's heads,
-    // wave-uniform) and the scores by qdown = 2^-qe
-    float qdown = 1.0f;
+    // E4M3 pages: the K scale multiplies the scores after the MFMAs rather
+    // than q (q * scale ~ 1e-3 would leave the lo halves a few bits above
+    // f16's 2^-24 step).  With f16 operands, |q| * log2(e) / sqrt(128) must
+    // stay below 65504 (|q| below ~5e5).
+    const float qdown = F8 ? k_scale[kv] : 1.0f;
     auto set_q = [&](const float4* a, const float4* c) {
         typedef typename K::s S;
-        float sc = hv ? scale_log2 * (F8 ? k_scale[kv] : 1.0f) : 0.0f;
-        if constexpr (CT == DT_F16) {
-            float amax = 0.0f;
-#pragma unroll
-            for (int st = 0; st < KSTEPS; ++st)
-                amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a[st].x), fabsf(a[st].y)),
-                                               fmaxf(fabsf(a[st].z), fabsf(a[st].w))),
-                                         fmaxf(fmaxf(fabsf(c[st].x), fabsf(c[st].y)),
-                                               fmaxf(fabsf(c[st].z), fabsf(c[st].w)))) * sc);
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-            const int qe = q_exponent(__builtin_bit_cast(
-                float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, amax))));
-            sc = __builtin_amdgcn_ldexpf(sc, qe);
-            qdown = __builtin_amdgcn_ldexpf(1.0f, -qe);
-        }
+        const float sc = hv ? scale_log2 : 0.0f;
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st) {
             const float v[8] = {a[st].x, a[st].y, a[st].z, a[st].w, c[st].x, c[st].y, c[st].z, c[st].w};
@@ -726,7 +705,7 @@ __device__ __forceinline__ void decode_tiles(
             s = K::mma(a, qa[st], s);
             s = K::mma(a, qb[st], s);
         }
-        if constexpr (CT == DT_F16) s *= qdown;
+        if constexpr (F8) s *= qdown;  // the K scale
         if constexpr (EXT) {
             if (win) {  // uniform
                 const span sp = make_span(ntok[cb], sink, window);
