@@ -52,6 +52,8 @@ def parse():
     p.add_argument("--suite", action="store_true",
                    help="instead of the headline line, time the other benchmark configurations "
                         "(1, 3, 4, 5) and append/gather, one JSON line each")
+    p.add_argument("--append-tokens", type=int, default=1,
+                   help="suite append part: tokens appended per sequence per call (config 2: 1)")
     p.add_argument("--c5-pool-frac", type=float, default=0.9,
                    help="config 5 pool size as a fraction of free HBM")
     p.add_argument("--parts", default="c1,append,e4m3,ceiling,c3,c4,c5",
@@ -421,17 +423,25 @@ def suite(args, dev):
     tab2 = synth.block_tables(s2, extra_tokens=1)
     dtab2 = torch.from_numpy(tab2.view(np.int32)).to(dev)
     if "append" in parts:  # append / gather at config 2's shape (one layer)
+        A = max(args.append_tokens, 1)
+        sa = synth.config2(0, extra_tokens=A) if A > 1 else s2
+        taba = synth.block_tables(sa, extra_tokens=A) if A > 1 else tab2
+        dtaba = torch.from_numpy(taba.view(np.int32)).to(dev)
+        lay2 = PagedKvLayout(sa.n_blocks, 16, sa.row_len, KvDataType.F16)
+        pool2 = torch.randn(lay2.floats_total(), generator=gen, device=dev, dtype=torch.float16)
+        nk2 = torch.randn((32 * A, sa.row_len), generator=gen, device=dev, dtype=torch.float16)
+        nv2 = torch.randn((32 * A, sa.row_len), generator=gen, device=dev, dtype=torch.float16)
+        cu2 = torch.arange(0, 32 * A + 1, A, dtype=torch.int32, device=dev)
+        st2 = torch.from_numpy(sa.ctx_lens.astype(np.int32)).to(dev)
+        us_app = graph_time_us(lambda st: kv.append_kv_batched(st, lay2, pool2, nk2, nv2, dtaba,
+                                                               cu2, st2, 32 * A), 20)
+        app_bytes = 32 * A * 2 * sa.row_len * 2 * 2
+        emit({"config": 2, "what": f"batched append of {A} token(s) per sequence "
+              f"({32 * A} x 1 KiB rows), f16", "latency_us": round(us_app, 2),
+              "GB/s": round(app_bytes / us_app / 1e3, 2)})
+        del pool2
         lay2 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, KvDataType.F16)
         pool2 = torch.randn(lay2.floats_total(), generator=gen, device=dev, dtype=torch.float16)
-        nk2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
-        nv2 = torch.randn((32, s2.row_len), generator=gen, device=dev, dtype=torch.float16)
-        cu2 = torch.arange(33, dtype=torch.int32, device=dev)
-        st2 = torch.from_numpy(s2.ctx_lens.astype(np.int32)).to(dev)
-        us_app = graph_time_us(lambda st: kv.append_kv_batched(st, lay2, pool2, nk2, nv2, dtab2,
-                                                               cu2, st2, 32), 20)
-        app_bytes = 32 * 2 * s2.row_len * 2 * 2
-        emit({"config": 2, "what": "batched append of one token per sequence (32 x 1 KiB rows), "
-              "f16", "latency_us": round(us_app, 2), "GB/s": round(app_bytes / us_app / 1e3, 2)})
         L0 = int(s2.ctx_lens[0])
         gout = torch.empty((L0, s2.row_len), dtype=torch.float16, device=dev)
         tab_row = dtab2[0].contiguous()
