@@ -173,10 +173,10 @@ def test_tiles_workspace_reuse(dev):
 def test_decode_large_keys_within_f16_range(dev, dtype, kstd, shape):
     """K of standard deviation 4-64 (inside f16's range) with N(0,1) q and V,
     under the strict bar, through the balanced MFMA kernel (hd 128) and the
-    fixed-split dot2 kernel (hd 64).  With f16 operands the q lo halves
-    (~2^-11 of q) and the small weights fall into f16's subnormal range,
-    which the MFMA / dot2 operands do not keep: q is scaled by a power of two
-    first and P carries 2^7, else the error grows with |K|."""
+    fixed-split dot2 kernel (hd 64).  With one f16 q the score error grows
+    with |K|; the kernels split q into hi + lo f16 halves taken from one
+    rounded value (the hd-64 kernel scales q by a power of two per wave
+    first), and sum l from the same f16-rounded weights that feed P.V."""
     n_head, n_kv, hd, bt = shape
     rng = np.random.default_rng(600 + int(kstd) + 10 * int(dtype) + hd)
     lens = np.array([2900, 1, 700, 16, 1500, 33], np.int64)
