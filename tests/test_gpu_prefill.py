@@ -233,6 +233,78 @@ def test_batched_ragged_chunks(dev, dtype):
         check_close(g[cu[b]:cu[b + 1]], ref, dtype, f"seq {b}")
 
 
+PP_CASES = [
+    # (dtype, n_head, n_kv, hd, bt, starts, lens)
+    (KvDataType.BF16, 32, 8, 128, 16, [2048, 0, 700], [512, 300, 129]),
+    (KvDataType.F16, 32, 8, 128, 16, [2048, 0, 700], [512, 300, 129]),
+    (KvDataType.FP8, 32, 8, 128, 16, [2048, 0, 700], [512, 300, 129]),
+    (KvDataType.BF16, 16, 2, 64, 8, [0, 5, 1000], [33, 1, 260]),
+    (KvDataType.F16, 12, 4, 128, 4, [90, 3], [77, 140]),
+]
+
+
+@pytest.mark.parametrize("case", PP_CASES, ids=lambda c: f"{c[0].name}-{c[1]}x{c[2]}-hd{c[3]}-bt{c[4]}")
+def test_pingpong_matches_single_phase(dev, monkeypatch, case):
+    """The two prefill kernels (eh_prefill_pp_*: the workgroup's halves take
+    turns at MFMAs and softmax; eh_prefill_*: every wave does both) compute the
+    same products in the same order per accumulator: outputs bit-identical on
+    ragged chunks over scattered pages, with one table entry pointing outside
+    the pool (its keys masked), for every page type the ping-pong kernel
+    takes; and the ping-pong output against the oracle."""
+    dtype, nh, nkv, hd, bt, starts, lens = case
+    rng = np.random.default_rng(77 + PP_CASES.index(case))
+    stride = max(-(-(s + n) // bt) for s, n in zip(starts, lens)) + 1
+    n_pages = sum(-(-(s + n) // bt) for s, n in zip(starts, lens)) + 3
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    tables = np.full((len(starts), stride), 0xFFFFFFFF, np.uint32)
+    o = 0
+    for b, (s0, n) in enumerate(zip(starts, lens)):
+        k = -(-(s0 + n) // bt)
+        tables[b, :k] = perm[o:o + k]
+        o += k
+    tables[0, 3] = n_pages + 7  # outside the pool: masked by both kernels
+    total = sum(lens)
+    q = rng.standard_normal((total, nh, hd)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    fa = FlashAttention2(0)
+    if dtype == KvDataType.FP8:
+        codes, ks, vs = gauss_codes(rng, n_pages, bt, nkv, hd)
+        dpool = torch.from_numpy(codes).to(dev)
+        f = orc.e4m3_to_f32(codes).reshape(n_pages, bt, 2, nkv, hd)
+        f[:, :, 0] *= ks[None, None, :, None]
+        f[:, :, 1] *= vs[None, None, :, None]
+        hpool = f.reshape(-1)
+        dks, dvs = torch.from_numpy(ks).to(dev), torch.from_numpy(vs).to(dev)
+    else:
+        dpool, hpool = make_pool(rng, n_pages, bt, nkv, hd, dtype, dev)
+    outs = {}
+    for kern in ("single", "pp"):
+        monkeypatch.setenv("EH_PREFILL_KERNEL", kern)
+        out = torch.full((total, nh, hd), float("nan"), device=dev)
+        args = (None, torch.from_numpy(q).to(dev), dpool, i32(tables, dev), i32(cu, dev),
+                i32(np.array(starts, np.uint32), dev), out, nh, nkv, hd, bt, max(lens))
+        if dtype == KvDataType.FP8:
+            fa.launch_batched_e4m3(*args, dks, dvs)
+        else:
+            fa.launch_batched(*args, kv_dtype=dtype)
+        torch.cuda.synchronize()
+        outs[kern] = out.cpu().numpy()
+    if hd == 128:  # both kernels walk 64-key tiles: one running-max update per tile each
+        assert np.array_equal(outs["pp"].view(np.uint32), outs["single"].view(np.uint32))
+    else:  # head_dim 64: the single-phase kernel's tiles hold 128 keys, so the
+        # lazy rescale points differ; both within the bar of each other
+        check_close(outs["pp"], outs["single"], KvDataType.F16, "pp vs single-phase")
+    # the oracle reads every table entry: sequences 1.. (sequence 0 holds the
+    # masked entry, pinned above by bit identity and by test_invalid_pages_are_masked)
+    for b, (s0, n) in enumerate(zip(starts, lens)):
+        if b == 0:
+            continue
+        k = -(-(s0 + n) // bt)
+        ref = orc.prefill_causal(hpool, tables[b, :k], bt, q[cu[b]:cu[b + 1]], n, s0, nh, nkv, hd)
+        check_close(outs["pp"][cu[b]:cu[b + 1]], ref,
+                    KvDataType.F16 if dtype == KvDataType.FP8 else dtype, f"pp seq {b}")
+
+
 def test_invalid_pages_are_masked(dev):
     # Entries past the pool mask their keys: the result equals attention over
     # the remaining keys (a sequence whose first page is invalid).

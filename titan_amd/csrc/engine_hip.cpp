@@ -14,6 +14,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -508,9 +509,27 @@ struct prefill_args {
 
 constexpr uint32_t kPrefillRows = 256;  // query rows per workgroup (8 waves x 32), mirrors ROWS
 // One launch: grid (256-row tiles, kv heads, sequences) of 512 threads.
+// bf16 pages with whole staging items per page take the ping-pong kernels
+// (eh_prefill_pp_*: the workgroup's two halves alternate their MFMA and
+// softmax phases), measured 7-8 % faster than the single-phase kernels at
+// config 3; f16 and E4M3 pages ran 3 % slower on them and keep the
+// single-phase kernels, as do f32 pages and other page sizes.  Both compute
+// the same products in the same order per accumulator, so their outputs are
+// bit-identical.  EH_PREFILL_KERNEL in the environment overrides the choice
+// for the 16-bit and E4M3 types: "single" or "pp" (a diagnostic).
+bool prefill_pingpong(const prefill_args& a) {
+    if (a.kv_dtype == EH_KV_F32) return false;
+    const uint32_t item_keys = a.head_dim == 128 ? 4u : 2u;  // pp_item_keys<HD>() in the kernel
+    if (a.block_tokens % item_keys != 0) return false;
+    const char* env = std::getenv("EH_PREFILL_KERNEL");
+    if (env && std::strcmp(env, "single") == 0) return false;
+    if (env && std::strcmp(env, "pp") == 0) return true;
+    return a.kv_dtype == EH_KV_BF16;
+}
+
 eh_status run_prefill(eh_context* c, eh_stream stream, const prefill_args& a) {
     char name[48];
-    std::snprintf(name, sizeof name, "eh_prefill_%s_hd%u",
+    std::snprintf(name, sizeof name, "eh_prefill_%s%s_hd%u", prefill_pingpong(a) ? "pp_" : "",
                   a.kv_dtype == EH_KV_FP8 ? "fp8" : dt_name(a.kv_dtype), a.head_dim);
     const uint32_t group = a.n_head / a.n_head_kv;
     const uint64_t tiles = div_ceil((uint64_t)a.max_q * group, kPrefillRows);

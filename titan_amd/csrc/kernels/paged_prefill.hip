@@ -150,6 +150,26 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // use it (an empty asm: no instruction is emitted).
 __device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
 
+// max / sum of x over lanes l and l ^ 32, on every lane, without the LDS
+// path of a shuffle: v_permlane32_swap(a, b) leaves the lower halves of a and
+// b in the first result and their upper halves in the second.  b is an opaque
+// copy of a: with the same value in both operands the compiler took the two
+// results for equal and dropped one of them.
+__device__ __forceinline__ uint2 halves(float x) {
+    uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+    asm volatile("" : "+v"(b));
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    return make_uint2(r[0], r[1]);
+}
+__device__ __forceinline__ float max_halves(float x) {
+    const uint2 r = halves(x);
+    return fmaxf(__builtin_bit_cast(float, r.x), __builtin_bit_cast(float, r.y));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+    const uint2 r = halves(x);
+    return __builtin_bit_cast(float, r.x) + __builtin_bit_cast(float, r.y);
+}
+
 // Transposed LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane
 // 4r + b points at 4 consecutive 16-bit elements of row r (columns 4b..4b+3)
 // of a 4 x 16 block; lane c receives column c of rows 0..3.
@@ -751,6 +771,550 @@ __device__ __forceinline__ void prefill(
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Ping-pong prefill for pages whose tiles are staged as f16 (f16; bf16 below
+// 2^16; E4M3), block_tokens a multiple of the staging item's keys.  The host
+// library sends bf16 pages here (7-8 % faster than prefill() at config 3; f16
+// and E4M3 pages ran 3 % slower here and stay on prefill()).
+//
+// Per 64-key tile a wave's work is MFMA-bound (S = K Q^T: 32 MFMAs with the q
+// split; P.V: 16) or VALU-bound (mask, running max, 32 exponentials, packing,
+// row sums).  With one barrier per tile the two waves of a SIMD run the same
+// phase at the same time.  Here the halves of the workgroup take turns: waves
+// 0-3 (one per SIMD) run their MFMA phase while waves 4-7 run their softmax,
+// then they swap, with a workgroup barrier between the phases.  A wave's MFMA
+// phase is P.V of the previous tile, then S of the current one, so P stays in
+// registers; it also stages the next tile (waves 0-3 write K one tile ahead,
+// waves 4-7 write V), whose VALU work then issues beside the MFMAs:
+//   interval 2j  : waves 0-3 MFMA [P.V(j-1), S(j)], write K(j+1)  waves 4-7 softmax(j-1)
+//   interval 2j+1: waves 0-3 softmax(j)   waves 4-7 MFMA [P.V(j-1), S(j)], write V(j)
+// K(j+1) is read at intervals 2j+2 and 2j+3 and its buffer next written at
+// 2j+4; V(j) is read at 2j+2 and 2j+3 and its buffer next written at 2j+5:
+// two buffers of each.  Tile t's key flags are written at 2t-2 and read by the
+// softmaxes at 2t+1 and 2t+2: three buffers.  The barriers wait for LDS only:
+// each staging thread's global loads for the next tile (and the page id for
+// the one after) stay in flight across them.  Operands, masking and softmax
+// are those of prefill(), in the same order per accumulator (bit-identical
+// outputs where both walk 64-key tiles, head_dim 128).  A bf16 tile holding a
+// value of magnitude >= 2^16 raises a flag that every wave reads after the
+// next barrier; the workgroup then restarts on prefill(), which computes such
+// tiles exactly.
+template <int HD>
+struct ppg {
+    static constexpr int N = 64;                 // keys per tile
+    static constexpr int SUB = N / 32;           // 32-key score blocks per tile
+    static constexpr int PARTS = HD / 8;         // 8-element chunks per head row
+    static constexpr int KPI = N * PARTS / 256;  // keys per staging item (256 threads per K or V tile)
+    static constexpr int KPITCH = HD * 2 + 16;   // bytes per K row in LDS (f16)
+    static constexpr int VRPITCH = HD * 2 + 128; // bytes per V row in LDS (f16)
+    static constexpr int KBYTES = N * KPITCH;
+    static constexpr int VBYTES = N * VRPITCH;
+    static constexpr int KFLAG = 64;             // [3][N] key valid bytes
+    static constexpr int KB0 = KFLAG + 3 * N;    // two K buffers
+    static constexpr int VB0 = KB0 + 2 * KBYTES; // two V buffers
+    static constexpr int BYTES = VB0 + 2 * VBYTES;
+    static_assert(KPI >= 1 && N * PARTS == 256 * KPI, "one staging item per thread of a half");
+};
+
+struct pp_hdr {
+    uint32_t tile_bad[2];  // tile index whose keys include an invalid page
+    uint32_t big_at;       // bf16 pages: interval that staged a value beyond f16's range
+};
+
+// Block-table entries per staging item for the ping-pong kernel (keys of an
+// item share one page when block_tokens is a multiple of it).
+template <int HD>
+constexpr uint32_t pp_item_keys() { return (uint32_t)ppg<HD>::KPI; }
+
+template <int DT, int HD>
+__device__ __forceinline__ void prefill_pp(
+    const float* __restrict__ q, const uint8_t* __restrict__ pool,
+    const uint32_t* __restrict__ bt_all, uint32_t bt_stride, uint32_t bt_entries,
+    const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ start_pos,
+    const uint32_t* __restrict__ pos_ptr, uint32_t q_tokens, uint32_t pos_offset,
+    float* __restrict__ out, uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens,
+    int bt_shift, uint32_t row_bytes, float scale_log2, uint64_t n_blocks, uint8_t* smem,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale) {
+    static_assert(DT == DT_F16 || DT == DT_BF16 || DT == DT_FP8, "f16-staged pages only");
+    constexpr bool B2H = DT == DT_BF16;
+    constexpr bool F8 = DT == DT_FP8;
+    typedef op_t<DT_F16> O;
+    typedef f16x8 opv;
+    typedef ppg<HD> G;
+    constexpr int N = G::N;
+    constexpr int SUB = G::SUB;
+    constexpr int KPI = G::KPI;
+    constexpr uint32_t SE = F8 ? 1u : 2u;  // stored element bytes
+
+    // ---- workgroup order: as prefill() (longest row block first)
+    const uint32_t gx = gridDim.x, gy = gridDim.y;
+    const uint32_t pairs = gy * gridDim.z;
+    const uint32_t d = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const uint32_t tile = gx - 1u - d / pairs;
+    const uint32_t hk = (d % pairs) % gy;
+    const uint32_t b = (d % pairs) / gy;
+
+    uint32_t qoff, n_q, p0;
+    const uint32_t* bt;
+    if (cu_q) {
+        qoff = min(cu_q[b], q_tokens);
+        const uint32_t end = min(cu_q[b + 1], q_tokens);
+        n_q = end > qoff ? end - qoff : 0u;
+        p0 = start_pos[b];
+        bt = bt_all + (uint64_t)b * bt_stride;
+    } else {
+        qoff = 0;
+        n_q = q_tokens;
+        p0 = pos_ptr ? pos_ptr[0] : pos_offset;
+        bt = bt_all;
+    }
+    const uint32_t group = n_head / n_head_kv;
+    const uint32_t rows = n_q * group;
+    const uint32_t row0 = tile * ROWS;
+    if (row0 >= rows) return;  // uniform over the workgroup
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;  // 0: waves 0-3 (stage K), 1: waves 4-7 (stage V)
+    const int l32 = lane & 31;
+    const int h = lane >> 5;
+    const uint32_t vtr_off = (4 * h + ((lane & 15) >> 2)) * G::VRPITCH +
+                             (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
+
+    const uint32_t row_raw = row0 + wave * 32 + l32;
+    const bool row_ok = row_raw < rows;
+    const uint32_t row = row_ok ? row_raw : rows - 1u;
+    const uint32_t tok = row / group;
+    const uint32_t head = hk * group + (row - tok * group);
+    const uint64_t cap = (uint64_t)bt_entries * block_tokens - 1u;
+    auto clamp_pos = [&](uint32_t t) -> uint32_t {
+        const uint64_t v = (uint64_t)p0 + t;
+        return (uint32_t)(v < cap ? v : cap);
+    };
+    const uint32_t lim = clamp_pos(tok);
+    const uint32_t wr0 = min(row0 + wave * 32u, rows - 1u);
+    const uint32_t wave_min = clamp_pos(wr0 / group);
+    const uint32_t kmax = clamp_pos(min(row0 + ROWS - 1u, rows - 1u) / group);
+    const uint32_t n_tiles = kmax / N + 1u;
+
+    pp_hdr* hdr = reinterpret_cast<pp_hdr*>(smem);
+    uint8_t* kflag = smem + G::KFLAG;
+    uint8_t* kbuf0 = smem + G::KB0;
+    uint8_t* vbuf0 = smem + G::VB0;
+
+    // ---- staging item of this thread: keys KPI*kg .. of a tile, 8-element
+    // chunk `part` of the kv head's K row (waves 0-3) or V row (waves 4-7)
+    const int sti = tid & 255;
+    const int part = sti % G::PARTS;
+    const int kg = sti / G::PARTS;
+    const uint64_t page_bytes = (uint64_t)block_tokens * 2u * row_bytes;
+    const uint32_t slot_bytes = 2u * row_bytes;
+    const uint32_t src_off = (grp ? row_bytes : 0u) + hk * HD * SE + part * 8u * SE;
+    auto entry_of = [&](uint32_t key) -> uint32_t {
+        return bt_shift >= 0 ? (key >> bt_shift) : key / block_tokens;
+    };
+    // The table entry of this item's keys in the next tile to issue is read
+    // one tile ahead and checked only when that tile is issued: a check right
+    // after the load would wait for every load in flight.  (bt_entries >= 1.)
+    uint32_t ph_e = entry_of(KPI * kg);
+    uint32_t ph = bt[min(ph_e, bt_entries - 1u)];
+    u32x4 r[KPI];
+    uint32_t okb = 0;  // bit j: key KPI*kg+j loadable; bit KPI+j: key <= kmax on a bad page
+    // Staging comes in pieces so that an MFMA phase can run them between its
+    // MFMAs (issue_addr, issue_key(j), issue_page; commit_key(j), commit_flags).
+    const uint8_t* ip = pool;  // address of key 0 of the item being issued
+    uint32_t istep = 0;        // bytes between its keys
+    auto issue_addr = [&](uint32_t t) {
+        const uint32_t key0 = t * N + KPI * kg;
+        const uint32_t slot = key0 - ph_e * block_tokens;
+        const bool pv = ph_e < bt_entries && (uint64_t)ph < n_blocks;
+        // an invalid page reads page 0 (in bounds; its keys are masked)
+        ip = pool + (uint64_t)(pv ? ph : 0u) * page_bytes + (pv ? slot * slot_bytes : 0u) + src_off;
+        istep = pv ? slot_bytes : 0u;
+        okb = 0;
+#pragma unroll
+        for (int j = 0; j < KPI; ++j) {
+            const bool live = key0 + j <= kmax;
+            okb |= (live && pv ? 1u : 0u) << j;
+            okb |= (live && !pv ? 1u : 0u) << (KPI + j);
+        }
+    };
+    auto issue_key = [&](int j) {
+        if constexpr (F8) {
+            const u32x2 a = *reinterpret_cast<const u32x2*>(ip + j * istep);
+            r[j] = u32x4{a[0], a[1], 0u, 0u};
+        } else {
+            r[j] = *reinterpret_cast<const u32x4*>(ip + j * istep);
+        }
+    };
+    auto issue_page = [&](uint32_t t) {  // the table entry for tile t + 1
+        if (t + 1 < n_tiles) {
+            ph_e = entry_of((t + 1) * N + KPI * kg);
+            ph = bt[min(ph_e, bt_entries - 1u)];
+        }
+    };
+    auto issue = [&](uint32_t t) {
+        issue_addr(t);
+#pragma unroll
+        for (int j = 0; j < KPI; ++j) issue_key(j);
+        issue_page(t);
+    };
+    // key j of the issued item into its tile buffer (bf16: widened, emax
+    // gathering the range check)
+    auto commit_key = [&](uint32_t t, int j, u16x2& emax) {
+        const int bb = t & 1;
+        u32x4 w = r[j];
+        if constexpr (F8) w = e4m3x8_to_f16(w[0], w[1]);
+        if constexpr (B2H) w = bf16x8_to_f16(w, emax);
+        if (grp == 0) {
+            *reinterpret_cast<u32x4*>(kbuf0 + bb * G::KBYTES + (KPI * kg + j) * G::KPITCH +
+                                      part * 16) = w;
+        } else {
+            // keys past the window or on a bad page: zero rows (their weights
+            // are 0, and 0 * a non-finite pool value would not be)
+            const bool z = !((okb >> j) & 1u);
+            *reinterpret_cast<u32x4*>(vbuf0 + bb * G::VBYTES + (KPI * kg + j) * G::VRPITCH +
+                                      part * 16) = z ? u32x4{0u, 0u, 0u, 0u} : w;
+        }
+    };
+    // the item's key flags (K stagers) and the bf16 range flag (interval `iv`)
+    auto commit_flags = [&](uint32_t t, uint32_t iv, u16x2 emax) {
+        const int bb = t & 1;
+        if constexpr (B2H) {
+            if (emax[0] >= BF16_F16_LIMIT || emax[1] >= BF16_F16_LIMIT) hdr->big_at = iv;
+        }
+        if (grp == 0) {
+            if (part == 0) {
+                uint32_t f = 0;
+#pragma unroll
+                for (int j = 0; j < KPI; ++j) f |= ((okb >> j) & 1u) << (8 * j);
+                // three flag buffers: tile t's are written during interval 2t-2
+                // and read by the softmaxes at 2t+1 and 2t+2
+                uint8_t* fl = kflag + (t % 3u) * N;
+                if constexpr (KPI == 4)
+                    *reinterpret_cast<uint32_t*>(fl + 4 * kg) = f;
+                else if constexpr (KPI == 2)
+                    *reinterpret_cast<uint16_t*>(fl + 2 * kg) = (uint16_t)f;
+                else
+                    fl[kg] = (uint8_t)f;
+            }
+            if (okb >> KPI) hdr->tile_bad[bb] = t;
+        }
+    };
+    auto commit = [&](uint32_t t, uint32_t iv) {
+        u16x2 emax = {0, 0};
+#pragma unroll
+        for (int j = 0; j < KPI; ++j) commit_key(t, j, emax);
+        commit_flags(t, iv, emax);
+    };
+
+    // ---- q operands (as prefill(): scaled per wave by a power of two, split
+    // hi + lo f16 behind opaque())
+    constexpr int QSTEPS = HD / O::KS;
+    const float qscale = scale_log2 * (F8 ? k_scale[hk] : 1.0f);
+    opv qa[QSTEPS], qb[QSTEPS];
+    float qdown;
+    {
+        const float* qrow = q + ((uint64_t)(qoff + tok) * n_head + head) * HD;
+        float4 a[QSTEPS], c[QSTEPS];
+        float amax = 0.0f;
+#pragma unroll
+        for (int t = 0; t < QSTEPS; ++t) {
+            a[t] = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h);
+            c[t] = *reinterpret_cast<const float4*>(qrow + 16 * t + 8 * h + 4);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a[t].x), fabsf(a[t].y)),
+                                     fmaxf(fabsf(a[t].z), fabsf(a[t].w))));
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(c[t].x), fabsf(c[t].y)),
+                                     fmaxf(fabsf(c[t].z), fabsf(c[t].w))));
+        }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        amax = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                             __builtin_bit_cast(int, amax))) * qscale;
+        const int qe = q_exponent(amax);
+        const float up = __builtin_amdgcn_ldexpf(qscale, qe);
+        qdown = __builtin_amdgcn_ldexpf(1.0f, -qe);
+#pragma unroll
+        for (int t = 0; t < QSTEPS; ++t) {
+            float x[8] = {a[t].x * up, a[t].y * up, a[t].z * up, a[t].w * up,
+                          c[t].x * up, c[t].y * up, c[t].z * up, c[t].w * up};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) opaque(x[e]);
+            pack8<DT_F16>(x, qa[t], qb[t]);
+        }
+    }
+
+    f32x16 acc[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) acc[i] = f32x16{};
+    float m_run = -1e30f, l_run = 0.f;
+    f32x16 sv[SUB];   // scores of the tile between a wave's MFMA phase and its softmax
+    opv pf[SUB][2];   // f16 weights of the tile between its softmax and the next MFMA phase
+
+    // a barrier that waits for this wave's LDS traffic only
+    auto bar = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // every wave reads the flag after the same barrier: a value set during
+    // interval iv is acted on at the start of interval iv + 1
+    auto big_seen = [&](uint32_t iv) -> bool {
+        if constexpr (B2H) return hdr->big_at < iv;
+        else return false;
+    };
+
+    // MFMA phase: O^T += V^T P^T for tile j-1 (pv), then S^T = K Q^T for tile j
+    // (sc).  In this phase no other wave of the SIMD issues MFMAs, so each
+    // operand is read from LDS ahead of its MFMA (P.V: PV_AHEAD MFMAs ahead;
+    // S: one step ahead) and the order is pinned with sched_barrier: left to
+    // itself the scheduler read each K operand right before its MFMAs and the
+    // matrix unit idled through every LDS round trip (a 48-MFMA phase took
+    // ~3000 cycles for 1536 of MFMA work).  The two score blocks' chains and
+    // the four P.V accumulators interleave; each accumulator sees its MFMAs
+    // in the order of prefill().
+    static_assert(SUB == 2, "two 32-key score blocks per tile");
+    bool bad_nx = false;  // tile of the next softmax holds a key on an invalid page
+    constexpr int NPV = SUB * 2 * (HD / 32);  // P.V MFMAs per tile: (sb, st, db)
+    constexpr int PV_AHEAD = 4;
+    constexpr uint32_t NONE = 0xFFFFFFFFu;
+    auto mma_phase = [&](uint32_t j, bool pv, bool sc, uint32_t commit_t = NONE,
+                         uint32_t issue_t = NONE, uint32_t iv = 0) {
+        // the MFMA phase issues ahead of the other half's softmax on the SIMD
+        // (without it the older waves 0-3 won every issue conflict and
+        // waves 4-7 ran both of their phases late)
+        __builtin_amdgcn_s_setprio(1);
+        const uint8_t* vtr = vbuf0 + ((j - 1u) & 1u) * G::VBYTES + vtr_off;
+        const uint8_t* kr = kbuf0 + (j & 1u) * G::KBYTES + l32 * G::KPITCH + 16 * h;
+        // operand of P.V MFMA i: sub-block i / (2 HD/32), step (i / (HD/32)) % 2, dims block i % (HD/32)
+        auto vread = [&](int i) -> opv {
+            const int sb = i / (2 * (HD / 32)), st = (i / (HD / 32)) & 1, db = i % (HD / 32);
+            const uint8_t* vp = vtr + (sb * 32 + 16 * st) * G::VRPITCH + db * 64;
+            const uint64_t r0 = lds_read_tr(vp);
+            const uint64_t r1 = lds_read_tr(vp + 8 * G::VRPITCH);
+            return __builtin_bit_cast(opv, u32x4{(uint32_t)r0, (uint32_t)(r0 >> 32), (uint32_t)r1,
+                                                 (uint32_t)(r1 >> 32)});
+        };
+        auto kread = [&](int t, int sb) -> opv {
+            return *reinterpret_cast<const opv*>(kr + sb * 32 * G::KPITCH + 32 * t);
+        };
+        opv ka0, ka1;
+        if (sc) {
+            ka0 = kread(0, 0);
+            ka1 = kread(0, 1);
+        }
+        if (pv) {
+            opv vq[PV_AHEAD];
+#pragma unroll
+            for (int i = 0; i < PV_AHEAD; ++i) vq[i] = vread(i);
+            // staging rides in the MFMA phase, while its first operand reads
+            // are in flight: this thread's item of tile commit_t goes to LDS,
+            // then its loads of tile issue_t go out.  (In the softmax phase it
+            // made that phase the longer one; spread between the MFMAs it
+            // measured slower still.)
+            __builtin_amdgcn_sched_barrier(0);
+            if (commit_t != NONE) {
+                commit(commit_t, iv);
+                if (issue_t != NONE) issue(issue_t);
+            }
+#pragma unroll
+            for (int i = 0; i < NPV; ++i) {
+                __builtin_amdgcn_sched_barrier(0);
+                const int db = i % (HD / 32);
+                const int sb = i / (2 * (HD / 32)), st = (i / (HD / 32)) & 1;
+                acc[db] = O::mma(vq[i % PV_AHEAD], pf[sb][st], acc[db]);
+                if (i + PV_AHEAD < NPV) vq[i % PV_AHEAD] = vread(i + PV_AHEAD);
+            }
+        }
+        if (sc) {
+            // the next softmax is tile j's: its page flag is read here, where
+            // the LDS round trip hides under the MFMAs
+            bad_nx = hdr->tile_bad[j & 1u] == j;
+            f32x16 s0 = f32x16{}, s1 = f32x16{};
+#pragma unroll
+            for (int t = 0; t < QSTEPS; ++t) {
+                __builtin_amdgcn_sched_barrier(0);
+                opv kn0 = ka0, kn1 = ka1;
+                if (t + 1 < QSTEPS) {
+                    kn0 = kread(t + 1, 0);
+                    kn1 = kread(t + 1, 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // step t+1's reads go out before step t's MFMAs
+                s0 = O::mma(ka0, qa[t], s0);
+                s1 = O::mma(ka1, qa[t], s1);
+                s0 = O::mma(ka0, qb[t], s0);
+                s1 = O::mma(ka1, qb[t], s1);
+                ka0 = kn0;
+                ka1 = kn1;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            sv[0] = s0;
+            sv[1] = s1;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // softmax phase for tile j: mask, one running-max update, weights (f16,
+    // in the P^T layout of the next MFMA phase) and their row sums
+    auto softmax = [&](uint32_t j) {
+        const int bb = j & 1;
+        const bool bad = bad_nx;
+#pragma unroll
+        for (int sb = 0; sb < SUB; ++sb) {
+            const uint32_t kb = j * N + sb * 32;
+            if (bad || kb + 31u > wave_min) {
+                const uint8_t* fl = kflag + (j % 3u) * N + sb * 32;
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int ko = 8 * g4 + 4 * h;
+                    const uint32_t f = bad ? *reinterpret_cast<const uint32_t*>(fl + ko) : 0x01010101u;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool ok = (kb + ko + e <= lim) && ((f >> (8 * e)) & 1u);
+                        sv[sb][4 * g4 + e] = ok ? sv[sb][4 * g4 + e] : -__builtin_inff();
+                    }
+                }
+            }
+        }
+        {
+            float mx = sv[0][0];
+#pragma unroll
+            for (int sb = 0; sb < SUB; ++sb)
+#pragma unroll
+                for (int r2 = 0; r2 < 16; ++r2) mx = fmaxf(mx, sv[sb][r2]);
+            mx = max_halves(mx) * qdown;
+            if (__builtin_amdgcn_ballot_w64(mx > m_run + RESCALE_LOG2)) {
+                const float mn = fmaxf(m_run, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+                l_run *= alpha;
+#pragma unroll
+                for (int i = 0; i < HD / 32; ++i) acc[i] *= alpha;
+                m_run = mn;
+            }
+        }
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        const f16x2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                opv pv;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    pv[e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sv[sb][8 * st + e], qdown, -m_run));
+                pf[sb][st] = pv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    l_run = __builtin_amdgcn_fdot2(f16x2{pv[2 * e], pv[2 * e + 1]}, one2, l_run, false);
+            }
+        }
+        // the weights and sums are made here, before the barrier that ends
+        // the phase: the optimiser otherwise sank the exponentials into the
+        // MFMA phase that consumes them
+#pragma unroll
+        for (int sb = 0; sb < SUB; ++sb)
+#pragma unroll
+            for (int st = 0; st < 2; ++st) asm volatile("" : "+v"(pf[sb][st]));
+        asm volatile("" : "+v"(l_run));
+    };
+
+    // ---- prologue: page ids and the first tile's loads, q, then K(0)
+    if (tid == 0) {
+        hdr->tile_bad[0] = 0xFFFFFFFFu;
+        hdr->tile_bad[1] = 0xFFFFFFFFu;
+        hdr->big_at = 0xFFFFFFFFu;
+    }
+    issue(0);
+    {  // tile -1 (see the main loop): its V buffer (1) holds zeros
+        u32x4* z = reinterpret_cast<u32x4*>(vbuf0 + G::VBYTES);
+        for (int i = tid; i < G::VBYTES / 16; i += NT) z[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int sb = 0; sb < SUB; ++sb)
+#pragma unroll
+        for (int r2 = 0; r2 < 16; ++r2) sv[sb][r2] = -__builtin_inff();
+#pragma unroll
+    for (int sb = 0; sb < SUB; ++sb) pf[sb][0] = pf[sb][1] = opv{};
+    bar();  // header initialised
+    if (grp == 0) {
+        commit(0, 0);
+        if (n_tiles > 1) issue(1);
+    }
+    bar();
+
+    // ---- main loop: interval 2j has number 2j + 1 (the prologue is 0)
+    // Both loops run the same body for every tile, the first one included
+    // (with a first iteration of their own the compiler peeled it, and the
+    // loads it issued into other registers made it wait for every load in
+    // flight at the head of each MFMA phase).  Tile -1 is a zero tile: its
+    // scores are -inf, its weights 0 and its V buffer zeroed in the prologue,
+    // so its P.V adds exact zeros and its softmax changes nothing.
+    bool exact = false;
+    if (grp == 0) {
+        for (uint32_t j = 0; j < n_tiles; ++j) {
+            if (big_seen(2 * j + 1)) { exact = true; break; }
+            mma_phase(j, true, true, j + 1 < n_tiles ? j + 1 : NONE, j + 2 < n_tiles ? j + 2 : NONE,
+                      2 * j + 1);
+            bar();
+            if (big_seen(2 * j + 2)) { exact = true; break; }
+            softmax(j);
+            bar();
+        }
+        if (!exact) {
+            mma_phase(n_tiles, true, false);
+            bar();
+            bar();
+        }
+    } else {
+        for (uint32_t j = 0; j < n_tiles; ++j) {
+            if (big_seen(2 * j + 1)) { exact = true; break; }
+            softmax(j - 1u);
+            bar();
+            if (big_seen(2 * j + 2)) { exact = true; break; }
+            mma_phase(j, true, true, j, j + 1 < n_tiles ? j + 1 : NONE, 2 * j + 2);
+            bar();
+        }
+        if (!exact) {
+            softmax(n_tiles - 1);
+            bar();
+            mma_phase(n_tiles, true, false);
+            bar();
+        }
+    }
+    if constexpr (B2H) {
+        if (exact) {  // uniform over the workgroup: every wave broke at the same interval
+            bar();
+            prefill<DT_BF16, HD>(q, pool, bt_all, bt_stride, bt_entries, cu_q, start_pos, pos_ptr,
+                                 q_tokens, pos_offset, out, n_head, n_head_kv, block_tokens,
+                                 bt_shift, row_bytes, scale_log2, n_blocks, smem, k_scale,
+                                 v_scale);
+            return;
+        }
+    }
+
+    // ---- epilogue: combine the two halves' sums, normalise, store
+    const float l_tot = sum_halves(l_run);
+    const float inv = l_tot > 0.f ? (F8 ? v_scale[hk] : 1.0f) / l_tot : 0.f;
+    if (row_ok) {
+        float* orow = out + ((uint64_t)(qoff + tok) * n_head + head) * HD;
+#pragma unroll
+        for (int db = 0; db < HD / 32; ++db) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int dd = db * 32 + 8 * g4 + 4 * h;
+                *reinterpret_cast<float4*>(orow + dd) =
+                    make_float4(acc[db][4 * g4 + 0] * inv, acc[db][4 * g4 + 1] * inv,
+                                acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 #define EH_PREFILL(DTN, DT, HD)                                                                   \
@@ -776,3 +1340,28 @@ EH_PREFILL(f32, DT_F32, 64)
 EH_PREFILL(f32, DT_F32, 128)
 EH_PREFILL(fp8, DT_FP8, 64)
 EH_PREFILL(fp8, DT_FP8, 128)
+
+// Ping-pong kernels (f16-staged pages, block_tokens a multiple of
+// pp_item_keys<HD>()); bf16 reserves the LDS of prefill() for its exact restart.
+#define EH_PREFILL_PP(DTN, DT, HD)                                                                \
+    extern "C" __global__ __launch_bounds__(NT, 1) void eh_prefill_pp_##DTN##_hd##HD(           \
+        const float* q, const uint8_t* pool, const uint32_t* bt, uint32_t bt_stride,             \
+        uint32_t bt_entries, const uint32_t* cu_q, const uint32_t* start_pos,                    \
+        const uint32_t* pos_ptr, uint32_t q_tokens, uint32_t pos_offset, float* out,             \
+        uint32_t n_head, uint32_t n_head_kv, uint32_t block_tokens, int bt_shift,                \
+        uint32_t row_bytes, float scale_log2, uint64_t n_blocks, const float* k_scale,           \
+        const float* v_scale) {                                                                  \
+        constexpr int OLD = 64 + SLICE * 4 + 2 * geo<DT, HD>::N + 2 * geo<DT, HD>::STAGE;        \
+        constexpr int BYTES = (DT == DT_BF16 && OLD > ppg<HD>::BYTES) ? OLD : ppg<HD>::BYTES;   \
+        __shared__ __attribute__((aligned(16))) uint8_t smem[BYTES];                             \
+        prefill_pp<DT, HD>(q, pool, bt, bt_stride, bt_entries, cu_q, start_pos, pos_ptr,         \
+                           q_tokens, pos_offset, out, n_head, n_head_kv, block_tokens, bt_shift, \
+                           row_bytes, scale_log2, n_blocks, smem, k_scale, v_scale);             \
+    }
+
+EH_PREFILL_PP(f16, DT_F16, 64)
+EH_PREFILL_PP(f16, DT_F16, 128)
+EH_PREFILL_PP(bf16, DT_BF16, 64)
+EH_PREFILL_PP(bf16, DT_BF16, 128)
+EH_PREFILL_PP(fp8, DT_FP8, 64)
+EH_PREFILL_PP(fp8, DT_FP8, 128)
