@@ -1289,6 +1289,10 @@ __device__ __forceinline__ void prefill_pp(
     if constexpr (B2H) {
         if (exact) {  // uniform over the workgroup: every wave broke at the same interval
             bar();
+            // (inlined: with the restart in the kernel the bf16 kernel keeps 4
+            // VGPRs of the prologue in scratch across the tile loops, stored once
+            // before them and reloaded once after; as a called function the
+            // kernel would carry 468 bytes of scratch per lane instead)
             prefill<DT_BF16, HD>(q, pool, bt_all, bt_stride, bt_entries, cu_q, start_pos, pos_ptr,
                                  q_tokens, pos_offset, out, n_head, n_head_kv, block_tokens,
                                  bt_shift, row_bytes, scale_log2, n_blocks, smem, k_scale,
