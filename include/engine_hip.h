@@ -472,10 +472,16 @@ eh_status eh_append_decode_batched_e4m3(eh_context* ctx, eh_stream stream,
  * attends keys 0..=p0+i through the block table (flash_attention_2.cu:44-68);
  * a row with no valid key is zero.  Size checks follow
  * flash_attention.rs:142-164 (q, out, ceil((pos_offset+q_tokens)/block_tokens)
- * table entries).  QK^T and PV run on MFMA: f16 KV with f16 operands, bf16 KV
- * with hi+lo bf16 operand pairs, f32 KV with f32 MFMA.  head_dim 64 or 128.
- * Keys whose block-table entry lies past the table or past the pool are
- * masked. */
+ * table entries).  QK^T and PV run on MFMA: f16 KV with f16 operands (q as
+ * hi + lo f16 halves for the scores); bf16 KV widened to f16 as it is staged
+ * (exact below 2^16), a tile holding a larger value on bf16 MFMAs with hi + lo
+ * bf16 operand pairs; f32 KV with f32 MFMA.  head_dim 64 or 128.  Keys whose
+ * block-table entry lies past the table or past the pool are masked.  bf16
+ * pages run the ping-pong kernel (the workgroup's halves alternate MFMA and
+ * softmax phases), the other types the single-phase kernel; at head_dim 128
+ * both give bit-identical outputs.  The environment variable
+ * EH_PREFILL_KERNEL=single or =pp, read at each call, overrides that choice
+ * for 16-bit and E4M3 pages (a diagnostic). */
 eh_status eh_flash_attention_prefill(eh_context* ctx, eh_stream stream, uint32_t kv_dtype,
                                      const float* q, uint64_t q_bytes, const void* pool,
                                      uint64_t pool_bytes, const uint32_t* block_table,
