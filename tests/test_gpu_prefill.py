@@ -154,6 +154,39 @@ def test_bf16_values_beyond_f16_range(dev, hd, nh, nkv):
     check_close(g, ref, KvDataType.BF16, "bf16 beyond f16 range", stress=True)
 
 
+@pytest.mark.parametrize("which", ["k", "v"])
+def test_bf16_late_tile_beyond_f16_range(dev, monkeypatch, which):
+    """One bf16 value of magnitude >= 2^16 in the K (or V) rows of a late tile
+    only: the ping-pong kernel stages K and V on different halves of the
+    workgroup, so each half's range flag is met mid-run, after many tiles on
+    the f16 path; every workgroup then restarts on the exact path.  Against
+    the oracle and bit-identical to the single-phase kernel."""
+    nh, nkv, hd, bt, p0, nq = 32, 8, 128, 16, 1500, 200
+    rng = np.random.default_rng(515 + (which == "v"))
+    total = p0 + nq
+    n_pages = -(-total // bt)
+    pool_pages = n_pages + 3
+    table = rng.permutation(pool_pages)[:n_pages].astype(np.uint32)
+    host = rng.standard_normal((pool_pages, bt, 2, nkv, hd)).astype(np.float32)
+    page = table[1400 // bt]  # key 1400 + slot: tile 21 of 27
+    host[page, 7, 0 if which == "k" else 1, 3, 5] = -2.0e5 if which == "k" else 7.5e4
+    t = torch.from_numpy(host.reshape(-1)).to(torch.bfloat16)
+    dpool, hpool = t.to(dev), t.to(torch.float32).numpy()
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    outs = {}
+    for kern in ("single", "pp"):
+        monkeypatch.setenv("EH_PREFILL_KERNEL", kern)
+        out = torch.full((nq, nh, hd), float("nan"), device=dev)
+        FlashAttention2(0).launch(None, torch.from_numpy(q).to(dev), dpool, i32(table, dev), out,
+                                  nh, nkv, hd, bt, nq, p0, kv_dtype=KvDataType.BF16)
+        torch.cuda.synchronize()
+        outs[kern] = out.cpu().numpy()
+    assert np.array_equal(outs["pp"].view(np.uint32), outs["single"].view(np.uint32))
+    ref = orc.prefill_causal(hpool, table, bt, q, nq, p0, nh, nkv, hd)
+    assert np.abs(ref).max() > (100.0 if which == "v" else 0.0)  # the large V value reaches the output
+    check_close(outs["pp"], ref, KvDataType.BF16, f"bf16 late {which}", stress=which == "v")
+
+
 @pytest.mark.parametrize("kstd", [4.0, 16.0, 64.0])
 @pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16])
 def test_large_keys_within_f16_range(dev, dtype, kstd):
