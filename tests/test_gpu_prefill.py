@@ -523,3 +523,78 @@ def test_prefill_random_sweep(dev, seed):
         ref = orc.prefill_causal(hpool, tables[b, :pages[b]], bt, q[cu[b]:cu[b + 1]], int(n),
                                  int(s), nh, nkv, hd)
         check_close(g[cu[b]:cu[b + 1]], ref, dtype, f"prefill sweep {seed} seq {b}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_pingpong_random_sweep(dev, monkeypatch, seed):
+    """The two prefill kernels on seeded random shapes: f16, bf16 and E4M3
+    pages; head_dim 64 or 128; 1-8 kv heads with 1-8 q heads each; pages of
+    4-64 tokens; 1-5 sequences with chunks of 1-700 tokens on contexts of
+    0-3000; up to two table entries pointing outside the pool.  Bit-identical
+    at head_dim 128 (both walk 64-key tiles), within the bar of each other at
+    64; every fourth shape also against the oracle (sequences without an
+    invalid entry)."""
+    rng = np.random.default_rng(90_000 + seed)
+    dtype = (KvDataType.F16, KvDataType.BF16, KvDataType.FP8)[int(rng.integers(3))]
+    hd = int(rng.choice([64, 128, 128]))
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 3, 4, 6, 7, 8]))
+    bt = int(rng.choice([4, 8, 16, 32, 64]))
+    B = int(rng.integers(1, 6))
+    starts = rng.choice([0, 0, bt - 1, bt, int(rng.integers(1, 3000))], B).astype(np.int64)
+    lens = rng.integers(1, 700, B).astype(np.int64)
+    nh = g * nkv
+    print(f"[pp sweep {seed}] {dtype.name} heads {nh}/{nkv} hd {hd} page {bt} "
+          f"starts {starts.tolist()} lens {lens.tolist()}", flush=True)
+    pages = [-(-(int(s0) + int(n)) // bt) for s0, n in zip(starts, lens)]
+    stride = max(pages) + int(rng.integers(0, 3))
+    n_pages = sum(pages) + 2
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    tables = np.full((B, stride), 0xFFFFFFFF, np.uint32)
+    o = 0
+    for b, k in enumerate(pages):
+        tables[b, :k] = perm[o:o + k]
+        o += k
+    bad_seqs = set()
+    for _ in range(int(rng.integers(0, 3))):
+        b = int(rng.integers(B))
+        tables[b, int(rng.integers(pages[b]))] = n_pages + 5 + int(rng.integers(100))
+        bad_seqs.add(b)
+    total = int(lens.sum())
+    q = rng.standard_normal((total, nh, hd)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    fa = FlashAttention2(0)
+    if dtype == KvDataType.FP8:
+        codes, ks, vs = gauss_codes(rng, n_pages, bt, nkv, hd)
+        dpool = torch.from_numpy(codes).to(dev)
+        f = orc.e4m3_to_f32(codes).reshape(n_pages, bt, 2, nkv, hd)
+        f[:, :, 0] *= ks[None, None, :, None]
+        f[:, :, 1] *= vs[None, None, :, None]
+        hpool = f.reshape(-1)
+        dks, dvs = torch.from_numpy(ks).to(dev), torch.from_numpy(vs).to(dev)
+    else:
+        dpool, hpool = make_pool(rng, n_pages, bt, nkv, hd, dtype, dev)
+    outs = {}
+    for kern in ("single", "pp"):
+        monkeypatch.setenv("EH_PREFILL_KERNEL", kern)
+        out = torch.full((total, nh, hd), float("nan"), device=dev)
+        args = (None, torch.from_numpy(q).to(dev), dpool, i32(tables, dev), i32(cu, dev),
+                i32(np.array(starts, np.uint32), dev), out, nh, nkv, hd, bt, int(lens.max()))
+        if dtype == KvDataType.FP8:
+            fa.launch_batched_e4m3(*args, dks, dvs)
+        else:
+            fa.launch_batched(*args, kv_dtype=dtype)
+        torch.cuda.synchronize()
+        outs[kern] = out.cpu().numpy()
+    if hd == 128:
+        assert np.array_equal(outs["pp"].view(np.uint32), outs["single"].view(np.uint32))
+    else:
+        check_close(outs["pp"], outs["single"], KvDataType.F16, "pp vs single-phase")
+    if seed % 4 == 0:
+        for b in range(B):
+            if b in bad_seqs:
+                continue
+            ref = orc.prefill_causal(hpool, tables[b, :pages[b]], bt, q[cu[b]:cu[b + 1]],
+                                     int(lens[b]), int(starts[b]), nh, nkv, hd)
+            check_close(outs["pp"][cu[b]:cu[b + 1]], ref,
+                        KvDataType.F16 if dtype == KvDataType.FP8 else dtype, f"pp seq {b}")
