@@ -269,6 +269,13 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
                          uint32_t head_dim, uint32_t block_tokens, uint32_t max_ctx,
                          uint32_t tokens_per_split_hint, uint32_t* tokens_per_split,
                          uint32_t* max_splits, uint64_t* workspace_bytes);
+/* Workspace bytes of a token-balanced decode call launched with `grid`
+ * workgroups, for callers that pass a grid of their own instead of the
+ * plan's to the calls taking one (eh_append_decode_batched[_e4m3],
+ * eh_decode_schedule / eh_append_decode_scheduled, and max_splits of the
+ * batched decodes): 4 * (grid + batch) * n_head * 130, the partial states of
+ * every run plus one per sequence (no reference counterpart). */
+uint64_t eh_decode_grid_workspace_bytes(uint32_t grid, uint32_t batch, uint32_t n_head);
 /* Name of the split kernel eh_paged_decode_batched launches for a shape
  * (diagnostics and profiling; no reference counterpart). */
 eh_status eh_decode_kernel_name(uint32_t kv_dtype, uint32_t n_head, uint32_t n_head_kv,

@@ -67,7 +67,7 @@ def run_decode(dev, dtype, lens, shape, seed, grid=None, tab=None, nb=None):
     plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(max(lens)), 0, dtype)
     assert plan[0] == 0, "shape should take the token-balanced kernel"
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, B, n_head)
     ws = PagedAttention.workspace(plan)
     out = torch.full((B, n_head, hd), float("nan"), device=dev)
     PagedAttention(0).decode_batched(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
@@ -212,7 +212,7 @@ def fused_case(dev, dtype, starts, shape, seed, grid=None):
     layout = PagedKvLayout(nb, bt, rl, dtype)
     plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(starts.max()) + 1, 0, dtype)
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, B, n_head)
     ws = PagedAttention.workspace(plan)
     out = torch.full((B, n_head, hd), float("nan"), device=dev)
     PagedAttention(0).append_decode_batched(None, layout, pool, newk.to(dev), newv.to(dev),
@@ -631,7 +631,7 @@ def run_both(dev, shape, pos, seed, dtype=KvDataType.F16, grid=None, layers=1):
     plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, dtype)
     assert plan[0] == 0
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, B, n_head)
     tab, nb, _, _, _, _ = sched_case(dev, shape, pos, seed, dtype)
     layout = PagedKvLayout(nb, bt, n_kv * hd, dtype)
     dtab, dpos = i32(tab, dev), i32(pos, dev)
@@ -671,6 +671,40 @@ def test_scheduled_step_equals_self_scheduled(dev, dtype, shape):
                                   np.asarray(SCHED_POS, np.uint32) + 1, bt, q.cpu().numpy(),
                                   n_head, n_kv, hd)
     check_close(out_b.cpu().numpy(), ref, what="scheduled")
+
+
+def test_grid_workspace_bytes(dev):
+    """A fused step launched with a grid larger than the plan's: the plan's
+    workspace is InvalidSize with expected = eh_decode_grid_workspace_bytes
+    for that grid (4 (grid + batch) n_head 130); with that workspace the step
+    writes the batched append's pool bytes and matches the oracle."""
+    shape = (48, 8, 128, 16)
+    pos = np.array([1300, 7, 0, 640, 15, 16, 999, 31], np.int64)
+    B, n_head = len(pos), shape[0]
+    plan = PagedAttention.plan(B, n_head, 8, 128, 16, int(pos.max()) + 1)
+    grid = plan[1] + 77
+    forced = PagedAttention.with_grid(plan, grid, B, n_head)
+    assert forced == (0, grid, 4 * (grid + B) * n_head * 130)
+    assert forced[2] > plan[2]
+    tab, nb, pool, k, v, q = sched_case(dev, shape, pos, 4242)
+    layout = PagedKvLayout(nb, 16, 8 * 128, KvDataType.F16)
+    pa = PagedAttention(0)
+    out = torch.full((B, n_head, 128), float("nan"), device=dev)
+    with pytest.raises(HipError) as e:
+        pa.append_decode_batched(None, layout, pool.clone(), k, v, i32(tab, dev), i32(pos, dev), q,
+                                 out, n_head, 128, (0, grid, plan[2]), PagedAttention.workspace(plan))
+    assert e.value.kind == "InvalidSize" and e.value.expected == forced[2]
+    assert e.value.actual == plan[2]
+    pool_ref = pool.clone()
+    cu = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    PagedKvGpu(0).append_kv_batched(None, layout, pool_ref, k, v, i32(tab, dev), cu, i32(pos, dev), B)
+    pa.append_decode_batched(None, layout, pool, k, v, i32(tab, dev), i32(pos, dev), q, out, n_head,
+                             128, forced, PagedAttention.workspace(forced))
+    torch.cuda.synchronize()
+    assert torch.equal(pool.view(torch.int16), pool_ref.view(torch.int16))
+    ref = orc.sdpa_decode_batched(pool.float().cpu().numpy(), tab, pos.astype(np.uint32) + 1, 16,
+                                  q.cpu().numpy(), n_head, 8, 128)
+    check_close(out.cpu().numpy(), ref, what="grid beyond the plan's")
 
 
 def test_scheduled_validation_errors(dev):
@@ -962,7 +996,7 @@ def test_scheduled_step_random_sweep(dev, seed):
     plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, dtype)
     assert plan[0] == 0
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, B, n_head)
     tab, nb, pool, k, v, q = sched_case(dev, shape, pos, 20_000 + seed, dtype)
     layout = PagedKvLayout(nb, bt, n_kv * hd, dtype)
     dtab, dpos = i32(tab, dev), i32(pos, dev)

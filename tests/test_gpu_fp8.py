@@ -129,7 +129,7 @@ def run_decode_e4m3(dev, lens, shape, seed, grid=None, data="gauss"):
     plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(max(lens)), 0, KvDataType.FP8)
     assert plan[0] == 0
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, B, n_head)
     ws = PagedAttention.workspace(plan)
     out = torch.full((B, n_head, hd), float("nan"), device=dev)
     PagedAttention(0).decode_batched_e4m3(None, torch.from_numpy(q).to(dev),
@@ -395,7 +395,7 @@ def test_e4m3_fused_step_matches_separate(dev, shape, grid):
     plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(pos.max()) + 1, 0, KvDataType.FP8)
     assert plan[0] == 0
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, B, n_head)
     lay = PagedKvLayout(nb, bt, rl, KvDataType.FP8)
     t = lambda a: torch.from_numpy(a).to(dev)
     dks, dvs, dq, dtab = t(ks), t(vs), t(q), i32(tab, dev)

@@ -69,7 +69,7 @@ def run(dev, dtype, shape, sink, window, seed, grid=None, lens=LENS):
     plan = PagedAttention.plan(len(lens), n_head, n_kv, hd, bt, int(max(lens)), 0, dtype)
     assert plan[0] == 0
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, len(lens), n_head)
     out = torch.full((len(lens), n_head, hd), float("nan"), device=dev)
     PagedAttention(0).decode_batched_window(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
                                             i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, sink,
@@ -143,7 +143,7 @@ def test_block_mass_matches_oracle(dev, dtype, shape, sink, window, grid):
         pool, pool_f32 = host.to(dev), host.float().numpy()
     plan = PagedAttention.plan(len(LENS), n_head, n_kv, hd, bt, int(max(LENS)), 0, dtype)
     if grid is not None:
-        plan = (0, grid, plan[2])
+        plan = PagedAttention.with_grid(plan, grid, len(LENS), n_head)
     extra = PagedAttention.mass_workspace_bytes(len(LENS), tab.shape[1], bt, n_head)
     ws = torch.zeros((plan[2] + extra + 3) // 4, device=dev)
     mass = torch.full((nb,), 0.5, device=dev)

@@ -74,6 +74,7 @@ _SIGS = {
                                              vp, u64, u32, u32, u32, u32, u32, u32, vp, vp, vp, u64,
                                              u32, vp, u64]),
     "eh_decode_mass_workspace_bytes": (u64, [u32, u32, u32, u32]),
+    "eh_decode_grid_workspace_bytes": (u64, [u32, u32, u32]),
     "eh_append_decode_batched": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, vp, u64, vp, u64,
                                        u32, vp, u32, vp, u64, vp, u64, u32, u32, u32, vp, u64]),
     "eh_decode_schedule_bytes": (u64, [u32, u32, u32, u32]),

@@ -1366,6 +1366,10 @@ uint64_t eh_decode_mass_workspace_bytes(uint32_t batch, uint32_t bt_stride, uint
     return mass_ws_bytes(batch, bt_stride, block_tokens, n_head);
 }
 
+uint64_t eh_decode_grid_workspace_bytes(uint32_t grid, uint32_t batch, uint32_t n_head) {
+    return tiles_ws_bytes(grid, batch, n_head);
+}
+
 static eh_status append_decode_body(eh_context* c, eh_stream stream, const eh_kv_layout* l,
                                     void* pool, uint64_t pool_bytes, const void* keys,
                                     uint64_t keys_bytes, const void* values, uint64_t values_bytes,

@@ -154,6 +154,15 @@ class PagedAttention:
             int(block_tokens), buf(k_scale)[0], buf(v_scale)[0], int(plan[1]), wp, wb))
 
     @staticmethod
+    def with_grid(plan, grid, batch, n_head):
+        """A token-balanced plan launched with `grid` workgroups instead of its
+        own, with the workspace size that grid needs."""
+        if plan[0] != 0:
+            raise ValueError("a grid applies to token-balanced plans (tokens_per_split 0)")
+        return 0, int(grid), int(_lib.load().eh_decode_grid_workspace_bytes(int(grid), int(batch),
+                                                                            int(n_head)))
+
+    @staticmethod
     def mass_workspace_bytes(batch, bt_stride, block_tokens, n_head):
         """Extra workspace decode_batched_window needs when it accumulates block_mass."""
         return int(_lib.load().eh_decode_mass_workspace_bytes(int(batch), int(bt_stride),
