@@ -720,11 +720,13 @@ def suite(args, dev):
               "timed call", "stream_bytes": c_bytes, "ceiling_us": c_us, "best": c_key,
               "sweep_us": sweep, "ceiling_GB/s": round(c_bytes / c_us / 1e3, 1),
               "ceiling_frac_of_8TB/s": round(c_bytes / c_us / 1e3 / 8000.0, 4)})
-        for label, call in (
-                ("fused append + decode (self-scheduled)",
+        k5 = PagedAttention.kernel_name(32, 8, 128, 16, KvDataType.F16)
+        for label, kern, call in (
+                ("fused append + decode (self-scheduled)", k5 + " + eh_decode_tiles_merge",
                  lambda: pa.append_decode_batched(stream, lay5, pool5, nk5, nv5, dtab5, st5, q5,
                                                   o5, 32, 128, plan5, ws5)),
                 ("fused append + decode from a step schedule",
+                 k5 + "_sched + eh_decode_tiles_merge_sched",
                  lambda: pa.append_decode_scheduled(stream, lay5, pool5, nk5, nv5, sched5,
                                                     stride5, q5, o5, 32, 128, plan5, ws5))):
             o5.fill_(float("nan"))
@@ -752,7 +754,7 @@ def suite(args, dev):
                   "frac_of_ceiling": round((b5 / us5) / (c_bytes / c_us), 4),
                   "check_vs_numpy_f64": {"max_abs": float(d.max()), "within_bar": ok,
                                          "appended_rows_bit_exact": bool(app_ok)},
-                  "kernel": PagedAttention.kernel_name(32, 8, 128, 16, KvDataType.F16)})
+                  "kernel": kern})
         del pool5, flush
 
 
