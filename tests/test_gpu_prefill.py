@@ -598,3 +598,88 @@ def test_pingpong_random_sweep(dev, monkeypatch, seed):
                                      int(lens[b]), int(starts[b]), nh, nkv, hd)
             check_close(outs["pp"][cu[b]:cu[b + 1]], ref,
                         KvDataType.F16 if dtype == KvDataType.FP8 else dtype, f"pp seq {b}")
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.BF16, KvDataType.F16, KvDataType.FP8],
+                         ids=lambda d: d.name)
+def test_graph_replay_successive_chunks(dev, dtype):
+    """Batched chunked prefill captured once in a HIP graph, then replayed for
+    successive chunks. Before each replay the caller writes the chunk's q,
+    cu_q and start positions into the captured buffers (eager copies and a
+    synchronisation, as a serving loop does). Every replay equals an eager
+    call on the same inputs bit for bit, and every chunk matches the oracle
+    (f16 bar; E4M3 on decode(code) * scale). Chunks are ragged and one
+    sequence has an empty chunk. bf16 pages run the ping-pong kernel, f16 and
+    E4M3 pages the single-phase kernel."""
+    nh, nkv, hd, bt = 16, 4, 128, 16
+    B, C, n_chunks = 3, 96, 4
+    rng = np.random.default_rng(4100 + int(dtype))
+    ctx0 = np.array([0, 37, 300], np.int64)
+    lens = rng.integers(1, C + 1, size=(n_chunks, B))
+    lens[2, 1] = 0
+    stride = -(-(int(ctx0.max()) + n_chunks * C) // bt) + 1
+    n_pages = B * stride + 3
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    tables = perm[:B * stride].reshape(B, stride).copy()
+    if dtype == KvDataType.FP8:
+        codes, ks, vs = gauss_codes(rng, n_pages, bt, nkv, hd)
+        dpool = torch.from_numpy(codes).to(dev)
+        f = orc.e4m3_to_f32(codes).reshape(n_pages, bt, 2, nkv, hd)
+        f[:, :, 0] *= ks[None, None, :, None]
+        f[:, :, 1] *= vs[None, None, :, None]
+        hpool = f.reshape(-1)
+        dks, dvs = torch.from_numpy(ks).to(dev), torch.from_numpy(vs).to(dev)
+    else:
+        dpool, hpool = make_pool(rng, n_pages, bt, nkv, hd, dtype, dev)
+    fa = FlashAttention2(0)
+    q_s = torch.zeros((B * C, nh, hd), device=dev)
+    cu_s = i32(np.zeros(B + 1, np.uint32), dev)
+    sp_s = i32(np.zeros(B, np.uint32), dev)
+    dtab = i32(tables, dev)
+    out_g = torch.empty_like(q_s)
+    out_e = torch.empty_like(q_s)
+
+    def call(stream, out):
+        if dtype == KvDataType.FP8:
+            fa.launch_batched_e4m3(stream, q_s, dpool, dtab, cu_s, sp_s, out, nh, nkv, hd, bt, C,
+                                   dks, dvs)
+        else:
+            fa.launch_batched(stream, q_s, dpool, dtab, cu_s, sp_s, out, nh, nkv, hd, bt, C,
+                              kv_dtype=dtype)
+
+    call(None, out_g)                                               # warm-up on empty chunks
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call(s, out_g)
+    torch.cuda.synchronize()
+    done = ctx0.copy()
+    for k in range(n_chunks):
+        cu = np.concatenate([[0], np.cumsum(lens[k])]).astype(np.uint32)
+        q = rng.standard_normal((B * C, nh, hd)).astype(np.float32)
+        q_s.copy_(torch.from_numpy(q))
+        cu_s.copy_(i32(cu, dev))
+        sp_s.copy_(i32(done.astype(np.uint32), dev))
+        out_g.fill_(float("nan"))
+        out_e.fill_(float("nan"))
+        torch.cuda.synchronize()
+        call(None, out_e)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g.view(torch.int32), out_e.view(torch.int32)), k
+        gh = out_g.cpu().numpy()
+        for b in range(B):
+            n, st = int(lens[k, b]), int(done[b])
+            if n == 0:
+                continue
+            pages = -(-(st + n) // bt)
+            ref = orc.prefill_causal(hpool, tables[b, :pages], bt, q[cu[b]:cu[b + 1]], n, st, nh,
+                                     nkv, hd)
+            check_close(gh[cu[b]:cu[b + 1]], ref,
+                        KvDataType.F16 if dtype == KvDataType.FP8 else dtype, f"chunk {k} seq {b}")
+        assert np.isnan(gh[cu[B]:]).all()                            # rows past the chunks untouched
+        done += lens[k]
