@@ -1014,3 +1014,84 @@ def test_scheduled_step_random_sweep(dev, seed):
     ref = orc.sdpa_decode_batched(pool.float().cpu().numpy(), tab, pos.astype(np.uint32) + 1, bt,
                                   q.cpu().numpy(), n_head, n_kv, hd)
     check_close(out.cpu().numpy(), ref, what=f"scheduled sweep {seed}")
+
+
+def test_scheduled_steps_on_two_streams(dev):
+    """The benchmark's fused step for two independent batches on two streams at
+    once, each with its own schedule buffer and workspace (the rule for calls
+    that overlap in time), beside a batched bf16 prefill on a third stream.
+    Each stream repeats its calls three times with no synchronisation between
+    the streams. Pools and outputs equal the same calls made one after
+    another bit for bit, and the decodes match the oracle with the appended
+    rows in place."""
+    from titan_amd.flash_attention import FlashAttention2
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl = n_kv * hd
+    rng = np.random.default_rng(31)
+    pa = PagedAttention(0)
+    jobs = []
+    for B, hi in ((24, 3000), (9, 700)):
+        lens = rng.integers(1, hi, size=B).astype(np.int64)
+        tab, nb = make_tables(rng, lens + 1, bt)
+        layout = PagedKvLayout(nb, bt, rl, KvDataType.F16)
+        plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(lens.max()) + 1)
+        assert plan[0] == 0
+        pool, pool_f32 = make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)
+        nk = rng.standard_normal((B, rl)).astype(np.float16)
+        nv = rng.standard_normal((B, rl)).astype(np.float16)
+        q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+        jobs.append(dict(B=B, lens=lens, tab=tab, layout=layout, plan=plan, pool0=pool,
+                         pool_f32=pool_f32, dtab=i32(tab, dev), pos=i32(lens, dev), nk=nk, nv=nv,
+                         k=torch.from_numpy(nk).to(dev), v=torch.from_numpy(nv).to(dev), q=q,
+                         dq=torch.from_numpy(q).to(dev), ws=PagedAttention.workspace(plan),
+                         sched=PagedAttention.schedule_buffer(B, tab.shape[1], bt, plan)))
+    # the prefill: two chunks of a bf16 pool (ping-pong kernel), 32/8 heads
+    pnh, pnkv = 32, 8
+    starts, plens = np.array([0, 900]), np.array([130, 77])
+    ptab, pnb = make_tables(rng, starts + plens, bt)
+    ppool, _ = make_pool(rng, pnb, bt, pnkv, hd, KvDataType.BF16, dev)
+    pq = torch.from_numpy(rng.standard_normal((int(plens.sum()), pnh, hd)).astype(np.float32)).to(dev)
+    pcu = i32(np.concatenate([[0], np.cumsum(plens)]), dev)
+    pst, pdt = i32(starts, dev), i32(ptab, dev)
+    fa = FlashAttention2(0)
+
+    def decode(j, stream, pool, out):
+        pa.build_schedule(stream, j["layout"], j["dtab"], j["pos"], 1, j["plan"], j["sched"])
+        pa.append_decode_scheduled(stream, j["layout"], pool, j["k"], j["v"], j["sched"],
+                                   j["tab"].shape[1], j["dq"], out, n_head, hd, j["plan"], j["ws"])
+
+    def prefill(stream, out):
+        fa.launch_batched(stream, pq, ppool, pdt, pcu, pst, out, pnh, pnkv, hd, bt,
+                          int(plens.max()), kv_dtype=KvDataType.BF16)
+
+    seq_pools = [j["pool0"].clone() for j in jobs]
+    seq_outs = [torch.full((j["B"], n_head, hd), float("nan"), device=dev) for j in jobs]
+    seq_pf = torch.full_like(pq, float("nan"))
+    for j, p, o in zip(jobs, seq_pools, seq_outs):
+        decode(j, None, p, o)
+    prefill(None, seq_pf)
+    torch.cuda.synchronize()
+    con_pools = [j["pool0"].clone() for j in jobs]
+    con_outs = [torch.full_like(o, float("nan")) for o in seq_outs]
+    con_pf = torch.full_like(pq, float("nan"))
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for j, s, p, o in zip(jobs, streams, con_pools, con_outs):
+            decode(j, s, p, o)
+        prefill(streams[2], con_pf)
+    torch.cuda.synchronize()
+    assert torch.equal(con_pf.view(torch.int32), seq_pf.view(torch.int32))
+    for i, j in enumerate(jobs):
+        assert torch.equal(con_pools[i].view(torch.int16), seq_pools[i].view(torch.int16)), i
+        assert torch.equal(con_outs[i].view(torch.int32), seq_outs[i].view(torch.int32)), i
+        ref_pool = j["pool_f32"].reshape(-1, bt, 2, rl).copy()
+        for b in range(j["B"]):
+            L = int(j["lens"][b])
+            ref_pool[j["tab"][b, L // bt], L % bt, 0] = j["nk"][b].astype(np.float32)
+            ref_pool[j["tab"][b, L // bt], L % bt, 1] = j["nv"][b].astype(np.float32)
+        assert np.array_equal(con_pools[i].float().cpu().numpy(), ref_pool.reshape(-1)), i
+        ref = orc.sdpa_decode_batched(ref_pool.reshape(-1), j["tab"],
+                                      (j["lens"] + 1).astype(np.uint32), bt, j["q"], n_head, n_kv,
+                                      hd)
+        check_close(con_outs[i].cpu().numpy(), ref, f"stream {i}")
