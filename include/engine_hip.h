@@ -274,7 +274,8 @@ eh_status eh_decode_plan(uint32_t kv_dtype, uint32_t batch, uint32_t n_head, uin
  * plan's to the calls taking one (eh_append_decode_batched[_e4m3],
  * eh_decode_schedule / eh_append_decode_scheduled, and max_splits of the
  * batched decodes): 4 * (grid + batch) * n_head * 130, the partial states of
- * every run plus one per sequence (no reference counterpart). */
+ * every run plus one per sequence, or UINT64_MAX where that does not fit
+ * 64 bits (no reference counterpart). */
 uint64_t eh_decode_grid_workspace_bytes(uint32_t grid, uint32_t batch, uint32_t n_head);
 /* Name of the split kernel eh_paged_decode_batched launches for a shape
  * (diagnostics and profiling; no reference counterpart). */

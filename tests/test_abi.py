@@ -111,6 +111,24 @@ def test_decode_plan():
     assert ws.value == 14 * 16 * (64 + 2) * 4
 
 
+def test_grid_workspace_bytes():
+    """Workspace of a token-balanced decode at a caller-chosen grid: one
+    (acc, m, l) partial per run and per sequence, 4 * (grid + batch) * n_head
+    * 130 bytes, saturating at UINT64_MAX where that leaves 64 bits."""
+    L = _lib.load()
+    assert L.eh_decode_grid_workspace_bytes(1024, 32, 12) == 4 * (1024 + 32) * 12 * 130
+    assert L.eh_decode_grid_workspace_bytes(1, 0, 1) == 520
+    assert L.eh_decode_grid_workspace_bytes(0, 0, 7) == 0
+    big = 4 * (2**32 - 1 + 2**32 - 1) * (2**32 - 1) * 130
+    assert big >= 2**64
+    assert L.eh_decode_grid_workspace_bytes(2**32 - 1, 2**32 - 1, 2**32 - 1) == 2**64 - 1
+    # either side of the 64-bit limit at n_head = 2^32 - 1
+    h = 2**32 - 1
+    assert 520 * 8_000_000 * h < 2**64 <= 520 * 9_000_000 * h
+    assert L.eh_decode_grid_workspace_bytes(8_000_000, 0, h) == 520 * 8_000_000 * h
+    assert L.eh_decode_grid_workspace_bytes(8_999_000, 1_000, h) == 2**64 - 1
+
+
 class HostCache:
     """Thin driver of the product's host bookkeeping through the C-ABI."""
 

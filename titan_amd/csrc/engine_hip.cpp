@@ -1367,7 +1367,11 @@ uint64_t eh_decode_mass_workspace_bytes(uint32_t batch, uint32_t bt_stride, uint
 }
 
 uint64_t eh_decode_grid_workspace_bytes(uint32_t grid, uint32_t batch, uint32_t n_head) {
-    return tiles_ws_bytes(grid, batch, n_head);
+    // (grid + batch) * n_head < 2^65; the size saturates where 520 times that
+    // leaves 64 bits (no call accepts such a shape)
+    const unsigned __int128 b = (unsigned __int128)tiles_ws_bytes(1, 0, 1) *
+                                ((uint64_t)grid + batch) * n_head;
+    return b > UINT64_MAX ? UINT64_MAX : (uint64_t)b;
 }
 
 static eh_status append_decode_body(eh_context* c, eh_stream stream, const eh_kv_layout* l,
