@@ -111,6 +111,69 @@ def test_decode_plan():
     assert ws.value == 14 * 16 * (64 + 2) * 4
 
 
+_SIZE_CHECKS = r"""
+import ctypes as C, json, sys
+sys.path.insert(0, sys.argv[1])
+from titan_amd import _lib
+L = _lib.load()
+ctx = C.c_void_p(64)   # never dereferenced: every case is rejected before the context is used
+U64 = 2**64 - 1
+
+def err():
+    e, a = C.c_uint64(), C.c_uint64()
+    L.eh_last_error(C.byref(e), C.byref(a), None, None)
+    return e.value, a.value
+
+def lay(nb, bt, rl, dt=1):
+    return _lib.eh_kv_layout(nb, bt, rl, dt, 0)
+
+out = {}
+def run(name, st):
+    out[name] = (st, *err())
+
+buf = C.c_void_p(4096)
+for name, l in (("bt0", lay(4, 0, 256)), ("bt_big", lay(4, 2**31, 256)), ("rl0", lay(4, 16, 0)),
+                ("row_big", lay(4, 16, 2**30, 0)), ("pool_wrap", lay(2**62, 16, 256))):
+    run("append_" + name, L.eh_append_kv(ctx, None, C.byref(l), buf, 1 << 20, buf, 1 << 20, buf,
+                                         1 << 20, buf, 64, 0, 1, None))
+run("gather_bt0", L.eh_gather_kv(ctx, None, C.byref(lay(4, 0, 256)), buf, 1 << 20, buf, 64, buf,
+                                 1 << 20, 0, 1, 0))
+run("copy_bt0", L.eh_copy_pages(ctx, None, C.byref(lay(4, 0, 256)), buf, 1 << 20, buf, buf, 1))
+run("sched_rl0", L.eh_decode_schedule(ctx, None, C.byref(lay(4, 16, 0)), buf, 64, 1, buf, 1, 1, 1,
+                                      buf, 1 << 20))
+# a page of 2^30 tokens x 2 x 2^30 kv heads x 128 x 4 B is 2^70 bytes: it wrapped to 0 before
+run("prefill_page_wrap", L.eh_flash_attention_prefill(ctx, None, 0, buf, 2**40, buf, 1 << 20, buf,
+                                                      4, buf, 2**40, 2**30, 2**30, 128, 2**30, 1,
+                                                      0, None))
+print(json.dumps(out))
+"""
+
+
+def test_layout_and_size_checks_before_any_hip_call():
+    """Pool layouts that would divide by zero or pass a wrapped size, and a
+    prefill whose page size passes 64 bits, are rejected with InvalidSize
+    before the context is used: block_tokens 0 or above 2^31 - 1, row_len 0,
+    rows of 2^31 bytes or more, and a pool or page size beyond 64 bits (the
+    expected size saturates at UINT64_MAX). The calls run in a child process,
+    so a regression shows as a failed test, not a crashed run."""
+    import json
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, "-c", _SIZE_CHECKS, ROOT], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    got = json.loads(r.stdout.strip().splitlines()[-1])
+    bad = 1  # EH_INVALID_SIZE
+    imax, u64 = 2**31 - 1, 2**64 - 1
+    want = {
+        "append_bt0": (bad, 1, 0), "append_bt_big": (bad, imax, 2**31), "append_rl0": (bad, 1, 0),
+        "append_row_big": (bad, imax, 2**32), "append_pool_wrap": (bad, u64, 1 << 20),
+        "gather_bt0": (bad, 1, 0), "copy_bt0": (bad, 1, 0), "sched_rl0": (bad, 1, 0),
+        "prefill_page_wrap": (bad, u64, 1 << 20),
+    }
+    assert {k: tuple(v) for k, v in got.items()} == want
+
+
 def test_grid_workspace_bytes():
     """Workspace of a token-balanced decode at a caller-chosen grid: one
     (acc, m, l) partial per run and per sequence, 4 * (grid + batch) * n_head

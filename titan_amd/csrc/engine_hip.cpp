@@ -124,7 +124,23 @@ uint64_t elt_bytes(uint32_t dt) {
     }
 }
 
-uint64_t div_ceil(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+uint64_t div_ceil(uint64_t a, uint64_t b) { return a / b + (a % b != 0); }
+
+// Byte counts of the argument checks saturate at UINT64_MAX: a size beyond 64
+// bits fits no real buffer, so its check fails instead of passing on a wrapped
+// value, and no page size wraps to 0 before a division.
+uint64_t smul(uint64_t a, uint64_t b) {
+    uint64_t r;
+    return __builtin_mul_overflow(a, b, &r) ? UINT64_MAX : r;
+}
+template <class... T>
+uint64_t smul(uint64_t a, uint64_t b, uint64_t c, T... rest) {
+    return smul(smul(a, b), c, rest...);
+}
+uint64_t sadd(uint64_t a, uint64_t b) {
+    uint64_t r;
+    return __builtin_add_overflow(a, b, &r) ? UINT64_MAX : r;
+}
 
 // Largest copy chunk (16/8/4/2 bytes) dividing the row size and every base.
 int pick_chunk(uint64_t row_bytes, std::initializer_list<const void*> ptrs) {
@@ -183,7 +199,7 @@ int dt_index(uint32_t dt) {
 
 // Workspace of the split-K decode: partial accumulators then (m, l) pairs.
 uint64_t decode_ws_floats(uint64_t rows, uint64_t max_splits, uint64_t head_dim) {
-    return max_splits <= 1 ? 0 : rows * max_splits * (head_dim + 2);
+    return max_splits <= 1 ? 0 : smul(rows, max_splits, sadd(head_dim, 2));
 }
 
 // Largest split that keeps a workgroup's block-table slice inside LDS.
@@ -357,27 +373,27 @@ uint32_t device_cus() {
 uint32_t tiles_grid(const tiles_cfg& t) { return device_cus() * (8u / t.nw); }
 
 uint64_t tiles_ws_bytes(uint64_t grid, uint64_t batch, uint64_t n_head) {
-    return 4ull * (grid + batch) * n_head * (128 + 2);
+    return smul(4, sadd(grid, batch), n_head, 128 + 2);
 }
 
 // Attention-mass scratch: one (weight sum, max) pair per (sequence, 16-token
 // tile the block table can address, q head), then the heads' final (M, L).
-uint64_t mass_rec_row(uint64_t bt_stride, uint64_t block_tokens) { return bt_stride * (block_tokens / 16); }
+uint64_t mass_rec_row(uint64_t bt_stride, uint64_t block_tokens) { return smul(bt_stride, block_tokens / 16); }
 uint64_t mass_ws_bytes(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens, uint64_t n_head) {
-    return 8ull * batch * n_head * (mass_rec_row(bt_stride, block_tokens) + 1);
+    return smul(8, batch, n_head, sadd(mass_rec_row(bt_stride, block_tokens), 1));
 }
 
 // Step schedule (eh_decode_schedule): P run headers, P * cap item
 // descriptors and batch sequence records, 16 bytes each; cap = the most
 // tiles one run can hold, from the tiles the block tables can address.
 uint64_t sched_tile_bound(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens) {
-    return batch * bt_stride * (block_tokens / 16);
+    return smul(batch, bt_stride, block_tokens / 16);
 }
 uint64_t sched_cap(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens, uint64_t grid) {
     return std::max<uint64_t>(div_ceil(sched_tile_bound(batch, bt_stride, block_tokens), grid), 1);
 }
 uint64_t sched_bytes(uint64_t batch, uint64_t bt_stride, uint64_t block_tokens, uint64_t grid) {
-    return 16ull * (grid + grid * sched_cap(batch, bt_stride, block_tokens, grid) + batch);
+    return smul(16, sadd(sadd(grid, smul(grid, sched_cap(batch, bt_stride, block_tokens, grid))), batch));
 }
 
 struct tiles_args {
@@ -473,11 +489,11 @@ eh_status validate_attention(uint32_t kv_dtype, uint64_t q_bytes, uint64_t pool_
     if (head_dim < 1) return invalid_size(1, head_dim);
     if (block_tokens < 1) return invalid_size(1, block_tokens);
     if (seq_tokens < 1) return invalid_size(1, seq_tokens);
-    const uint64_t q_expected = n_head * head_dim * 4;
+    const uint64_t q_expected = smul(n_head, head_dim, 4);
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
     if (pool_bytes < 4) return invalid_size(4, pool_bytes);
-    const uint64_t bt_expected = div_ceil(seq_tokens, block_tokens) * 4;
+    const uint64_t bt_expected = smul(div_ceil(seq_tokens, block_tokens), 4);
     if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes);
     const uint64_t imax = 0x7FFFFFFFull;
     for (uint64_t v : {n_head, n_head_kv, head_dim, block_tokens, seq_tokens, query_pos})
@@ -551,11 +567,24 @@ eh_status validate_prefill_shape(uint32_t kv_dtype, uint64_t n_head, uint64_t n_
                                  bool e4m3 = false) {
     if (e4m3 ? kv_dtype != EH_KV_FP8 : !dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
     if (!prefill_hd(head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 128, head_dim);
-    const uint64_t page_bytes = block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
+    const uint64_t page_bytes = smul(block_tokens, 2, n_head_kv, head_dim, elt_bytes(kv_dtype));
     if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
     const uint64_t imax = 0x7FFFFFFFull;
     for (uint64_t v : {n_head, n_head_kv, block_tokens})
         if (v > imax) return invalid_size(imax, v);
+    return EH_OK;
+}
+
+// Shape checks of every call that takes a pool layout, ahead of its own: the
+// kernels take the page and row sizes as 32-bit values, and the checks divide
+// by block_tokens.
+eh_status check_layout(const eh_kv_layout* l) {
+    const uint64_t imax = 0x7FFFFFFFull;
+    if (l->block_tokens < 1) return invalid_size(1, 0, "block_tokens");
+    if (l->block_tokens > imax) return invalid_size(imax, l->block_tokens, "block_tokens");
+    if (l->row_len < 1) return invalid_size(1, 0, "row_len");
+    const uint64_t row_bytes = smul(l->row_len, std::max<uint64_t>(elt_bytes(l->data_type), 1));
+    if (row_bytes > imax) return invalid_size(imax, row_bytes, "row bytes");
     return EH_OK;
 }
 
@@ -593,7 +622,7 @@ eh_status eh_last_error(uint64_t* expected, uint64_t* actual, const char** site,
 uint64_t eh_kv_element_bytes(uint32_t data_type) { return elt_bytes(data_type); }
 
 uint64_t eh_kv_layout_bytes_total(const eh_kv_layout* l) {
-    return l->n_blocks * l->block_tokens * 2 * l->row_len * elt_bytes(l->data_type);
+    return smul(l->n_blocks, l->block_tokens, 2, l->row_len, elt_bytes(l->data_type));
 }
 
 eh_status eh_create(int device, const char* code_object_dir, eh_context** out) {
@@ -681,22 +710,23 @@ eh_status eh_append_kv(eh_context* c, eh_stream stream, const eh_kv_layout* l, v
                        uint64_t bt_bytes, uint64_t start_token, uint64_t n_tokens,
                        const uint32_t* pos_ptr) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     const uint64_t elt = elt_bytes(l->data_type);
     if (!elt) return fail(EH_UNSUPPORTED, "data_type");
     // paged_kv.rs:240-267 (element size taken from the layout, not fixed at 4).
     const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
     if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
-    const uint64_t kv_expected = n_tokens * l->row_len * elt;
+    const uint64_t kv_expected = smul(n_tokens, l->row_len, elt);
     if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
     if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
     if (bt_bytes == 0) return invalid_size(4, 0);
     if (n_tokens == 0) return EH_OK;
     // Added check: the table must cover start+n tokens when the host knows start.
     if (!pos_ptr) {
-        const uint64_t need = div_ceil(start_token + n_tokens, l->block_tokens) * 4;
+        const uint64_t need = smul(div_ceil(sadd(start_token, n_tokens), l->block_tokens), 4);
         if (bt_bytes < need) return invalid_size(need, bt_bytes, "block_table");
     }
-    const uint64_t row_bytes = l->row_len * elt;
+    const uint64_t row_bytes = smul(l->row_len, elt);
     const int ch = pick_chunk(row_bytes, {pool, keys, values});
     if (!ch) return fail(EH_UNSUPPORTED, "row alignment", 2, row_bytes);
     const uint64_t total = n_tokens * 2 * (row_bytes / ch);
@@ -718,18 +748,19 @@ eh_status eh_gather_kv(eh_context* c, eh_stream stream, const eh_kv_layout* l, c
                        uint64_t pool_bytes, const uint32_t* bt, uint64_t bt_bytes, void* out,
                        uint64_t out_bytes, uint64_t start_token, uint64_t n_tokens, int is_value) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     const uint64_t elt = elt_bytes(l->data_type);
     if (!elt) return fail(EH_UNSUPPORTED, "data_type");
     // paged_kv.rs:391-416
     const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
     if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
-    const uint64_t out_expected = n_tokens * l->row_len * elt;
+    const uint64_t out_expected = smul(n_tokens, l->row_len, elt);
     if (out_bytes < out_expected) return invalid_size(out_expected, out_bytes);
     if (bt_bytes == 0) return invalid_size(4, 0);
     if (n_tokens == 0) return EH_OK;
-    const uint64_t need = div_ceil(start_token + n_tokens, l->block_tokens) * 4;
+    const uint64_t need = smul(div_ceil(sadd(start_token, n_tokens), l->block_tokens), 4);
     if (bt_bytes < need) return invalid_size(need, bt_bytes, "block_table");
-    const uint64_t row_bytes = l->row_len * elt;
+    const uint64_t row_bytes = smul(l->row_len, elt);
     const int ch = pick_chunk(row_bytes, {pool, out});
     if (!ch) return fail(EH_UNSUPPORTED, "row alignment", 2, row_bytes);
     const uint64_t total = n_tokens * (row_bytes / ch);
@@ -751,19 +782,20 @@ eh_status eh_append_kv_batched(eh_context* c, eh_stream stream, const eh_kv_layo
                                uint64_t bt_bytes, uint32_t bt_stride, const uint32_t* cu_seqlens,
                                const uint32_t* start_pos, uint32_t batch, uint64_t total_tokens) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     const uint64_t elt = elt_bytes(l->data_type);
     if (!elt) return fail(EH_UNSUPPORTED, "data_type");
     const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
     if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
-    const uint64_t kv_expected = total_tokens * l->row_len * elt;
+    const uint64_t kv_expected = smul(total_tokens, l->row_len, elt);
     if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
     if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
     if (total_tokens == 0 || batch == 0) return EH_OK;
     if (!cu_seqlens || !start_pos) return fail(EH_INVALID_ARGS, "cu_seqlens/start_pos are null");
     if (bt_stride == 0) return invalid_size(1, 0, "bt_stride");
-    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    const uint64_t bt_expected = smul(batch, bt_stride, 4);
     if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
-    const uint64_t row_bytes = l->row_len * elt;
+    const uint64_t row_bytes = smul(l->row_len, elt);
     const int ch = pick_chunk(row_bytes, {pool, keys, values});
     if (!ch) return fail(EH_UNSUPPORTED, "row alignment", 2, row_bytes);
     const uint64_t total = total_tokens * 2 * (row_bytes / ch);
@@ -798,17 +830,18 @@ eh_status eh_append_kv_e4m3_batched(eh_context* c, eh_stream stream, const eh_kv
                                     uint32_t batch, uint64_t total_tokens, uint32_t head_dim,
                                     const float* k_scale, const float* v_scale) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     eh_status st = check_e4m3(l, head_dim, k_scale, v_scale);
     if (st) return st;
     const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
     if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
-    const uint64_t kv_expected = total_tokens * l->row_len * 4;
+    const uint64_t kv_expected = smul(total_tokens, l->row_len, 4);
     if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
     if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
     if (total_tokens == 0 || batch == 0) return EH_OK;
     if (!cu_seqlens || !start_pos) return fail(EH_INVALID_ARGS, "cu_seqlens/start_pos are null");
     if (bt_stride == 0) return invalid_size(1, 0, "bt_stride");
-    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    const uint64_t bt_expected = smul(batch, bt_stride, 4);
     if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
     if (((uintptr_t)keys | (uintptr_t)values) % 16 || (uintptr_t)pool % 4)
         return fail(EH_UNSUPPORTED, "alignment (keys/values 16 B, pool 4 B)");
@@ -828,13 +861,14 @@ eh_status eh_kv_e4m3_scales(eh_context* c, eh_stream stream, const eh_kv_layout*
                             float* k_scale, uint64_t k_scale_bytes, float* v_scale,
                             uint64_t v_scale_bytes) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     eh_status st = check_e4m3(l, head_dim, k_scale, v_scale);
     if (st) return st;
     const uint64_t n_kv = l->row_len / head_dim;
     if (k_scale_bytes < n_kv * 4) return invalid_size(n_kv * 4, k_scale_bytes, "k_scale");
     if (v_scale_bytes < n_kv * 4) return invalid_size(n_kv * 4, v_scale_bytes, "v_scale");
     if (n_kv > 65535) return invalid_size(65535, n_kv, "kv heads");
-    const uint64_t kv_expected = n_rows * l->row_len * 4;
+    const uint64_t kv_expected = smul(n_rows, l->row_len, 4);
     if (keys_bytes < kv_expected) return invalid_size(kv_expected, keys_bytes);
     if (values_bytes < kv_expected) return invalid_size(kv_expected, values_bytes);
     if (n_rows && (!keys || !values)) return fail(EH_INVALID_ARGS, "keys/values are null");
@@ -852,15 +886,16 @@ eh_status eh_gather_kv_e4m3(eh_context* c, eh_stream stream, const eh_kv_layout*
                             uint64_t bt_bytes, float* out, uint64_t out_bytes, uint64_t start_token,
                             uint64_t n_tokens, int is_value, uint32_t head_dim, const float* scale) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     eh_status st = check_e4m3(l, head_dim, scale, scale);
     if (st) return st;
     const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
     if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
-    const uint64_t out_expected = n_tokens * l->row_len * 4;
+    const uint64_t out_expected = smul(n_tokens, l->row_len, 4);
     if (out_bytes < out_expected) return invalid_size(out_expected, out_bytes);
     if (bt_bytes == 0) return invalid_size(4, 0);
     if (n_tokens == 0) return EH_OK;
-    const uint64_t need = div_ceil(start_token + n_tokens, l->block_tokens) * 4;
+    const uint64_t need = smul(div_ceil(sadd(start_token, n_tokens), l->block_tokens), 4);
     if (bt_bytes < need) return invalid_size(need, bt_bytes, "block_table");
     if ((uintptr_t)out % 16 || (uintptr_t)pool % 4)
         return fail(EH_UNSUPPORTED, "alignment (out 16 B, pool 4 B)");
@@ -880,13 +915,14 @@ eh_status eh_copy_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l, 
                         uint64_t pool_bytes, const uint32_t* src_ids, const uint32_t* dst_ids,
                         uint32_t n_pairs) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     const uint64_t elt = elt_bytes(l->data_type);
     if (!elt) return fail(EH_UNSUPPORTED, "data_type");
     const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
     if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
     if (n_pairs == 0) return EH_OK;
     if (!src_ids || !dst_ids) return fail(EH_INVALID_ARGS, "page id arrays are null");
-    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    const uint64_t page_bytes = smul(l->block_tokens, 2, l->row_len, elt);
     const int ch = pick_chunk(page_bytes, {pool});
     if (!ch) return fail(EH_UNSUPPORTED, "page alignment", 2, page_bytes);
     eh_status st = bind(c);
@@ -902,9 +938,10 @@ eh_status eh_stream_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l
                          uint64_t ids_bytes, uint32_t n_ids, uint32_t depth, uint32_t grid,
                          uint32_t* out, uint64_t out_bytes) {
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     const uint64_t elt = elt_bytes(l->data_type);
     if (!elt) return fail(EH_UNSUPPORTED, "data_type");
-    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    const uint64_t page_bytes = smul(l->block_tokens, 2, l->row_len, elt);
     if (page_bytes == 0 || page_bytes % 16384)
         return fail(EH_UNSUPPORTED, "page bytes: a multiple of 16 KiB", 16384, page_bytes);
     const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
@@ -914,7 +951,7 @@ eh_status eh_stream_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l
     if (n_ids == 0) return EH_OK;
     if (!ids || !out || !pool) return fail(EH_INVALID_ARGS, "null pool, ids or out");
     if (ids_bytes < 4ull * n_ids) return invalid_size(4ull * n_ids, ids_bytes, "ids");
-    const uint64_t out_need = 4ull * grid * 8;
+    const uint64_t out_need = smul(4, grid, 8);
     if (out_bytes < out_need) return invalid_size(out_need, out_bytes, "out");
     eh_status st = bind(c);
     if (st) return st;
@@ -972,7 +1009,7 @@ static eh_status single_seq_attention(eh_context* c, eh_stream stream, uint32_t 
     if (st) return st;
     st = bind(c);
     if (st) return st;
-    const uint64_t page_bytes = block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
+    const uint64_t page_bytes = smul(block_tokens, 2, n_head_kv, head_dim, elt_bytes(kv_dtype));
     decode_args a{};
     a.kv_dtype = kv_dtype;
     a.q = q;
@@ -1197,15 +1234,15 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
     if (max_splits < 1) return invalid_size(1, max_splits, "max_splits");
     if (kv_dtype == EH_KV_FP8) return fail(EH_UNSUPPORTED, "E4M3 pages: eh_paged_decode_batched_e4m3");
     if (tps == 0) {  // token-balanced kernel, max_splits workgroups
-        const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+        const uint64_t q_expected = smul(batch, n_head, head_dim, 4);
         if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
         if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
-        const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+        const uint64_t bt_expected = smul(batch, bt_stride, 4);
         if (bt_stride == 0 || bt_bytes < bt_expected)
             return invalid_size(bt_expected, bt_bytes, "block_tables");
         const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, batch);
         if (!tc.ok) return fail(EH_UNSUPPORTED, "tokens_per_split 0: shape outside the balanced kernel");
-        const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * 2;
+        const uint64_t page_bytes = smul(block_tokens, 2, n_head_kv, head_dim, 2);
         if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
         const uint64_t ws_need = tiles_ws_bytes(max_splits, batch, n_head);
         if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
@@ -1229,17 +1266,17 @@ eh_status eh_paged_decode_batched(eh_context* c, eh_stream stream, uint32_t kv_d
         a.ws = ws;
         return run_tiles(c, stream, a, tc);
     }
-    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    const uint64_t q_expected = smul(batch, n_head, head_dim, 4);
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
-    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    const uint64_t bt_expected = smul(batch, bt_stride, 4);
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
-    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype);
+    const uint64_t page_bytes = smul(block_tokens, 2, n_head_kv, head_dim, elt_bytes(kv_dtype));
     if (!dt_name(kv_dtype)) return fail(EH_UNSUPPORTED, "kv_dtype");
     if (!supported_hd(kv_dtype, head_dim)) return fail(EH_UNSUPPORTED, "head_dim", 256, head_dim);
     if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
     if (max_splits > kMaxSplits) return invalid_size(kMaxSplits, max_splits, "max_splits");
-    const uint64_t ws_need = 4 * decode_ws_floats((uint64_t)batch * n_head, max_splits, head_dim);
+    const uint64_t ws_need = smul(4, decode_ws_floats(smul(batch, n_head), max_splits, head_dim));
     if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
     eh_status st = bind(c);
     if (st) return st;
@@ -1289,19 +1326,19 @@ static eh_status decode_tiles_entry(eh_context* c, eh_stream stream, uint32_t kv
     if (max_splits < 1) return invalid_size(1, max_splits, "max_splits");
     const tiles_cfg tc = pick_tiles(kv_dtype, head_dim, n_head, n_head_kv, block_tokens, batch);
     if (!tc.ok) return fail(EH_UNSUPPORTED, "shape outside the token-balanced kernel");
-    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    const uint64_t q_expected = smul(batch, n_head, head_dim, 4);
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
-    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    const uint64_t bt_expected = smul(batch, bt_stride, 4);
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
-    const uint64_t page_bytes = (uint64_t)block_tokens * 2 * n_head_kv * head_dim * (f8 ? 1 : 2);
+    const uint64_t page_bytes = smul(block_tokens, 2, n_head_kv, head_dim, f8 ? 1 : 2);
     if (pool_bytes < page_bytes) return invalid_size(page_bytes, pool_bytes);
     const uint64_t ws_tiles = tiles_ws_bytes(max_splits, batch, n_head);
     const uint64_t ws_need =
         ws_tiles + (block_mass ? mass_ws_bytes(batch, bt_stride, block_tokens, n_head) : 0);
     if (ws_bytes < ws_need) return invalid_size(ws_need, ws_bytes, "workspace");
-    if (block_mass && block_mass_bytes < pool_bytes / page_bytes * 4)
-        return invalid_size(pool_bytes / page_bytes * 4, block_mass_bytes, "block_mass");
+    if (block_mass && block_mass_bytes < smul(pool_bytes / page_bytes, 4))
+        return invalid_size(smul(pool_bytes / page_bytes, 4), block_mass_bytes, "block_mass");
     if (block_tokens % 16) return fail(EH_UNSUPPORTED, "block_tokens");
     eh_status st = bind(c);
     if (st) return st;
@@ -1385,13 +1422,14 @@ static eh_status append_decode_body(eh_context* c, eh_stream stream, const eh_kv
                                     const float* v_scale) {
     const bool e4m3 = k_scale != nullptr;
     if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
     if (batch == 0) return EH_OK;
     if (!start_pos) return fail(EH_INVALID_ARGS, "start_pos is null");
     if (head_dim < 1 || l->row_len % head_dim) return invalid_size(head_dim, l->row_len % (head_dim ? head_dim : 1));
     const uint64_t n_head_kv = l->row_len / head_dim;
     if (n_head < 1 || n_head_kv < 1 || n_head % n_head_kv) return invalid_size(n_head_kv, n_head);
     const uint64_t elt = elt_bytes(l->data_type);
-    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    const uint64_t page_bytes = smul(l->block_tokens, 2, l->row_len, elt);
     if (l->n_blocks < 1 || page_bytes == 0) return fail(EH_INVALID_ARGS, "layout");
     if (pool_bytes < l->n_blocks * page_bytes) return invalid_size(l->n_blocks * page_bytes, pool_bytes);
     if (e4m3 && (l->data_type != EH_KV_FP8 || !v_scale))
@@ -1399,12 +1437,12 @@ static eh_status append_decode_body(eh_context* c, eh_stream stream, const eh_kv
     if (!e4m3 && l->data_type == EH_KV_FP8)
         return fail(EH_UNSUPPORTED, "FP8 pages: use eh_append_decode_batched_e4m3");
     // E4M3: the appended rows arrive as f32 and are quantised in the launch
-    const uint64_t row_expected = (uint64_t)batch * l->row_len * (e4m3 ? 4 : elt);
+    const uint64_t row_expected = smul(batch, l->row_len, e4m3 ? 4 : elt);
     if (keys_bytes < row_expected) return invalid_size(row_expected, keys_bytes);
     if (values_bytes < row_expected) return invalid_size(row_expected, values_bytes);
-    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    const uint64_t bt_expected = smul(batch, bt_stride, 4);
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
-    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    const uint64_t q_expected = smul(batch, n_head, head_dim, 4);
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
     const tiles_cfg tc = pick_tiles(l->data_type, head_dim, n_head, n_head_kv, l->block_tokens, batch);
@@ -1506,6 +1544,7 @@ static eh_status check_sched_shape(const eh_kv_layout* l, uint32_t batch, uint32
     if (l->block_tokens < 16 || (l->block_tokens & (l->block_tokens - 1)) ||
         l->block_tokens > 0xFFFFFFFFull)
         return fail(EH_UNSUPPORTED, "block_tokens: a power of two of at least 16");
+    if (eh_status ls = check_layout(l)) return ls;
     if (batch > kTilesMaxBatch) return invalid_size(kTilesMaxBatch, batch, "batch");
     if (bt_stride == 0) return invalid_size(1, 0, "bt_stride");
     if (grid < 1) return invalid_size(1, grid, "grid");
@@ -1528,7 +1567,7 @@ eh_status eh_decode_schedule(eh_context* c, eh_stream stream, const eh_kv_layout
     // the kernels read and write the schedule as 16-byte records
     if (!sched || (uintptr_t)sched % 16)
         return fail(EH_INVALID_ARGS, "schedule is null or not 16-byte aligned");
-    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    const uint64_t bt_expected = smul(batch, bt_stride, 4);
     if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
     if (l->n_blocks < 1) return fail(EH_INVALID_ARGS, "layout");
     st = bind(c);
@@ -1566,15 +1605,15 @@ eh_status eh_append_decode_scheduled(eh_context* c, eh_stream stream, const eh_k
     const bool f8 = l->data_type == EH_KV_FP8;
     if (f8 && (!k_scale || !v_scale)) return fail(EH_INVALID_ARGS, "E4M3 pages: both scales");
     const uint64_t elt = elt_bytes(l->data_type);
-    const uint64_t page_bytes = l->block_tokens * 2 * l->row_len * elt;
+    const uint64_t page_bytes = smul(l->block_tokens, 2, l->row_len, elt);
     if (l->n_blocks < 1 || page_bytes == 0) return fail(EH_INVALID_ARGS, "layout");
     if (pool_bytes < l->n_blocks * page_bytes) return invalid_size(l->n_blocks * page_bytes, pool_bytes);
     if (keys) {  // E4M3: the appended rows arrive as f32 and are quantised in the launch
-        const uint64_t row_expected = (uint64_t)batch * l->row_len * (f8 ? 4 : elt);
+        const uint64_t row_expected = smul(batch, l->row_len, f8 ? 4 : elt);
         if (keys_bytes < row_expected) return invalid_size(row_expected, keys_bytes);
         if (values_bytes < row_expected) return invalid_size(row_expected, values_bytes);
     }
-    const uint64_t q_expected = (uint64_t)batch * n_head * head_dim * 4;
+    const uint64_t q_expected = smul(batch, n_head, head_dim, 4);
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
     const tiles_cfg tc = pick_tiles(l->data_type, head_dim, n_head, n_head_kv, l->block_tokens, batch);
@@ -1623,10 +1662,10 @@ eh_status eh_flash_attention_prefill(eh_context* c, eh_stream stream, uint32_t k
     if (block_tokens < 1) return invalid_size(1, block_tokens);
     // flash_attention.rs:142-169: q, out, then the block table of
     // ceil((pos_offset + q_tokens) / block_tokens) entries.
-    const uint64_t q_expected = q_tokens * n_head * head_dim * 4;
+    const uint64_t q_expected = smul(q_tokens, n_head, head_dim, 4);
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
-    const uint64_t bt_expected = div_ceil(pos_offset + q_tokens, block_tokens) * 4;
+    const uint64_t bt_expected = smul(div_ceil(sadd(pos_offset, q_tokens), block_tokens), 4);
     if (bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes);
     eh_status st = validate_prefill_shape(kv_dtype, n_head, n_head_kv, head_dim, block_tokens,
                                           pool_bytes);
@@ -1640,7 +1679,7 @@ eh_status eh_flash_attention_prefill(eh_context* c, eh_stream stream, uint32_t k
     a.kv_dtype = kv_dtype;
     a.q = q;
     a.pool = pool;
-    a.n_blocks = pool_bytes / (block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype));
+    a.n_blocks = pool_bytes / smul(block_tokens, 2, n_head_kv, head_dim, elt_bytes(kv_dtype));
     a.bt = bt;
     a.bt_stride = 0;
     a.bt_entries = (uint32_t)std::min<uint64_t>(bt_bytes / 4, 0xFFFFFFFFull);
@@ -1673,10 +1712,10 @@ static eh_status prefill_batched_body(eh_context* c, eh_stream stream, uint32_t 
     if (n_head % n_head_kv != 0) return invalid_size(n_head_kv, n_head % n_head_kv);
     if (head_dim < 1) return invalid_size(1, head_dim);
     if (block_tokens < 1) return invalid_size(1, block_tokens);
-    const uint64_t q_expected = (uint64_t)total_q_tokens * n_head * head_dim * 4;
+    const uint64_t q_expected = smul(total_q_tokens, n_head, head_dim, 4);
     if (q_bytes < q_expected) return invalid_size(q_expected, q_bytes);
     if (out_bytes < q_expected) return invalid_size(q_expected, out_bytes);
-    const uint64_t bt_expected = (uint64_t)batch * bt_stride * 4;
+    const uint64_t bt_expected = smul(batch, bt_stride, 4);
     if (bt_stride == 0 || bt_bytes < bt_expected) return invalid_size(bt_expected, bt_bytes, "block_tables");
     eh_status st = validate_prefill_shape(kv_dtype, n_head, n_head_kv, head_dim, block_tokens,
                                           pool_bytes, e4m3);
@@ -1689,7 +1728,7 @@ static eh_status prefill_batched_body(eh_context* c, eh_stream stream, uint32_t 
     a.kv_dtype = kv_dtype;
     a.q = q;
     a.pool = pool;
-    a.n_blocks = pool_bytes / ((uint64_t)block_tokens * 2 * n_head_kv * head_dim * elt_bytes(kv_dtype));
+    a.n_blocks = pool_bytes / smul(block_tokens, 2, n_head_kv, head_dim, elt_bytes(kv_dtype));
     a.bt = bt;
     a.bt_stride = bt_stride;
     a.bt_entries = bt_stride;
