@@ -785,8 +785,8 @@ __device__ __forceinline__ void prefill(
 // 0-3 (one per SIMD) run their MFMA phase while waves 4-7 run their softmax,
 // then they swap, with a workgroup barrier between the phases.  A wave's MFMA
 // phase is P.V of the previous tile, then S of the current one, so P stays in
-// registers; it also stages the next tile (waves 0-3 write K one tile ahead,
-// waves 4-7 write V), whose VALU work then issues beside the MFMAs:
+// registers; it ends by staging the next tile (waves 0-3 write K one tile
+// ahead, waves 4-7 write V) behind its last MFMAs:
 //   interval 2j  : waves 0-3 MFMA [P.V(j-1), S(j)], write K(j+1)  waves 4-7 softmax(j-1)
 //   interval 2j+1: waves 0-3 softmax(j)   waves 4-7 MFMA [P.V(j-1), S(j)], write V(j)
 // K(j+1) is read at intervals 2j+2 and 2j+3 and its buffer next written at
@@ -1111,16 +1111,6 @@ __device__ __forceinline__ void prefill_pp(
             opv vq[PV_AHEAD];
 #pragma unroll
             for (int i = 0; i < PV_AHEAD; ++i) vq[i] = vread(i);
-            // staging rides in the MFMA phase, while its first operand reads
-            // are in flight: this thread's item of tile commit_t goes to LDS,
-            // then its loads of tile issue_t go out.  (In the softmax phase it
-            // made that phase the longer one; spread between the MFMAs it
-            // measured slower still.)
-            __builtin_amdgcn_sched_barrier(0);
-            if (commit_t != NONE) {
-                commit(commit_t, iv);
-                if (issue_t != NONE) issue(issue_t);
-            }
 #pragma unroll
             for (int i = 0; i < NPV; ++i) {
                 __builtin_amdgcn_sched_barrier(0);
@@ -1154,6 +1144,17 @@ __device__ __forceinline__ void prefill_pp(
             __builtin_amdgcn_sched_barrier(0);
             sv[0] = s0;
             sv[1] = s1;
+        }
+        // staging ends the MFMA phase, behind its last MFMAs and operand
+        // reads: this thread's item of tile commit_t goes to LDS, then its
+        // loads of tile issue_t go out.  (At the start of the phase it
+        // measured 1.3 % slower for bf16 pages, after the P.V MFMAs 0.6 %; in
+        // the softmax phase it made that phase the longer one, and spread
+        // between the MFMAs slower still.)
+        __builtin_amdgcn_sched_barrier(0);
+        if (commit_t != NONE) {
+            commit(commit_t, iv);
+            if (issue_t != NONE) issue(issue_t);
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
@@ -1289,7 +1290,7 @@ __device__ __forceinline__ void prefill_pp(
     if constexpr (B2H) {
         if (exact) {  // uniform over the workgroup: every wave broke at the same interval
             bar();
-            // (inlined: with the restart in the kernel the bf16 kernel keeps 4
+            // (inlined: with the restart in the kernel the bf16 kernel keeps 3
             // VGPRs of the prologue in scratch across the tile loops, stored once
             // before them and reloaded once after; as a called function the
             // kernel would carry 468 bytes of scratch per lane instead)
