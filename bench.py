@@ -56,9 +56,9 @@ def parse():
                    help="suite append part: tokens appended per sequence per call (config 2: 1)")
     p.add_argument("--c5-pool-frac", type=float, default=0.9,
                    help="config 5 pool size as a fraction of free HBM")
-    p.add_argument("--parts", default="c1,append,e4m3,ceiling,c3,c4,c5",
-                   help="suite parts to run (comma list of c1, append, e4m3, ceiling, c3, c4, "
-                        "c5)")
+    p.add_argument("--parts", default="c1,append,e4m3,bf16,ceiling,c3,c4,c5",
+                   help="suite parts to run (comma list of c1, append, e4m3, bf16, ceiling, c3, "
+                        "c4, c5)")
     return p.parse_args()
 
 
@@ -378,8 +378,9 @@ def suite(args, dev):
     on synthetic seeded inputs resident in HBM; timings are HIP events around
     graph replays (launch cost inside the graph, host enqueue outside).
     --parts selects: c1 (config 1), append (config 2 append / gather), e4m3
-    (config 2 decode over E4M3 pages), c3 (config 3 prefill), c4 (config 4
-    compaction), c5 (config 5 long-context decode on a ~90 % HBM pool)."""
+    (config 2 decode over E4M3 pages), bf16 (config 2 decode over bf16 pages
+    beside f16), c3 (config 3 prefill), c4 (config 4 compaction), c5 (config 5
+    long-context decode on a ~90 % HBM pool)."""
     import numpy as np
     import torch
 
@@ -588,6 +589,38 @@ def suite(args, dev):
               "decode_frac_of_8TB/s": round(dec_bytes / us_dec / 1e3 / 8000.0, 4),
               "decode_frac_of_ceiling": round((dec_bytes / us_dec) / (st_bytes / best[0]), 4)})
         del pools
+
+    if "bf16" in parts:  # config 2's decode over bf16 pages beside f16, 16 rotated pools each
+        lens16 = torch.from_numpy((s2.ctx_lens + 1).astype(np.int32)).to(dev)
+        q16 = torch.randn((32, 12, 128), generator=gen, device=dev)
+        b16 = int((s2.ctx_lens + 1).sum()) * 2 * 128 * 2 * 2
+        st16 = int(tab2.shape[1])
+        for dt, tdt in ((KvDataType.F16, torch.float16), (KvDataType.BF16, torch.bfloat16)):
+            lay16 = PagedKvLayout(s2.n_blocks, 16, s2.row_len, dt)
+            pools16 = [torch.randn(lay16.floats_total(), generator=gen, device=dev, dtype=tdt)
+                       for _ in range(16)]
+            plan16 = PagedAttention.plan(32, 12, 2, 128, 16, int(s2.ctx_lens.max()) + 1, 0, dt)
+            ws16 = PagedAttention.workspace(plan16)
+            sched16 = PagedAttention.schedule_buffer(32, st16, 16, plan16)
+            pa.build_schedule(None, lay16, dtab2, lens16, 0, plan16, sched16)
+            o16 = torch.empty_like(q16)
+            turn = [0]
+
+            def dec16(st):
+                p = pools16[turn[0] % len(pools16)]
+                turn[0] += 1
+                pa.append_decode_scheduled(st, lay16, p, None, None, sched16, st16, q16, o16, 12,
+                                           128, plan16, ws16)
+            us16 = graph_time_us(dec16, 20, 32)
+            emit({"config": 2, "what": f"decode from a step schedule over {dt.name.lower()} pages, "
+                  "B=32, 12/2 heads, hd 128, one layer, 16 rotated pools",
+                  "latency_us": round(us16, 2), "kv_bytes": b16,
+                  "GB/s": round(b16 / us16 / 1e3, 1),
+                  "hbm_frac_of_8TB/s": round(b16 / us16 / 1e3 / 8000.0, 4),
+                  "kernel": PagedAttention.kernel_name(12, 2, 128, 16, dt) +
+                  "_sched + eh_decode_tiles_merge_sched"})
+            del pools16
+            torch.cuda.empty_cache()
 
     if "c3" in parts:  # bf16 chunked prefill, B=8, 512 new tokens on 2048 cached, 32/8 heads
         s3 = synth.config3(0)
