@@ -435,6 +435,18 @@ eh_status eh_stream_pages(eh_context* ctx, eh_stream stream, const eh_kv_layout*
                           const void* pool, uint64_t pool_bytes, const uint32_t* ids,
                           uint64_t ids_bytes, uint32_t n_ids, uint32_t depth, uint32_t grid,
                           uint32_t* out, uint64_t out_bytes);
+/* Measurement aid (no counterpart in the reference): the same read in the
+ * token-balanced decode's access pattern, one wave per kv head.  The page
+ * list is cut into equal contiguous ranges, one per group of n_kv waves
+ * (n_kv = row_len / head_dim: 1, 2, 4 or 8); wave h of a group reads only kv
+ * head h's K and V rows of each page, two pages in flight, as the decode's
+ * waves of one run do.  Pages of 16 tokens and kv head rows of 256 bytes
+ * (head_dim * element bytes); out as eh_stream_pages (grid * 8 words, the
+ * xor of every word each wave read). */
+eh_status eh_stream_pages_heads(eh_context* ctx, eh_stream stream, const eh_kv_layout* layout,
+                                const void* pool, uint64_t pool_bytes, const uint32_t* ids,
+                                uint64_t ids_bytes, uint32_t n_ids, uint32_t head_dim,
+                                uint32_t grid, uint32_t* out, uint64_t out_bytes);
 
 /* ---- eh_append_decode_batched without a workspace argument, for callers
  * that cannot allocate device memory (code under HIP graph capture, tight

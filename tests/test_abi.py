@@ -47,7 +47,7 @@ def test_code_objects_contain_launched_kernels():
             assert f"{k}{ch}".encode() in kv
     for k in ("eh_remap_block_tables", "eh_page_refcounts", "eh_fill_u32", "eh_append_kv_e4m3",
               "eh_gather_kv_e4m3", "eh_kv_e4m3_scales", "eh_stream_pages_d1",
-              "eh_stream_pages_d2"):
+              "eh_stream_pages_d2", "eh_stream_pages_heads"):
         assert k.encode() in kv
     for dt in ("f32", "f16", "bf16"):
         dec = open(os.path.join(_lib.LIB_DIR, f"paged_decode_{dt}.hsaco"), "rb").read()

@@ -211,3 +211,40 @@ def test_copy_pages_remap_and_refcounts(dev):
         for p in r[:n]:
             exp_counts[p] += 1
     assert np.array_equal(counts.cpu().numpy(), exp_counts)
+
+
+@pytest.mark.parametrize("n_kv,hd,dtype", [(2, 128, KvDataType.F16), (8, 128, KvDataType.F16),
+                                           (4, 64, KvDataType.F32), (1, 128, KvDataType.BF16)],
+                         ids=["2x128-f16", "8x128-f16", "4x64-f32", "1x128-bf16"])
+def test_stream_pages_fold_every_listed_word(dev, n_kv, hd, dtype):
+    """The read-ceiling aids fold every word of the listed pages into their
+    per-wave xors exactly once: the xor over all waves equals the xor of
+    the listed pages' words on the host, for whole pages (eh_stream_pages,
+    depth 1 and 2, where pages are a multiple of 16 KiB) and for the
+    per-kv-head pattern of the decode (eh_stream_pages_heads), on grids
+    smaller and larger than the page count; an id past the pool is skipped."""
+    bt, nb = 16, 37
+    rl = n_kv * hd
+    layout = PagedKvLayout(nb, bt, rl, dtype)
+    rng = np.random.default_rng(77 + n_kv + hd)
+    words = rng.integers(0, 2**32, size=layout.bytes_total() // 4, dtype=np.uint32)
+    pool = to_dev(words, dev)
+    listed = rng.permutation(nb)[:29].astype(np.uint32)
+    ids = np.insert(listed, 11, nb + 5)                      # past the pool: skipped
+    dids = to_dev(ids, dev)
+    pw = layout.page_bytes() // 4
+    want = np.bitwise_xor.reduce(np.concatenate([words[p * pw:(p + 1) * pw] for p in listed]))
+    kv = PagedKvGpu(0)
+    for grid in (1, 3, 64):
+        out = torch.zeros(grid * 8, dtype=torch.int32, device=dev)
+        kv.stream_pages_heads(None, layout, pool, dids, out, hd, grid)
+        torch.cuda.synchronize()
+        got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+        assert got == want, ("heads", grid)
+        if layout.page_bytes() % 16384 == 0:
+            for depth in (1, 2):
+                out.zero_()
+                kv.stream_pages(None, layout, pool, dids, out, depth, grid)
+                torch.cuda.synchronize()
+                got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+                assert got == want, ("whole", depth, grid)

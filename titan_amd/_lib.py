@@ -50,6 +50,8 @@ _SIGS = {
     "eh_copy_pages": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, vp, u32]),
     "eh_remap_block_tables": (i32, [vp, vp, vp, u64, vp, u32]),
     "eh_stream_pages": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, u32, u32, u32, vp, u64]),
+    "eh_stream_pages_heads": (i32, [vp, vp, P(eh_kv_layout), vp, u64, vp, u64, u32, u32, u32, vp,
+                                    u64]),
     "eh_page_refcounts": (i32, [vp, vp, vp, u32, vp, u32, vp, u32]),
     "eh_paged_attention": (i32, [vp, vp, u32, vp, u64, vp, u64, vp, u64, vp, u64, u64, u64, u64,
                                  u64, u64, u64, i32, vp]),

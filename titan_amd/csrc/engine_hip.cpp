@@ -960,6 +960,37 @@ eh_status eh_stream_pages(eh_context* c, eh_stream stream, const eh_kv_layout* l
                   (uint64_t)l->n_blocks, out);
 }
 
+eh_status eh_stream_pages_heads(eh_context* c, eh_stream stream, const eh_kv_layout* l,
+                               const void* pool, uint64_t pool_bytes, const uint32_t* ids,
+                               uint64_t ids_bytes, uint32_t n_ids, uint32_t head_dim, uint32_t grid,
+                               uint32_t* out, uint64_t out_bytes) {
+    if (!c || !l) return fail(EH_INVALID_ARGS, "null context or layout");
+    if (eh_status ls = check_layout(l)) return ls;
+    const uint64_t elt = elt_bytes(l->data_type);
+    if (!elt) return fail(EH_UNSUPPORTED, "data_type");
+    if (l->block_tokens != 16) return fail(EH_UNSUPPORTED, "block_tokens: 16", 16, l->block_tokens);
+    if (head_dim == 0 || l->row_len % head_dim)
+        return invalid_size(head_dim, l->row_len, "head_dim (dividing row_len)");
+    if (head_dim * elt != 256) return fail(EH_UNSUPPORTED, "kv head row: 256 bytes", 256, head_dim * elt);
+    const uint64_t n_kv = l->row_len / head_dim;
+    if (n_kv != 1 && n_kv != 2 && n_kv != 4 && n_kv != 8)
+        return fail(EH_UNSUPPORTED, "kv heads: 1, 2, 4 or 8", 8, n_kv);
+    const uint64_t pool_expected = eh_kv_layout_bytes_total(l);
+    if (pool_bytes < pool_expected) return invalid_size(pool_expected, pool_bytes);
+    if (grid < 1) return invalid_size(1, grid, "grid");
+    if (n_ids == 0) return EH_OK;
+    if (!ids || !out || !pool) return fail(EH_INVALID_ARGS, "null pool, ids or out");
+    if (ids_bytes < 4ull * n_ids) return invalid_size(4ull * n_ids, ids_bytes, "ids");
+    const uint64_t out_need = smul(4, grid, 8);
+    if (out_bytes < out_need) return invalid_size(out_need, out_bytes, "out");
+    eh_status st = bind(c);
+    if (st) return st;
+    const uint64_t row_bytes = l->row_len * elt;
+    return launch(c, c->mod_kv, "eh_stream_pages_heads", dim3(grid), dim3(512), stream,
+                  (const uint8_t*)pool, ids, n_ids, smul(16, 2, row_bytes), (uint64_t)l->n_blocks,
+                  (uint32_t)row_bytes, (uint32_t)n_kv, out);
+}
+
 eh_status eh_remap_block_tables(eh_context* c, eh_stream stream, uint32_t* bt, uint64_t n_entries,
                                 const uint32_t* remap, uint32_t n_remap) {
     if (!c) return fail(EH_INVALID_ARGS, "null context");

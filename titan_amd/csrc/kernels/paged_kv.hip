@@ -385,3 +385,51 @@ __device__ __forceinline__ void stream_pages_body(const uint8_t* __restrict__ po
     }
 EH_STREAM_PAGES(1)
 EH_STREAM_PAGES(2)
+
+// The same read in the decode's pattern (a measurement aid): the token-balanced
+// decode runs one wave per kv head, and the waves of a run walk the same pages
+// together, each reading only its kv head's K and V rows.  Here the page list
+// is cut into equal contiguous ranges, one per group of n_kv waves (8 / n_kv
+// groups per workgroup); wave h of a group reads kv head h's 256-byte slice of
+// the K row and of the V row of every token (16 lanes per slice, 4 tokens per
+// instruction), two pages in flight.  Pages hold 16 tokens; row_bytes is one
+// K (or V) row, n_kv * 256 bytes.  Every word read is folded into one xor per
+// wave; ids past the pool are skipped (read as page 0, not folded).
+extern "C" __global__ __launch_bounds__(512) void eh_stream_pages_heads(
+    const uint8_t* __restrict__ pool, const uint32_t* __restrict__ ids, uint32_t n_ids,
+    uint64_t page_bytes, uint64_t n_blocks, uint32_t row_bytes, uint32_t n_kv,
+    uint32_t* __restrict__ out) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = blockIdx.x * 8u + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t G = gridDim.x * 8u / n_kv, g = w / n_kv, h = w % n_kv;
+    const uint32_t i0 = (uint32_t)((uint64_t)n_ids * g / G), i1 = (uint32_t)((uint64_t)n_ids * (g + 1) / G);
+    uint32_t off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)  // j < 4: K rows of tokens 4j..4j+3, j >= 4: V rows
+        off[j] = (4u * (j & 3) + lane / 16u) * 2u * row_bytes + (j >= 4 ? row_bytes : 0u) +
+                 h * 256u + (lane & 15u) * 16u;
+    u32x4v acc = {0u, 0u, 0u, 0u};
+    for (uint32_t i = i0; i < i1; i += 2) {
+        const uint32_t pa = ids[i], pb = ids[i + 1 < i1 ? i + 1 : i];
+        const bool oka = (uint64_t)pa < n_blocks, okb = i + 1 < i1 && (uint64_t)pb < n_blocks;
+        const uint8_t* a = pool + (oka ? (uint64_t)pa : 0u) * page_bytes;
+        const uint8_t* b = pool + ((uint64_t)pb < n_blocks ? (uint64_t)pb : 0u) * page_bytes;
+        u32x4v r[16];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = *reinterpret_cast<const u32x4v*>(a + off[j]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[8 + j] = *reinterpret_cast<const u32x4v*>(b + off[j]);
+        u32x4v xa = r[0], xb = r[8];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            xa ^= r[j];
+            xb ^= r[8 + j];
+        }
+        acc ^= oka ? xa : u32x4v{0u, 0u, 0u, 0u};
+        acc ^= okb ? xb : u32x4v{0u, 0u, 0u, 0u};
+    }
+    uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v ^= (uint32_t)__shfl_xor((int)v, o, 64);
+    if (lane == 0) out[w] = v;
+}

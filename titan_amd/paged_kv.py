@@ -175,6 +175,18 @@ class PagedKvGpu:
                                       C.byref(layout.c()), pp, pb, ip, ib, int(ids.numel()),
                                       int(depth), int(grid), op, ob))
 
+    def stream_pages_heads(self, stream, layout, pool, ids, out, head_dim, grid=256):
+        """Measurement aid (no reference counterpart): reads the pages listed
+        in `ids` in the token-balanced decode's pattern, one wave per kv head
+        reading only that head's K and V rows, the n_kv waves of a group
+        walking the same pages (two in flight); `out` as stream_pages."""
+        pp, pb = buf(pool)
+        ip, ib = buf(ids)
+        op, ob = buf(out)
+        check(self._L.eh_stream_pages_heads(self._ctx.handle, stream_handle(stream),
+                                            C.byref(layout.c()), pp, pb, ip, ib, int(ids.numel()),
+                                            int(head_dim), int(grid), op, ob))
+
     def remap_block_tables(self, stream, block_tables, remap):
         """entry = remap[entry] for every entry below len(remap)."""
         check(self._L.eh_remap_block_tables(self._ctx.handle, stream_handle(stream),
