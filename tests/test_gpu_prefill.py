@@ -683,3 +683,54 @@ def test_graph_replay_successive_chunks(dev, dtype):
                         KvDataType.F16 if dtype == KvDataType.FP8 else dtype, f"chunk {k} seq {b}")
         assert np.isnan(gh[cu[B]:]).all()                            # rows past the chunks untouched
         done += lens[k]
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.BF16, KvDataType.F16, KvDataType.FP8],
+                         ids=lambda d: d.name)
+def test_long_prompt_in_one_chunk(dev, dtype):
+    """A whole 8192-token prompt in one chunk (position 0) beside a
+    3000-token chunk continuing at position 5000, 32/8 heads, hd 128, pages
+    of 16 on scattered tables: each row block walks up to 128 key tiles
+    (the random sweeps stop near 700-token chunks).  40 sampled query rows
+    against the oracle (first and last rows, row-block edges, random),
+    strict bar; bf16 pages run the ping-pong kernel."""
+    nh, nkv, hd, bt = 32, 8, 128, 16
+    starts, lens = np.array([0, 5000]), np.array([8192, 3000])
+    rng = np.random.default_rng(5100 + int(dtype))
+    need = [-(-(s + n) // bt) for s, n in zip(starts, lens)]
+    n_pages = sum(need) + 3
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    tables = np.full((2, max(need)), 0xFFFFFFFF, np.uint32)
+    tables[0, :need[0]] = perm[:need[0]]
+    tables[1, :need[1]] = perm[need[0]:need[0] + need[1]]
+    if dtype == KvDataType.FP8:
+        codes, ks, vs = gauss_codes(rng, n_pages, bt, nkv, hd)
+        dpool = torch.from_numpy(codes).to(dev)
+        f = orc.e4m3_to_f32(codes).reshape(n_pages, bt, 2, nkv, hd)
+        f[:, :, 0] *= ks[None, None, :, None]
+        f[:, :, 1] *= vs[None, None, :, None]
+        hpool = f.reshape(-1)
+    else:
+        dpool, hpool = make_pool(rng, n_pages, bt, nkv, hd, dtype, dev)
+    total = int(lens.sum())
+    q = rng.standard_normal((total, nh, hd)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    out = torch.full((total, nh, hd), float("nan"), device=dev)
+    args = (None, torch.from_numpy(q).to(dev), dpool, i32(tables, dev), i32(cu, dev),
+            i32(starts.astype(np.uint32), dev), out, nh, nkv, hd, bt, int(lens.max()))
+    if dtype == KvDataType.FP8:
+        FlashAttention2(0).launch_batched_e4m3(*args, torch.from_numpy(ks).to(dev),
+                                               torch.from_numpy(vs).to(dev))
+    else:
+        FlashAttention2(0).launch_batched(*args, kv_dtype=dtype)
+    torch.cuda.synchronize()
+    g = out.cpu().numpy()
+    assert not np.isnan(g).any()
+    edges = [0, 1, 63, 64, 8191, 8192, 8192 + 2999, 4096 - 1, 4096, 8192 + 1500]
+    for r in np.concatenate([edges, rng.integers(0, total, size=30)]):
+        b = 0 if r < lens[0] else 1
+        i = int(r - cu[b])
+        ref = orc.prefill_causal(hpool, tables[b, :need[b]], bt, q[r:r + 1], 1, int(starts[b]) + i,
+                                 nh, nkv, hd)
+        check_close(g[r:r + 1], ref, KvDataType.F16 if dtype == KvDataType.FP8 else dtype,
+                    f"row {r}")
