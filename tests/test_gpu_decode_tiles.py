@@ -1095,3 +1095,43 @@ def test_scheduled_steps_on_two_streams(dev):
                                       (j["lens"] + 1).astype(np.uint32), bt, j["q"], n_head, n_kv,
                                       hd)
         check_close(con_outs[i].cpu().numpy(), ref, f"stream {i}")
+
+
+@pytest.mark.parametrize("shape", [(12, 2, 128, 16), (32, 8, 128, 16)], ids=["12x2", "32x8"])
+def test_largest_batch(dev, shape):
+    """The largest batch the token-balanced kernel takes, 2048 sequences
+    (lengths and tile offsets staged in LDS), with short ragged contexts
+    (some empty): the self-scheduled decode against the oracle, and the
+    scheduled fused step (schedule + append + decode) against the
+    self-scheduled fused step, pool and output bit for bit."""
+    n_head, n_kv, hd, bt = shape
+    B = 2048
+    rng = np.random.default_rng(2048 + n_kv)
+    lens = rng.integers(0, 60, size=B).astype(np.int64)
+    lens[rng.integers(0, B, size=40)] = 0
+    out, pool_f32, tab, q = run_decode(dev, KvDataType.F16, lens, shape, 2048 + n_kv)
+    ref = orc.sdpa_decode_batched(pool_f32, tab, lens.astype(np.uint32), bt, q, n_head, n_kv, hd)
+    check_close(out, ref, "B=2048")
+    # fused step: append one token at position lens[b], attend lens[b] + 1 tokens
+    tab2, nb = make_tables(rng, lens + 1, bt)
+    layout = PagedKvLayout(nb, bt, n_kv * hd, KvDataType.F16)
+    pool_a, _ = make_pool(rng, nb, bt, n_kv, hd, KvDataType.F16, dev)
+    pool_b = pool_a.clone()
+    k = torch.from_numpy(rng.standard_normal((B, n_kv * hd)).astype(np.float16)).to(dev)
+    v = torch.from_numpy(rng.standard_normal((B, n_kv * hd)).astype(np.float16)).to(dev)
+    dq = torch.from_numpy(rng.standard_normal((B, n_head, hd)).astype(np.float32)).to(dev)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(lens.max()) + 1)
+    ws = PagedAttention.workspace(plan)
+    pa = PagedAttention(0)
+    dtab, pos = i32(tab2, dev), i32(lens, dev)
+    out_a = torch.full((B, n_head, hd), float("nan"), device=dev)
+    out_b = torch.full_like(out_a, float("nan"))
+    pa.append_decode_batched(None, layout, pool_a, k, v, dtab, pos, dq, out_a, n_head, hd, plan, ws)
+    sched = PagedAttention.schedule_buffer(B, tab2.shape[1], bt, plan)
+    pa.build_schedule(None, layout, dtab, pos, 1, plan, sched)
+    pa.append_decode_scheduled(None, layout, pool_b, k, v, sched, tab2.shape[1], dq, out_b, n_head,
+                               hd, plan, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a.view(torch.int16), pool_b.view(torch.int16))
+    assert torch.equal(out_a.view(torch.int32), out_b.view(torch.int32))
+    assert not torch.isnan(out_a).any()
