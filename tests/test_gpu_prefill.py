@@ -10,8 +10,9 @@ staged (exact below 2^16) and take the same path, and a tile holding a bf16
 value of magnitude 2^16 or more is re-staged raw and run on bf16 MFMAs with q
 and P as hi + lo bf16 pairs.  Shapes: the
 reference's own FA2 test (flash_attention_parity.rs:45-207), ragged chunks on
-scattered pages, GQA groups 1..8, both compiled head sizes, and benchmark
-config 3 (sampled rows at full size).
+scattered pages, GQA groups 1..8, both compiled head sizes, benchmark
+config 3 (sampled rows at full size), a whole 8192-token prompt in one chunk,
+and one captured graph replayed over successive chunks.
 """
 import numpy as np
 import pytest
