@@ -200,19 +200,7 @@ __device__ __forceinline__ void decode_split(
     const uint32_t b = blockIdx.z;
     const uint32_t qh0 = hk * group + hc * G;
 
-    const uint32_t n = live_tokens(L, b);
     const uint32_t t0 = split * tps;
-    if (t0 >= n) {
-        // No live tokens at all: the output is zero (forward_cpu.rs:436-439).
-        if (n == 0 && split == 0)
-            for (int idx = threadIdx.x; idx < G * HD; idx += NW * 64)
-                if (hc * G + idx / HD < group)
-                    out[((uint64_t)b * n_head + qh0 + idx / HD) * HD + idx % HD] = 0.0f;
-        return;
-    }
-    const uint32_t t1 = (n - t0 < tps) ? n : t0 + tps;
-    const uint32_t nsplit = split_count(n, tps, max_splits);
-
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int grp = lane / LPT;
@@ -228,9 +216,13 @@ __device__ __forceinline__ void decode_split(
         return bt_shift >= 0 ? (t >> bt_shift) : (t / block_tokens);
     };
 
-    // Stage the block-table slice of this split (invalid entries -> ~0).
+    // Stage the block-table slice of this split's whole range (invalid
+    // entries -> ~0) and load the query slice before the live length is
+    // known: with a device position that length is one more memory round
+    // trip.  Entries past the length are staged and never read; the host's
+    // bound on tokens per split keeps a whole range's slice inside BT_SLICE.
     const uint32_t pg0 = page_of(t0);
-    const uint32_t npg = page_of(t1 - 1) - pg0 + 1;
+    const uint32_t npg = page_of(t0 + tps - 1) - pg0 + 1;
     for (uint32_t i = threadIdx.x; i < npg && i < BT_SLICE; i += NW * 64) {
         const uint32_t pg = pg0 + i;
         s_bt[i] = pg < bt_stride ? bt_row[pg] : 0xFFFFFFFFu;
@@ -257,6 +249,18 @@ __device__ __forceinline__ void decode_split(
             for (int e = 0; e < EPL; ++e) qv[h][e] = qp[e] * sc;
         }
     }
+
+    const uint32_t n = live_tokens(L, b);
+    if (t0 >= n) {  // uniform over the workgroup
+        // No live tokens at all: the output is zero (forward_cpu.rs:436-439).
+        if (n == 0 && split == 0)
+            for (int idx = threadIdx.x; idx < G * HD; idx += NW * 64)
+                if (hc * G + idx / HD < group)
+                    out[((uint64_t)b * n_head + qh0 + idx / HD) * HD + idx % HD] = 0.0f;
+        return;
+    }
+    const uint32_t t1 = (n - t0 < tps) ? n : t0 + tps;
+    const uint32_t nsplit = split_count(n, tps, max_splits);
 
     float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -745,9 +749,9 @@ __device__ __forceinline__ void decode_slots(
 // Log-sum-exp merge of split partials: out = sum_s w_s acc_s / sum_s w_s l_s
 // with w_s = exp2(m_s - max m), splits with l_s == 0 skipped.  One thread
 // per output element (grid (ceil(n_head * head_dim / 256), batch), 256
-// threads); the partials of 8 splits are fetched together before they are
-// folded in (an online max keeps one pass), so a context of S splits costs
-// ceil(S / 8) memory round trips.
+// threads); the partials of up to 32 splits are fetched together before they
+// are folded in (an online max keeps one pass), so a context of S splits
+// costs ceil(S / 32) memory round trips, the first beside the length read.
 extern "C" __global__ __launch_bounds__(256) void eh_decode_merge(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml, float* __restrict__ out,
     const uint32_t* lens_ptr, uint32_t lens_mode, uint32_t seq_tokens, uint32_t query_pos,
@@ -756,25 +760,36 @@ extern "C" __global__ __launch_bounds__(256) void eh_decode_merge(
     const uint32_t b = blockIdx.y;
     const uint32_t e = blockIdx.x * 256 + threadIdx.x;
     if (e >= n_head * head_dim) return;
-    const uint32_t n = live_tokens(L, b);
-    const uint32_t nsplit = split_count(n, tps, max_splits);
-    if (n == 0 || nsplit <= 1) return;  // the split kernel wrote the output
     const uint32_t qh = e / head_dim, d = e - qh * head_dim;
     const uint64_t qrow = (uint64_t)b * n_head + qh;
     const float2* ml = reinterpret_cast<const float2*>(part_ml) + qrow * max_splits;
     const float* pa = part_acc + qrow * max_splits * head_dim + d;
     // Partials in batches of NB: every load of a batch is in flight at once
-    // (one memory round trip for up to NB splits).
+    // (one memory round trip for up to NB splits).  The first batch goes out
+    // before the live length is known (a device position is one more round
+    // trip): slots past the length lie inside the row's max_splits slots and
+    // are not folded.
     constexpr int NB = 32;
+    float2 v[NB];
+    float x[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t sidx = (uint32_t)i < max_splits ? (uint32_t)i : 0u;
+        v[i] = ml[sidx];
+        x[i] = pa[(uint64_t)sidx * head_dim];
+    }
+    const uint32_t n = live_tokens(L, b);
+    const uint32_t nsplit = split_count(n, tps, max_splits);
+    if (n == 0 || nsplit <= 1) return;  // the split kernel wrote the output
     float M = -INFINITY, Ls = 0.0f, A = 0.0f;
     for (uint32_t s0 = 0; s0 < nsplit; s0 += NB) {
-        float2 v[NB];
-        float x[NB];
+        if (s0 > 0) {
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const uint32_t sidx = s0 + i < nsplit ? s0 + i : s0;
-            v[i] = ml[sidx];
-            x[i] = pa[(uint64_t)sidx * head_dim];
+            for (int i = 0; i < NB; ++i) {
+                const uint32_t sidx = s0 + i < nsplit ? s0 + i : s0;
+                v[i] = ml[sidx];
+                x[i] = pa[(uint64_t)sidx * head_dim];
+            }
         }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
