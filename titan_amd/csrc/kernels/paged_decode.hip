@@ -222,7 +222,8 @@ __device__ __forceinline__ void decode_split(
     // trip.  Entries past the length are staged and never read; the host's
     // bound on tokens per split keeps a whole range's slice inside BT_SLICE.
     const uint32_t pg0 = page_of(t0);
-    const uint32_t npg = page_of(t0 + tps - 1) - pg0 + 1;
+    const uint32_t t_end = t0 > 0xFFFFFFFFu - tps ? 0xFFFFFFFFu : t0 + tps;  // >= every t1
+    const uint32_t npg = page_of(t_end - 1) - pg0 + 1;
     for (uint32_t i = threadIdx.x; i < npg && i < BT_SLICE; i += NW * 64) {
         const uint32_t pg = pg0 + i;
         s_bt[i] = pg < bt_stride ? bt_row[pg] : 0xFFFFFFFFu;
