@@ -319,19 +319,25 @@ __device__ __forceinline__ void decode_split(
                 s[h] = group_sum<LPT>(p);
             }
             const bool okj = ok[j];
+            // A masked lane (past the range, or on an invalid page) adds
+            // nothing: its V row is a stand-in (the wave's first row, page 0,
+            // or an appended row not written yet), and a zero weight on a
+            // non-finite row would not be zero.
+            if (okj) {
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                if (okj && s[h] > m[h]) {  // rescale only when the running max moves
-                    const float corr = fast_exp2(m[h] - s[h]);
-                    l[h] *= corr;
+                for (int h = 0; h < G; ++h) {
+                    if (s[h] > m[h]) {  // rescale only when the running max moves
+                        const float corr = fast_exp2(m[h] - s[h]);
+                        l[h] *= corr;
 #pragma unroll
-                    for (int e = 0; e < EPL; ++e) acc[h][e] *= corr;
-                    m[h] = s[h];
+                        for (int e = 0; e < EPL; ++e) acc[h][e] *= corr;
+                        m[h] = s[h];
+                    }
+                    const float p = fast_exp2(s[h] - m[h]);
+                    l[h] += p;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p, elem<DT>(vr[j], e), acc[h][e]);
                 }
-                const float p = okj ? fast_exp2(s[h] - m[h]) : 0.0f;
-                l[h] += p;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p, elem<DT>(vr[j], e), acc[h][e]);
             }
             if (new_k != nullptr && okj) {  // fused append: write the new row to its page
                 const uint32_t t = w0 + (uint32_t)(k * NW * TPW) + grp;
@@ -660,6 +666,13 @@ __device__ __forceinline__ void decode_slots(
             scores(kr[j0], ok[j0], s0);
             scores(kr[j1], ok[j1], s1);
             rescale_if(s0, s1);
+            // masked tokens (invalid pages read page 0) carry zero V words:
+            // their weights are 0, and 0 times a non-finite word would not be
+#pragma unroll
+            for (int w = 0; w < NWD; ++w) {
+                vr[j0].w[w] = ok[j0] ? vr[j0].w[w] : 0u;
+                vr[j1].w[w] = ok[j1] ? vr[j1].w[w] : 0u;
+            }
             if constexpr (DT == DT_F16) {
                 uint32_t vp[EPL];  // (token k, token k+1) pairs per dim
 #pragma unroll

@@ -580,13 +580,18 @@ __device__ __forceinline__ void decode_tiles(
                 const float sc = kh ? k_scale[kv] : v_scale[kv];
                 const uint32_t c4 = e4m3_code(nv.x / sc) | (e4m3_code(nv.y / sc) << 8) |
                                     (e4m3_code(nv.z / sc) << 16) | (e4m3_code(nv.w / sc) << 24);
+                // Lanes of tokens past pos (masked) take the appended token's
+                // codes as well: they re-read the tile's first token, which is
+                // the appended one when it opens the tile, and its pool row is
+                // not written yet (a zero weight on a non-finite V row would
+                // not be zero).
                 static_for<0, KREG>([&](auto Sc) {
                     constexpr int j = decltype(Sc)::value;
                     u32x4 c;
 #pragma unroll
                     for (int w = 0; w < 4; ++w)
                         c[w] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((8u * g + 4u * j + w) * 4u), (int)c4);
-                    if (x == pos) kr[D][j] = c;
+                    if (x >= pos) kr[D][j] = c;
                 });
                 u32x4 cv;
 #pragma unroll
@@ -594,14 +599,19 @@ __device__ __forceinline__ void decode_tiles(
                     cv[w] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((32u + 4u * (lane & 7u) + w) * 4u), (int)c4);
                 static_for<0, VREG>([&](auto Rc) {
                     constexpr int j = decltype(Rc)::value;
-                    if (v_tok(j) == pos) vr[D][j] = cv;
+                    if (v_tok(j) >= pos) vr[D][j] = cv;
                 });
             }
         } else {
-            const uint32_t pos = nvalid - 1u;  // appended token within the tile (when last)
+            // appended token within the tile (when last); lanes of tokens past
+            // it (masked) read the appended row too, not the tile's first
+            // token, which is the appended one when it opens the tile and is
+            // not in the pool yet (a zero weight on a non-finite V row would
+            // not be zero)
+            const uint32_t pos = nvalid - 1u;
             const uint64_t nrow = (uint64_t)ib * row_bytes + kv_off;
             {
-                const bool isnew = last && x == pos;
+                const bool isnew = last && x >= pos;
                 const uint8_t* src = isnew ? new_k + nrow : base + (x < nvalid ? x : 0u) * slot_bytes;
                 static_for<0, KREG>([&](auto Sc) {
                     constexpr int j = decltype(Sc)::value;
@@ -611,7 +621,7 @@ __device__ __forceinline__ void decode_tiles(
             static_for<0, VREG>([&](auto Rc) {
                 constexpr int j = decltype(Rc)::value;
                 const uint32_t t = v_tok(j);
-                const bool isnew = last && t == pos;
+                const bool isnew = last && t >= pos;
                 const uint8_t* src = isnew ? new_v + nrow
                                            : base + row_bytes + (t < nvalid ? t : 0u) * slot_bytes;
                 vr[D][j] = *reinterpret_cast<const u32x4*>(src + v_off);
