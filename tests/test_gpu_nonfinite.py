@@ -12,7 +12,8 @@ such a V row (0 * NaN = NaN) would fail.  The paths covered:
   * the fixed-split and slot-major kernels of one sequence, with host and
     device positions, the fused append onto a new page, and invalid table
     entries inside the attended range (their stand-in, page 0, is NaN);
-  * chunked prefill, both kernels.
+  * chunked prefill, both kernels, also with invalid table entries inside a
+    chunk's causal window (page 0 NaN).
 Outputs are compared with the oracle, which reads only the attended tokens,
 or, where the table has invalid entries, with a float64 numpy attention over
 the tokens on valid pages; the bar is the usual one (tests/parity.py), and
@@ -307,3 +308,41 @@ def test_prefill(dev, monkeypatch, dtype, kern):
         ref = orc.prefill_causal(host.reshape(-1), tab[b, :k], bt, q[cu[b]:cu[b + 1]],
                                  int(lens[b]), int(starts[b]), nh, nkv, hd)
         check(g[cu[b]:cu[b + 1]], ref, False, f"{dtype.name} {kern} seq {b}")
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16], ids=lambda d: d.name)
+@pytest.mark.parametrize("kern", ["single", "pp"])
+def test_prefill_invalid_pages(dev, monkeypatch, dtype, kern):
+    """Invalid table entries inside a prefill chunk's causal window mask
+    their keys; both kernels read page 0 in their place, and page 0 here is
+    all NaN.  Every query row against a float64 attention over its causal
+    keys on valid pages."""
+    monkeypatch.setenv("EH_PREFILL_KERNEL", kern)
+    nh, nkv, hd, bt = 8, 2, 128, 16
+    rl = nkv * hd
+    rng = np.random.default_rng(83 + int(dtype))
+    p0, nq = 40, 90
+    n = p0 + nq
+    n_pg = -(-n // bt)
+    nb = n_pg + 3
+    table = (1 + rng.permutation(nb - 1)[:n_pg]).astype(np.uint32)   # page 0 is never used
+    bad = [1, 5]
+    table[bad] = [NONE, nb + 9]
+    host = np.full((nb, bt, 2, rl), np.nan, np.float32)
+    for t in range(n):
+        if t // bt not in bad:
+            host[table[t // bt], t % bt] = rng.standard_normal((2, rl)).astype(np.float32)
+    pool_t = torch.from_numpy(host.reshape(-1)).to(TDT[dtype])
+    host = pool_t.to(torch.float32).numpy().reshape(nb, bt, 2, rl)
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    out = torch.full((nq, nh, hd), float("nan"), device=dev)
+    FlashAttention2(0).launch_batched(None, torch.from_numpy(q).to(dev), pool_t.to(dev),
+                                      i32(table[None, :], dev), i32(np.array([0, nq]), dev),
+                                      i32(np.array([p0]), dev), out, nh, nkv, hd, bt, nq,
+                                      kv_dtype=dtype)
+    torch.cuda.synchronize()
+    g = out.cpu().numpy()
+    assert np.isfinite(g).all()
+    ref = np.stack([np_attend(host, table, [t for t in range(p0 + i + 1) if t // bt not in bad],
+                              q[i], nh, nkv, hd) for i in range(nq)])
+    check(g, ref, False, f"{dtype.name} {kern}")
