@@ -12,6 +12,7 @@ such a V row (0 * NaN = NaN) would fail.  The paths covered:
   * the fixed-split and slot-major kernels of one sequence, with host and
     device positions, the fused append onto a new page, and invalid table
     entries inside the attended range (their stand-in, page 0, is NaN);
+  * decode over the protected-sinks range, with every unattended row NaN;
   * chunked prefill, both kernels, also with invalid table entries inside a
     chunk's causal window (page 0 NaN).
 Outputs are compared with the oracle, which reads only the attended tokens,
@@ -346,3 +347,68 @@ def test_prefill_invalid_pages(dev, monkeypatch, dtype, kern):
     ref = np.stack([np_attend(host, table, [t for t in range(p0 + i + 1) if t // bt not in bad],
                               q[i], nh, nkv, hd) for i in range(nq)])
     check(g, ref, False, f"{dtype.name} {kern}")
+
+
+@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16, KvDataType.FP8],
+                         ids=lambda d: d.name)
+@pytest.mark.parametrize("sink,window", [(4, 15), (0, 40), (5, 3), (20, 100), (17, 1)])
+def test_window_decode_unattended_rows(dev, dtype, sink, window):
+    """Decode over the protected-sinks range where every token outside the
+    sinks and the window holds NaN on its valid page (and the page tails and
+    unreferenced pages too): tiles that the range cuts (the sink edge, the
+    window's first tile, the last tile) mix attended and NaN rows.  Output and
+    per-page H2O mass against the oracle, which reads only attended tokens."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    rl = n_kv * hd
+    rng = np.random.default_rng(71 + 3 * sink + window + int(dtype))
+    lens = np.array([0, 1, 5, 17, 33, 300, 2049, 100, 7, 64], np.int64)
+    B = len(lens)
+    tab, nb = tables(rng, lens, bt)
+
+    def attended(n):
+        if n == 0:
+            return []
+        lo = max(sink, n - 1 - window)
+        return [t for t in range(n) if t < sink or t >= lo]
+
+    ks = vs = None
+    if dtype == KvDataType.FP8:
+        ksn = np.full(n_kv, 4.0 / 448, np.float32)
+        vsn = np.full(n_kv, 4.0 / 448, np.float32)
+        codes = np.full((nb, bt, 2, n_kv, hd), 0x7F, np.uint8)
+        for b, n in enumerate(lens):
+            for t in attended(int(n)):
+                x = rng.standard_normal((2, n_kv, hd)).astype(np.float32)
+                for hh in range(n_kv):
+                    codes[tab[b, t // bt], t % bt, 0, hh] = orc.f32_to_e4m3(x[0, hh], ksn[hh])
+                    codes[tab[b, t // bt], t % bt, 1, hh] = orc.f32_to_e4m3(x[1, hh], vsn[hh])
+        f = orc.e4m3_to_f32(codes.reshape(-1)).reshape(nb, bt, 2, n_kv, hd)
+        f[:, :, 0] *= ksn[None, None, :, None]
+        f[:, :, 1] *= vsn[None, None, :, None]
+        host = f.reshape(-1)
+        pool = torch.from_numpy(codes.reshape(-1)).to(dev)
+        ks, vs = torch.from_numpy(ksn).to(dev), torch.from_numpy(vsn).to(dev)
+    else:
+        h = np.full((nb, bt, 2, rl), np.nan, np.float32)
+        for b, n in enumerate(lens):
+            for t in attended(int(n)):
+                h[tab[b, t // bt], t % bt] = rng.standard_normal((2, rl)).astype(np.float32)
+        t16 = torch.from_numpy(h.reshape(-1)).to(TDT[dtype])
+        host, pool = t16.to(torch.float32).numpy(), t16.to(dev)
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(lens.max()), 0, dtype)
+    extra = PagedAttention.mass_workspace_bytes(B, tab.shape[1], bt, n_head)
+    ws = torch.zeros((plan[2] + extra + 3) // 4, device=dev)
+    mass = torch.zeros((nb,), device=dev)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    PagedAttention(0).decode_batched_window(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                            i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, sink,
+                                            window, plan, ws, ks, vs, block_mass=mass)
+    torch.cuda.synchronize()
+    ref, ref_mass = orc.sdpa_decode_window_batched(host, tab, lens.astype(np.uint32), bt, q, n_head,
+                                                   n_kv, hd, sink, window, n_blocks=nb)
+    check(out.cpu().numpy(), ref, False, f"{dtype.name} window {sink}/{window}")
+    got = mass.cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    bad = np.abs(got - ref_mass) > 2e-4 * n_head + 1e-3 * ref_mass
+    assert not bad.any(), (np.argwhere(bad)[:4], got[bad][:4], ref_mass[bad][:4])

@@ -682,9 +682,36 @@ __device__ __forceinline__ void decode_tiles(
         const uint32_t nvalid = info & 31u;
         const uint32_t cb = seqp[D];
         const bool win = EXT && window != 0u;
+        // sinks/window: a tile that the attended range cuts (uniform)
+        span sp{};
+        bool cut = false;
+        if constexpr (EXT) {
+            if (win) {
+                sp = make_span(ntok[cb], sink, window);
+                cut = sp.partial(tok0);
+            }
+        }
 
         // V tile rows into LDS as f16 (16-bit lane (g, x): tokens 4g..4g+3,
-        // dims 8x..8x+7; E4M3 lane l: tokens l/8 and l/8 + 8, dims 16 (l%8)..)
+        // dims 8x..8x+7; E4M3 lane l: tokens l/8 and l/8 + 8, dims 16 (l%8)..).
+        // In a cut tile the rows of unattended tokens (outside the sinks and
+        // the window, on a valid page) are zeroed first: their weight is 0,
+        // and 0 times a non-finite row would not be.
+        if constexpr (EXT) {
+            if (cut) {
+                if constexpr (F8) {
+                    static_for<0, VREG>([&](auto Rc) {
+                        constexpr int j = decltype(Rc)::value;
+                        if (!sp.valid(tok0 + (lane >> 3) + 8 * j)) vr[D][j] = u32x4{0u, 0u, 0u, 0u};
+                    });
+                } else {
+                    static_for<0, 4>([&](auto Rc) {
+                        constexpr int r = decltype(Rc)::value;
+                        if (!sp.valid(tok0 + 4 * g + r)) vr[D][r] = u32x4{0u, 0u, 0u, 0u};
+                    });
+                }
+            }
+        }
         if constexpr (F8) {
             static_for<0, VREG>([&](auto Rc) {
                 constexpr int j = decltype(Rc)::value;
@@ -718,8 +745,7 @@ __device__ __forceinline__ void decode_tiles(
         if constexpr (F8) s *= qdown;  // the K scale
         if constexpr (EXT) {
             if (win) {  // uniform
-                const span sp = make_span(ntok[cb], sink, window);
-                if (sp.partial(tok0)) {
+                if (cut) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         s[r] = sp.valid(tok0 + 4 * g + r) ? s[r] : -__builtin_inff();
