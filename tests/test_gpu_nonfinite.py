@@ -13,8 +13,8 @@ such a V row (0 * NaN = NaN) would fail.  The paths covered:
     device positions, the fused append onto a new page, and invalid table
     entries inside the attended range (their stand-in, page 0, is NaN);
   * decode over the protected-sinks range, with every unattended row NaN;
-  * chunked prefill, both kernels, also with invalid table entries inside a
-    chunk's causal window (page 0 NaN).
+  * chunked prefill, both kernels, over f32, f16, bf16 and E4M3 pages, also
+    with invalid table entries inside a chunk's causal window (page 0 NaN).
 Outputs are compared with the oracle, which reads only the attended tokens,
 or, where the table has invalid entries, with a float64 numpy attention over
 the tokens on valid pages; the bar is the usual one (tests/parity.py), and
@@ -281,14 +281,18 @@ def test_single_sequence_invalid_pages(dev, dtype, hd):
     check(out.cpu().numpy(), ref, dtype == KvDataType.F32, f"{dtype.name} hd{hd}")
 
 
-@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16], ids=lambda d: d.name)
-@pytest.mark.parametrize("kern", ["single", "pp"])
-def test_prefill(dev, monkeypatch, dtype, kern):
-    """Causal chunked prefill over NaN-tailed pages, both kernels: keys past
-    each chunk's last position (the rest of its last page) and unreferenced
-    pages hold NaN."""
+@pytest.mark.parametrize("dtype,kern,hd", [
+    (KvDataType.F16, "single", 128), (KvDataType.F16, "pp", 128),
+    (KvDataType.BF16, "single", 128), (KvDataType.BF16, "pp", 128),
+    (KvDataType.F16, "single", 64), (KvDataType.BF16, "pp", 64),
+    (KvDataType.F32, "single", 128), (KvDataType.F32, "single", 64)],
+    ids=lambda v: getattr(v, "name", str(v)))
+def test_prefill(dev, monkeypatch, dtype, kern, hd):
+    """Causal chunked prefill over NaN-tailed pages, both kernels (f32 pages
+    have one): keys past each chunk's last position (the rest of its last
+    page) and unreferenced pages hold NaN."""
     monkeypatch.setenv("EH_PREFILL_KERNEL", kern)
-    nh, nkv, hd, bt = 16, 4, 128, 16
+    nh, nkv, bt = 16, 4, 16
     rl = nkv * hd
     rng = np.random.default_rng(73 + int(dtype))
     starts, lens = np.array([0, 37, 200]), np.array([45, 100, 9])
@@ -308,11 +312,13 @@ def test_prefill(dev, monkeypatch, dtype, kern):
         k = (int(n_tok[b]) + bt - 1) // bt
         ref = orc.prefill_causal(host.reshape(-1), tab[b, :k], bt, q[cu[b]:cu[b + 1]],
                                  int(lens[b]), int(starts[b]), nh, nkv, hd)
-        check(g[cu[b]:cu[b + 1]], ref, False, f"{dtype.name} {kern} seq {b}")
+        check(g[cu[b]:cu[b + 1]], ref, dtype == KvDataType.F32, f"{dtype.name} {kern} seq {b}")
 
 
-@pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16], ids=lambda d: d.name)
-@pytest.mark.parametrize("kern", ["single", "pp"])
+@pytest.mark.parametrize("dtype,kern", [
+    (KvDataType.F16, "single"), (KvDataType.F16, "pp"), (KvDataType.BF16, "single"),
+    (KvDataType.BF16, "pp"), (KvDataType.F32, "single")],
+    ids=lambda v: getattr(v, "name", str(v)))
 def test_prefill_invalid_pages(dev, monkeypatch, dtype, kern):
     """Invalid table entries inside a prefill chunk's causal window mask
     their keys; both kernels read page 0 in their place, and page 0 here is
@@ -346,7 +352,78 @@ def test_prefill_invalid_pages(dev, monkeypatch, dtype, kern):
     assert np.isfinite(g).all()
     ref = np.stack([np_attend(host, table, [t for t in range(p0 + i + 1) if t // bt not in bad],
                               q[i], nh, nkv, hd) for i in range(nq)])
-    check(g, ref, False, f"{dtype.name} {kern}")
+    check(g, ref, dtype == KvDataType.F32, f"{dtype.name} {kern}")
+
+
+def e4m3_pool(rng, nb, bt, n_kv, hd, rows):
+    """E4M3 pool [nb, bt, 2, n_kv, hd] of the NaN code (0x7F) with quantised
+    N(0,1) K/V at the (page, slot) pairs in `rows`, scales 4 / 448; returns
+    the codes, the dequantised f32 pool and the scales."""
+    ks = np.full(n_kv, 4.0 / 448, np.float32)
+    vs = np.full(n_kv, 4.0 / 448, np.float32)
+    codes = np.full((nb, bt, 2, n_kv, hd), 0x7F, np.uint8)
+    for pg, sl in rows:
+        x = rng.standard_normal((2, n_kv, hd)).astype(np.float32)
+        for hh in range(n_kv):
+            codes[pg, sl, 0, hh] = orc.f32_to_e4m3(x[0, hh], ks[hh])
+            codes[pg, sl, 1, hh] = orc.f32_to_e4m3(x[1, hh], vs[hh])
+    f = orc.e4m3_to_f32(codes.reshape(-1)).reshape(nb, bt, 2, n_kv, hd)
+    f[:, :, 0] *= ks[None, None, :, None]
+    f[:, :, 1] *= vs[None, None, :, None]
+    return codes, f.reshape(nb, bt, 2, n_kv * hd), ks, vs
+
+
+@pytest.mark.parametrize("kern", ["single", "pp"])
+def test_e4m3_prefill(dev, monkeypatch, kern):
+    """Causal chunked prefill over E4M3 pages, both kernels: NaN codes past
+    each chunk's last position and on unreferenced pages, then a chunk whose
+    table has invalid entries inside its causal window (page 0, their
+    stand-in, all NaN codes)."""
+    monkeypatch.setenv("EH_PREFILL_KERNEL", kern)
+    nh, nkv, hd, bt = 16, 4, 128, 16
+    rng = np.random.default_rng(89)
+    starts, lens = np.array([0, 37, 200]), np.array([45, 100, 9])
+    n_tok = starts + lens
+    tab, nb = tables(rng, n_tok, bt)
+    rows = [(int(tab[b, t // bt]), t % bt) for b, n in enumerate(n_tok) for t in range(int(n))]
+    codes, host, ks, vs = e4m3_pool(rng, nb, bt, nkv, hd, rows)
+    dks, dvs = torch.from_numpy(ks).to(dev), torch.from_numpy(vs).to(dev)
+    total = int(lens.sum())
+    q = rng.standard_normal((total, nh, hd)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    out = torch.full((total, nh, hd), float("nan"), device=dev)
+    fa = FlashAttention2(0)
+    fa.launch_batched_e4m3(None, torch.from_numpy(q).to(dev),
+                           torch.from_numpy(codes.reshape(-1)).to(dev), i32(tab, dev),
+                           i32(cu, dev), i32(starts, dev), out, nh, nkv, hd, bt,
+                           int(lens.max()), dks, dvs)
+    torch.cuda.synchronize()
+    g = out.cpu().numpy()
+    for b in range(len(lens)):
+        k = (int(n_tok[b]) + bt - 1) // bt
+        ref = orc.prefill_causal(host.reshape(-1), tab[b, :k], bt, q[cu[b]:cu[b + 1]],
+                                 int(lens[b]), int(starts[b]), nh, nkv, hd)
+        check(g[cu[b]:cu[b + 1]], ref, False, f"E4M3 {kern} seq {b}")
+
+    p0, nq = 40, 90
+    n = p0 + nq
+    n_pg = -(-n // bt)
+    nb = n_pg + 3
+    table = (1 + rng.permutation(nb - 1)[:n_pg]).astype(np.uint32)   # page 0 is never used
+    bad = [1, 5]
+    table[bad] = [NONE, nb + 9]
+    rows = [(int(table[t // bt]), t % bt) for t in range(n) if t // bt not in bad]
+    codes, host, ks, vs = e4m3_pool(rng, nb, bt, nkv, hd, rows)
+    q = rng.standard_normal((nq, nh, hd)).astype(np.float32)
+    out = torch.full((nq, nh, hd), float("nan"), device=dev)
+    fa.launch_batched_e4m3(None, torch.from_numpy(q).to(dev),
+                           torch.from_numpy(codes.reshape(-1)).to(dev), i32(table[None, :], dev),
+                           i32(np.array([0, nq]), dev), i32(np.array([p0]), dev), out, nh, nkv,
+                           hd, bt, nq, dks, dvs)
+    torch.cuda.synchronize()
+    ref = np.stack([np_attend(host, table, [t for t in range(p0 + i + 1) if t // bt not in bad],
+                              q[i], nh, nkv, hd) for i in range(nq)])
+    check(out.cpu().numpy(), ref, False, f"E4M3 {kern} invalid pages")
 
 
 @pytest.mark.parametrize("dtype", [KvDataType.F16, KvDataType.BF16, KvDataType.FP8],
