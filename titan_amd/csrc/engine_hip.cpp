@@ -442,7 +442,7 @@ eh_status run_tiles(eh_context* c, eh_stream stream, const tiles_args& a, const 
     const uint32_t rec_row = (uint32_t)mass_rec_row(a.bt_stride, a.block_tokens);
     float* tile_rec = a.block_mass ? (float*)a.mass_ws : nullptr;
     float* fin = a.block_mass ? tile_rec + 2ull * a.batch * rec_row * a.n_head : nullptr;
-    eh_status st = launch_lds(c, mod, name, dim3((a.grid + runs_per_wg - 1) / runs_per_wg),
+    eh_status st = launch_lds(c, mod, name, dim3((uint32_t)div_ceil(a.grid, runs_per_wg)),
                               dim3(waves * 64), lds, stream, a.q,
                               (uint8_t*)a.pool, a.n_blocks, a.bt, a.bt_stride, a.lens, a.lens_add,
                               (const uint8_t*)a.new_k, (const uint8_t*)a.new_v, a.batch, a.out,
