@@ -56,9 +56,9 @@ def parse():
                    help="suite append part: tokens appended per sequence per call (config 2: 1)")
     p.add_argument("--c5-pool-frac", type=float, default=0.9,
                    help="config 5 pool size as a fraction of free HBM")
-    p.add_argument("--parts", default="c1,append,e4m3,bf16,ceiling,c3,c4,c5",
-                   help="suite parts to run (comma list of c1, append, e4m3, bf16, ceiling, c3, "
-                        "c4, c5)")
+    p.add_argument("--parts", default="c1,append,e4m3,bf16,ceiling,c2u,c3,c4,c5",
+                   help="suite parts to run (comma list of c1, append, e4m3, bf16, ceiling, "
+                        "c2u, c3, c4, c5)")
     return p.parse_args()
 
 
@@ -379,7 +379,8 @@ def suite(args, dev):
     graph replays (launch cost inside the graph, host enqueue outside).
     --parts selects: c1 (config 1), append (config 2 append / gather), e4m3
     (config 2 decode over E4M3 pages), bf16 (config 2 decode over bf16 pages
-    beside f16), c3 (config 3 prefill), c4 (config 4 compaction), c5 (config 5
+    beside f16), ceiling (config 2's read ceilings), c2u (config 2's shape at a
+    uniform 4 k context), c3 (config 3 prefill), c4 (config 4 compaction), c5 (config 5
     long-context decode on a ~90 % HBM pool)."""
     import numpy as np
     import torch
@@ -391,6 +392,34 @@ def suite(args, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
     parts = set(args.parts.split(","))
+
+    def pools_graph_us(call, pools, reps=20):
+        """µs per call: one call per pool (the headline step's rotation) in one
+        graph, median of `reps` replays after 50 ms of warm replays."""
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        call(None, pools[0])
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(st):
+            with torch.cuda.graph(g, stream=st):
+                for p in pools:
+                    call(st, p)
+        torch.cuda.synchronize()
+        t_end = time.perf_counter() + 0.05
+        while time.perf_counter() < t_end:
+            with torch.cuda.stream(st):
+                g.replay()
+            torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        with torch.cuda.stream(st):
+            ev[0].record(st)
+            for k in range(reps):
+                g.replay()
+                ev[k + 1].record(st)
+        torch.cuda.synchronize()
+        return (float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)])) * 1e3 /
+                len(pools))
 
     if "c1" in parts:  # f32, B=1, 14/2 heads, hd 64, page 16, 511 cached + 1 appended
         s1 = synth.config1(0)
@@ -537,32 +566,8 @@ def suite(args, dev):
         xo = torch.empty(1024 * 8, dtype=torch.int32, device=dev)
         dec_bytes = int(n_tok.sum()) * 2 * 128 * 2 * 2 + 2 * 32 * 2 * s2.row_len * 2
 
-        def graph_us(call, reps=20):
-            """µs per call: 28 calls (one per pool) in one graph, median of
-            `reps` replays after 50 ms of warm replays."""
-            st = torch.cuda.Stream()
-            st.wait_stream(torch.cuda.current_stream())
-            call(None, pools[0])
-            torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.stream(st):
-                with torch.cuda.graph(g, stream=st):
-                    for i in range(L):
-                        call(st, pools[i])
-            torch.cuda.synchronize()
-            t_end = time.perf_counter() + 0.05
-            while time.perf_counter() < t_end:
-                with torch.cuda.stream(st):
-                    g.replay()
-                torch.cuda.synchronize()
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
-            with torch.cuda.stream(st):
-                ev[0].record(st)
-                for k in range(reps):
-                    g.replay()
-                    ev[k + 1].record(st)
-            torch.cuda.synchronize()
-            return float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)])) * 1e3 / L
+        def graph_us(call):
+            return pools_graph_us(call, pools)
 
         pa.build_schedule(None, lay2, dtab2, pos2, 1, plan2, sched2)
         us_dec = graph_us(lambda st, p: pa.append_decode_scheduled(
@@ -601,6 +606,76 @@ def suite(args, dev):
               "decode_frac_of_heads_ceiling": round((dec_bytes / us_dec) /
                                                     (st_bytes / heads[hk]), 4)})
         del pools
+
+    if "c2u" in parts:
+        # Config 2's shape with every sequence at a full 4 k context (the
+        # north star's "batch-32 ... at 4k context"): 4095 cached tokens + the
+        # appended one, 256 pages each drawn in shuffled order from a pool of
+        # 1.2x the pages, 28 rotated pools as the headline step.  The fused
+        # step from a step schedule, then the read ceilings of the same pages
+        # timed the same way, then a check of the last call against a float64
+        # numpy attention over a host copy of its pages.
+        L = 28
+        n_pg = 32 * 256
+        nbu = n_pg * 6 // 5
+        tabu = np.random.default_rng(4096).permutation(nbu)[:n_pg].astype(np.uint32)
+        tabu = tabu.reshape(32, 256)
+        layu = PagedKvLayout(nbu, 16, 256, KvDataType.F16)
+        poolsu = [torch.randn(layu.floats_total(), generator=gen, device=dev, dtype=torch.float16)
+                  for _ in range(L)]
+        dtabu = torch.from_numpy(tabu.view(np.int32)).to(dev)
+        posu = torch.full((32,), 4095, dtype=torch.int32, device=dev)
+        planu = PagedAttention.plan(32, 12, 2, 128, 16, 4096)
+        wsu = PagedAttention.workspace(planu)
+        schedu = PagedAttention.schedule_buffer(32, 256, 16, planu)
+        qu = torch.randn((32, 12, 128), generator=gen, device=dev)
+        ou = torch.full((32, 12, 128), float("nan"), device=dev)
+        nku = torch.randn((32, 256), generator=gen, device=dev, dtype=torch.float16)
+        nvu = torch.randn((32, 256), generator=gen, device=dev, dtype=torch.float16)
+        pa.build_schedule(None, layu, dtabu, posu, 1, planu, schedu)
+        us_u = pools_graph_us(lambda st, p: pa.append_decode_scheduled(
+            st, layu, p, nku, nvu, schedu, 256, qu, ou, 12, 128, planu, wsu), poolsu)
+        torch.cuda.synchronize()
+        host = poolsu[-1].view(nbu, 16, 2, 2, 128)[dtabu.long()].cpu().numpy()
+        host = host.reshape(32, 4096, 2, 2, 128)
+        app_ok = bool(np.array_equal(host[:, 4095, 0].reshape(32, 256).view(np.uint16),
+                                     nku.cpu().numpy().view(np.uint16)) and
+                      np.array_equal(host[:, 4095, 1].reshape(32, 256).view(np.uint16),
+                                     nvu.cpu().numpy().view(np.uint16)))
+        ref = np_decode_f64(host, qu.cpu().numpy())
+        del host
+        d = np.abs(ou.cpu().numpy().astype(np.float64) - ref)
+        ok = bool(np.isfinite(d).all() and d.max() <= 2e-3 and
+                  (d <= 2e-3 + 1e-3 * np.abs(ref)).all())
+        ids = torch.from_numpy(tabu.reshape(-1).view(np.int32)).to(dev)
+        xo = torch.empty(1024 * 8, dtype=torch.int32, device=dev)
+        whole = {f"d{dp}_g{g}": round(pools_graph_us(
+            lambda st, p: kv.stream_pages(st, layu, p, ids, xo, dp, g), poolsu), 2)
+            for dp in (1, 2) for g in (256, 512, 1024)}
+        heads = {g: round(pools_graph_us(
+            lambda st, p: kv.stream_pages_heads(st, layu, p, ids, xo, 128, g), poolsu), 2)
+            for g in (256, 512, 1024)}
+        c_us, h_us = min(whole.values()), min(heads.values())
+        st_b = n_pg * layu.page_bytes()
+        dec_b = 32 * 4096 * 2 * 128 * 2 * 2 + 2 * 32 * 2 * 256 * 2
+        emit({"config": "2u", "what": "config 2's shape at a uniform 4 k context: B=32, 12/2 "
+              "heads, hd 128, page 16, f16, 4095 cached + 1 appended per sequence, fused append "
+              "+ decode from a step schedule, 28 rotated pools; read ceilings of the same 8192 "
+              "pages (whole pages, eh_stream_pages, 1 or 2 pages in flight; per-kv-head pattern, "
+              "eh_stream_pages_heads) timed the same way",
+              "latency_us": round(us_u, 2), "kv_bytes": dec_b,
+              "GB/s": round(dec_b / us_u / 1e3, 1),
+              "frac_of_8TB/s": round(dec_b / us_u / 1e3 / 8000.0, 4),
+              "step_ms_28_layers": round(28 * us_u / 1e3, 4),
+              "ceiling_us": whole, "heads_ceiling_us": heads,
+              "frac_of_ceiling": round((dec_b / us_u) / (st_b / c_us), 4),
+              "frac_of_heads_ceiling": round((dec_b / us_u) / (st_b / h_us), 4),
+              "check_vs_numpy_f64": {"max_abs": float(d.max()), "within_bar": ok,
+                                     "appended_rows_bit_exact": app_ok},
+              "kernel": PagedAttention.kernel_name(12, 2, 128, 16, KvDataType.F16) +
+              "_sched + eh_decode_tiles_merge_sched"})
+        del poolsu
+        torch.cuda.empty_cache()
 
     if "bf16" in parts:  # config 2's decode over bf16 pages beside f16, 16 rotated pools each
         lens16 = torch.from_numpy((s2.ctx_lens + 1).astype(np.int32)).to(dev)
