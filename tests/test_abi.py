@@ -145,6 +145,33 @@ run("sched_rl0", L.eh_decode_schedule(ctx, None, C.byref(lay(4, 16, 0)), buf, 64
 run("prefill_page_wrap", L.eh_flash_attention_prefill(ctx, None, 0, buf, 2**40, buf, 1 << 20, buf,
                                                       4, buf, 2**40, 2**30, 2**30, 128, 2**30, 1,
                                                       0, None))
+# measurement aids: layout, page size, depth, grid and buffer checks
+f16 = lay(4, 16, 256)  # 16 KiB pages, pool 64 KiB
+run("stream_bt0", L.eh_stream_pages(ctx, None, C.byref(lay(4, 0, 256)), buf, 1 << 20, buf, 64, 1,
+                                    1, 1, buf, 64))
+run("stream_page", L.eh_stream_pages(ctx, None, C.byref(lay(4, 8, 256)), buf, 1 << 20, buf, 64, 1,
+                                     1, 1, buf, 64))
+run("stream_pool", L.eh_stream_pages(ctx, None, C.byref(f16), buf, 1000, buf, 64, 1, 1, 1, buf, 64))
+run("stream_depth", L.eh_stream_pages(ctx, None, C.byref(f16), buf, 1 << 16, buf, 64, 1, 3, 1, buf,
+                                      64))
+run("stream_grid0", L.eh_stream_pages(ctx, None, C.byref(f16), buf, 1 << 16, buf, 64, 1, 1, 0, buf,
+                                      64))
+run("stream_ids", L.eh_stream_pages(ctx, None, C.byref(f16), buf, 1 << 16, buf, 8, 10, 1, 1, buf,
+                                    64))
+run("stream_out", L.eh_stream_pages(ctx, None, C.byref(f16), buf, 1 << 16, buf, 64, 1, 1, 4, buf,
+                                    64))
+run("heads_bt32", L.eh_stream_pages_heads(ctx, None, C.byref(lay(4, 32, 256)), buf, 1 << 20, buf,
+                                          64, 1, 128, 1, buf, 64))
+run("heads_hd96", L.eh_stream_pages_heads(ctx, None, C.byref(f16), buf, 1 << 16, buf, 64, 1, 96, 1,
+                                          buf, 64))
+run("heads_hd64", L.eh_stream_pages_heads(ctx, None, C.byref(f16), buf, 1 << 16, buf, 64, 1, 64, 1,
+                                          buf, 64))
+run("heads_nkv3", L.eh_stream_pages_heads(ctx, None, C.byref(lay(4, 16, 384)), buf, 1 << 20, buf,
+                                          64, 1, 128, 1, buf, 64))
+run("heads_grid0", L.eh_stream_pages_heads(ctx, None, C.byref(f16), buf, 1 << 16, buf, 64, 1, 128,
+                                           0, buf, 64))
+run("heads_out", L.eh_stream_pages_heads(ctx, None, C.byref(f16), buf, 1 << 16, buf, 64, 1, 128, 4,
+                                         buf, 64))
 print(json.dumps(out))
 """
 
@@ -154,8 +181,11 @@ def test_layout_and_size_checks_before_any_hip_call():
     prefill whose page size passes 64 bits, are rejected with InvalidSize
     before the context is used: block_tokens 0 or above 2^31 - 1, row_len 0,
     rows of 2^31 bytes or more, and a pool or page size beyond 64 bits (the
-    expected size saturates at UINT64_MAX). The calls run in a child process,
-    so a regression shows as a failed test, not a crashed run."""
+    expected size saturates at UINT64_MAX). The read-ceiling measurement aids
+    reject page sizes, depths, head shapes, grids and short buffers outside
+    their contract with the status and (expected, actual) pair of each rule.
+    The calls run in a child process, so a regression shows as a failed test,
+    not a crashed run."""
     import json
     import subprocess
     import sys
@@ -163,13 +193,18 @@ def test_layout_and_size_checks_before_any_hip_call():
                        timeout=120)
     assert r.returncode == 0, r.stderr[-2000:]
     got = json.loads(r.stdout.strip().splitlines()[-1])
-    bad = 1  # EH_INVALID_SIZE
+    bad, uns = 1, 30  # EH_INVALID_SIZE, EH_UNSUPPORTED
     imax, u64 = 2**31 - 1, 2**64 - 1
     want = {
         "append_bt0": (bad, 1, 0), "append_bt_big": (bad, imax, 2**31), "append_rl0": (bad, 1, 0),
         "append_row_big": (bad, imax, 2**32), "append_pool_wrap": (bad, u64, 1 << 20),
         "gather_bt0": (bad, 1, 0), "copy_bt0": (bad, 1, 0), "sched_rl0": (bad, 1, 0),
         "prefill_page_wrap": (bad, u64, 1 << 20),
+        "stream_bt0": (bad, 1, 0), "stream_page": (uns, 16384, 8192),
+        "stream_pool": (bad, 1 << 16, 1000), "stream_depth": (uns, 2, 3),
+        "stream_grid0": (bad, 1, 0), "stream_ids": (bad, 40, 8), "stream_out": (bad, 128, 64),
+        "heads_bt32": (uns, 16, 32), "heads_hd96": (bad, 96, 256), "heads_hd64": (uns, 256, 128),
+        "heads_nkv3": (uns, 8, 3), "heads_grid0": (bad, 1, 0), "heads_out": (bad, 128, 64),
     }
     assert {k: tuple(v) for k, v in got.items()} == want
 
