@@ -12,7 +12,8 @@ such a V row (0 * NaN = NaN) would fail.  The paths covered:
   * the fixed-split and slot-major kernels of one sequence, with host and
     device positions, the fused append onto a new page, and invalid table
     entries inside the attended range (their stand-in, page 0, is NaN);
-  * decode over the protected-sinks range, with every unattended row NaN;
+  * decode over the protected-sinks range, with every unattended row NaN,
+    on fixed and seeded random shapes;
   * chunked prefill, both kernels, over f32, f16, bf16 and E4M3 pages, also
     with invalid table entries inside a chunk's causal window (page 0 NaN).
 Outputs are compared with the oracle, which reads only the attended tokens,
@@ -485,6 +486,70 @@ def test_window_decode_unattended_rows(dev, dtype, sink, window):
     ref, ref_mass = orc.sdpa_decode_window_batched(host, tab, lens.astype(np.uint32), bt, q, n_head,
                                                    n_kv, hd, sink, window, n_blocks=nb)
     check(out.cpu().numpy(), ref, False, f"{dtype.name} window {sink}/{window}")
+    got = mass.cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    bad = np.abs(got - ref_mass) > 2e-4 * n_head + 1e-3 * ref_mass
+    assert not bad.any(), (np.argwhere(bad)[:4], got[bad][:4], ref_mass[bad][:4])
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_window_random_sweep(dev, seed):
+    """Decode over the protected-sinks range on seeded random shapes: f16,
+    bf16 or E4M3 pages; 1/2/4/8 kv heads with 1-8 q heads each; pages of 16,
+    32 or 64 tokens; 1-16 sequences of 0-2500 tokens; sinks and windows on and
+    off tile edges; a planner or forced grid.  Every unattended row holds NaN.
+    Output and per-page H2O mass against the oracle."""
+    rng = np.random.default_rng(500_000 + seed)
+    dtype = (KvDataType.F16, KvDataType.BF16, KvDataType.FP8)[int(rng.integers(3))]
+    n_kv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 3, 4, 6, 8]))
+    n_head, hd, bt = g * n_kv, 128, int(rng.choice([16, 32, 64]))
+    rl = n_kv * hd
+    B = int(rng.integers(1, 17))
+    lens = np.where(rng.integers(0, 2, B) == 0, rng.integers(0, 70, B),
+                    rng.integers(70, 2500, B)).astype(np.int64)
+    sink = int(rng.choice([0, 1, 4, 15, 16, 17, 40]))
+    window = int(rng.choice([1, 3, 15, 16, 31, 64, 100, 700]))
+    tab, nb = tables(rng, lens, bt)
+
+    def attended(n):
+        if n == 0:
+            return []
+        lo = max(sink, n - 1 - window)
+        return [t for t in range(n) if t < sink or t >= lo]
+
+    ks = vs = None
+    if dtype == KvDataType.FP8:
+        rows = [(int(tab[b, t // bt]), t % bt) for b, n in enumerate(lens) for t in attended(int(n))]
+        codes, host, ksn, vsn = e4m3_pool(rng, nb, bt, n_kv, hd, rows)
+        host = host.reshape(-1)
+        pool = torch.from_numpy(codes.reshape(-1)).to(dev)
+        ks, vs = torch.from_numpy(ksn).to(dev), torch.from_numpy(vsn).to(dev)
+    else:
+        h = np.full((nb, bt, 2, rl), np.nan, np.float32)
+        for b, n in enumerate(lens):
+            for t in attended(int(n)):
+                h[tab[b, t // bt], t % bt] = rng.standard_normal((2, rl)).astype(np.float32)
+        t16 = torch.from_numpy(h.reshape(-1)).to(TDT[dtype])
+        host, pool = t16.to(torch.float32).numpy(), t16.to(dev)
+    q = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, max(int(lens.max()), 1), 0, dtype)
+    assert plan[0] == 0
+    if rng.integers(2):
+        plan = PagedAttention.with_grid(plan, int(rng.choice([1, 2, 7, 64, 333])), B, n_head)
+    extra = PagedAttention.mass_workspace_bytes(B, tab.shape[1], bt, n_head)
+    ws = torch.zeros((plan[2] + extra + 3) // 4, device=dev)
+    mass = torch.zeros((nb,), device=dev)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    print(f"[window sweep {seed}] {dtype.name} heads {n_head}/{n_kv} page {bt} B {B} sink {sink} "
+          f"window {window} max len {int(lens.max())}", flush=True)
+    PagedAttention(0).decode_batched_window(None, torch.from_numpy(q).to(dev), pool, i32(tab, dev),
+                                            i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, sink,
+                                            window, plan, ws, ks, vs, block_mass=mass)
+    torch.cuda.synchronize()
+    ref, ref_mass = orc.sdpa_decode_window_batched(host, tab, lens.astype(np.uint32), bt, q, n_head,
+                                                   n_kv, hd, sink, window, n_blocks=nb)
+    check(out.cpu().numpy(), ref, False, f"window sweep {seed}")
     got = mass.cpu().numpy().astype(np.float64)
     assert np.isfinite(got).all()
     bad = np.abs(got - ref_mass) > 2e-4 * n_head + 1e-3 * ref_mass
