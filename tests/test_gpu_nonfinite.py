@@ -12,6 +12,8 @@ such a V row (0 * NaN = NaN) would fail.  The paths covered:
   * the fixed-split and slot-major kernels of one sequence, with host and
     device positions, the fused append onto a new page, and invalid table
     entries inside the attended range (their stand-in, page 0, is NaN);
+  * the single-pass decode of one sequence and the batched fixed-split
+    decode;
   * decode over the protected-sinks range, with every unattended row NaN,
     on fixed and seeded random shapes;
   * chunked prefill, both kernels, over f32, f16, bf16 and E4M3 pages, also
@@ -554,3 +556,51 @@ def test_window_random_sweep(dev, seed):
     assert np.isfinite(got).all()
     bad = np.abs(got - ref_mass) > 2e-4 * n_head + 1e-3 * ref_mass
     assert not bad.any(), (np.argwhere(bad)[:4], got[bad][:4], ref_mass[bad][:4])
+
+
+@pytest.mark.parametrize("dtype,hd", [(KvDataType.F32, 64), (KvDataType.F16, 64),
+                                      (KvDataType.BF16, 32), (KvDataType.F16, 128)],
+                         ids=lambda v: getattr(v, "name", str(v)))
+def test_single_pass_and_fixed_split_batched(dev, dtype, hd):
+    """The single-pass decode of one sequence (`eh_paged_attention`, host and
+    device positions) and the batched fixed-split decode (head sizes outside
+    the balanced kernel, or a caller's tokens_per_split) over NaN-tailed
+    pages, against the oracle."""
+    n_head, n_kv, bt = 8, 2, 16
+    rl = n_kv * hd
+    rng = np.random.default_rng(97 + hd + int(dtype))
+    f32 = dtype == KvDataType.F32
+    pa = PagedAttention(0)
+    n = 300
+    tab, nb = tables(rng, [n + 40], bt)
+    pool0, host = nan_pool(rng, nb, bt, rl, tab, [n], dtype)
+    pool = pool0.to(dev)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    ref = orc.sdpa_decode(host.reshape(-1), tab[0], bt, n, q, n_head, n_kv, hd, True, n - 1)
+    out = torch.full((n_head * hd,), float("nan"), device=dev)
+    pa.launch(None, torch.from_numpy(q).to(dev), pool, i32(tab[0], dev), out, n_head, n_kv, hd, bt,
+              n, n - 1, True, kv_dtype=dtype)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), ref, f32, f"{dtype.name} hd{hd} single pass")
+    out.fill_(float("nan"))
+    pa.launch_with_pos_ptr(None, torch.from_numpy(q).to(dev), pool, i32(tab[0], dev), out, n_head,
+                           n_kv, hd, bt, n + 39, n + 38, True,
+                           torch.tensor([n - 1], dtype=torch.int32, device=dev), kv_dtype=dtype)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), ref, f32, f"{dtype.name} hd{hd} single pass, device position")
+
+    lens = np.array([1, 15, 16, 17, 250, 0, 600, 47], np.int64)
+    B = len(lens)
+    tab, nb = tables(rng, lens, bt)
+    pool0, host = nan_pool(rng, nb, bt, rl, tab, lens, dtype)
+    qb = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(lens.max()), 64, dtype)
+    assert plan[0] != 0  # fixed splits (16-bit pages round the hint up to 256 tokens)
+    out = torch.full((B, n_head, hd), float("nan"), device=dev)
+    pa.decode_batched(None, torch.from_numpy(qb).to(dev), pool0.to(dev), i32(tab, dev),
+                      i32(lens, dev), out, n_head, n_kv, hd, bt, dtype, plan,
+                      PagedAttention.workspace(plan))
+    torch.cuda.synchronize()
+    ref = orc.sdpa_decode_batched(host.reshape(-1), tab, lens.astype(np.uint32), bt, qb, n_head,
+                                  n_kv, hd)
+    check(out.cpu().numpy(), ref, f32, f"{dtype.name} hd{hd} fixed-split batched")
