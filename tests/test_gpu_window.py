@@ -6,7 +6,8 @@ Tolerance: max-abs <= 2e-3 and
 |gpu - ref| <= 2e-3 + 1e-3*|ref| (tests/parity.py) (16-bit and E4M3 pages).  The
 cases cover sinks that end mid-tile, windows shorter than one tile, windows
 that start mid-tile, gaps of many tiles, sinks covering the whole sequence,
-runs that cross sequences whose walked tiles skip a gap, and window 0 (which
+runs that cross sequences whose walked tiles skip a gap, graph replay as the
+device lengths grow, and window 0 (which
 must equal the plain decode bit for bit).
 """
 import numpy as np
@@ -238,3 +239,59 @@ def test_window_mass_buffer_checks(dev):
     pa.decode_batched_window(*args, PagedAttention.workspace(plan))
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
+
+
+def test_window_graph_replay_growing_lengths(dev):
+    """The windowed decode with H2O mass captured once in a graph and replayed
+    as the device lengths grow across tile, page and window edges (the
+    walked tiles and cut tiles follow the lengths each replay): output and
+    per-page mass equal the oracle at every replay, with eager work and
+    synchronisations between the replays."""
+    n_head, n_kv, hd, bt = 12, 2, 128, 16
+    sink, window = 4, 40
+    rng = np.random.default_rng(23)
+    start = np.array([1, 14, 44, 300, 47, 0], np.int64)
+    steps = 6
+    B = len(start)
+    tab, nb = make_tables(rng, start + 3 * steps, bt)
+    host = torch.from_numpy(rng.standard_normal(nb * bt * 2 * n_kv * hd).astype(np.float32)).half()
+    pool, pool_f32 = host.to(dev), host.float().numpy()
+    plan = PagedAttention.plan(B, n_head, n_kv, hd, bt, int(start.max()) + 3 * steps)
+    extra = PagedAttention.mass_workspace_bytes(B, tab.shape[1], bt, n_head)
+    ws = torch.zeros((plan[2] + extra + 3) // 4, device=dev)
+    mass = torch.zeros((nb,), device=dev)
+    lens = i32(start, dev)
+    q = torch.empty((B, n_head, hd), device=dev)
+    out = torch.empty((B, n_head, hd), device=dev)
+    dtab = i32(tab, dev)
+    pa = PagedAttention(0)
+
+    def call(st):
+        pa.decode_batched_window(st, q, pool, dtab, lens, out, n_head, n_kv, hd, bt,
+                                 KvDataType.F16, sink, window, plan, ws, block_mass=mass)
+    call(None)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call(s)
+    torch.cuda.synchronize()
+    for step in range(steps):
+        cur = start + 3 * step
+        qn = rng.standard_normal((B, n_head, hd)).astype(np.float32)
+        q.copy_(torch.from_numpy(qn))
+        lens.copy_(i32(cur, dev))
+        mass.zero_()
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref, ref_mass = orc.sdpa_decode_window_batched(pool_f32, tab, cur.astype(np.uint32), bt, qn,
+                                                       n_head, n_kv, hd, sink, window,
+                                                       n_blocks=nb)
+        check_close(out.cpu().numpy(), ref, what=f"window graph replay {step}")
+        got = mass.cpu().numpy().astype(np.float64)
+        bad = np.abs(got - ref_mass) > 2e-4 * n_head + 1e-3 * ref_mass
+        assert not bad.any(), (step, np.argwhere(bad)[:4])
